@@ -1,0 +1,102 @@
+/*
+ * ttc_lqr.h -- C ABI of the MI355X (gfx950) batched receding-horizon LQR solver
+ * behind TTC-Net's TTCLayer (solver_impl="hip").
+ *
+ * The reference has no native boundary: its hot path is the Python/Triton pair
+ *   fused_lqr_layer_fwd   (ttc/solvers/fused_lqr.py:18-146)
+ *   fused_lqr_layer_bwd   (ttc/solvers/fused_lqr.py:148-253)
+ * called from FusedLQRSolveFunc (fused_lqr.py:255-291).  The entry points below
+ * replace exactly those two functions; the Python autograd Function in
+ * ttc-net_amd/ttc/solvers/hip_lqr.py binds them with ctypes.
+ *
+ * Conventions
+ *   - All tensors are fp32, contiguous, row-major, device pointers.  Shapes use
+ *     N tokens, H heads, state dim d, control dim du, horizon T, P = N*H:
+ *       A_diag [N,H,d]  B [N,d,du]  Q [N,d,d]  R_inv [N,H,du]  Q_f [N,H,d,d]
+ *       log_gamma_A [N,H]  log_gamma_B [N,H,du]  log_gamma_Q [N,H,d]  h0 [N,H,d]
+ *     (the reference's shapes, fused_lqr.py:37-45).
+ *   - The kernels implement d == du in {16, 32, 64}; other sizes are padded by
+ *     the caller (zero state rows / unit-cost dummy controls leave the solution
+ *     unchanged).  Anything else returns TTC_LQR_EUNSUPPORTED.
+ *   - Nothing here allocates device memory, throws, or synchronises the device.
+ *     All work is enqueued on `stream` (a hipStream_t, NULL = default stream).
+ *   - `status` (device int32, caller-zeroed, may be NULL) receives bit flags:
+ *     TTC_LQR_STATUS_NONFINITE if any output is NaN/Inf, TTC_LQR_STATUS_LARGE if
+ *     a gradient has |g| >= grad_limit.  The caller reads it after the stream
+ *     completes and raises (the reference raises RuntimeError, fused_lqr.py:101,246).
+ *   - Q and Q_f enter through their symmetric parts; the Q / Q_f gradients are
+ *     the symmetric gradients (as the reference's fused/kkt solvers return).
+ *   - Thread-safe and re-entrant; calls that share a workspace or stash must be
+ *     ordered by the caller.
+ */
+#ifndef TTC_LQR_H
+#define TTC_LQR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTC_LQR_OK 0
+#define TTC_LQR_EINVAL 1        /* bad sizes / null pointer / workspace too small */
+#define TTC_LQR_EUNSUPPORTED 2  /* d, du combination not compiled */
+#define TTC_LQR_ELAUNCH 3       /* HIP launch error */
+
+#define TTC_LQR_STATUS_NONFINITE 1
+#define TTC_LQR_STATUS_LARGE 2
+
+/* Library version string. */
+const char* ttc_lqr_version(void);
+
+/* Human-readable text for a TTC_LQR_* return code. */
+const char* ttc_lqr_strerror(int code);
+
+/* 1 if the kernels were compiled for this (d, du), else 0. */
+int ttc_lqr_supported(int32_t d, int32_t du);
+
+/* Bytes of the optional gain stash written by ttc_lqr_forward for the backward:
+ * per problem T*d*du gain floats plus du*du floats of the step-0 control Hessian. */
+size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T);
+
+/* Workspace bytes ttc_lqr_backward needs to process `chunk_tokens` tokens per pass
+ * (it loops over the tokens in chunks of that size).  `with_stash` != 0 when the
+ * forward stash is passed to the backward (then the gains are not recomputed). */
+size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
+                               int32_t with_stash);
+
+/* Forward: u = first optimal action [N,H,du] of every problem.
+ * Replaces fused_lqr_layer_fwd (ttc/solvers/fused_lqr.py:18-146).
+ * gain_stash / quu0_stash: NULL, or ttc_lqr_stash_bytes() of device memory split as
+ *   gain_stash [P,T,du,d] (feedback gains K_t, row-major) and quu0_stash [P,du,du].
+ * Pass them to ttc_lqr_backward to skip the gain recomputation. */
+int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const float* R_inv,
+                    const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
+                    const float* log_gamma_Q, const float* h0, int64_t n_tokens, int32_t heads,
+                    int32_t d, int32_t du, int32_t T, float* u, float* gain_stash, float* quu0_stash,
+                    int32_t* status, void* stream);
+
+/* Backward: gradients of sum(d_u * u) w.r.t. the nine inputs.
+ * Replaces fused_lqr_layer_bwd (ttc/solvers/fused_lqr.py:148-253).
+ * grad_B / grad_Q are summed over heads (B and Q are head-shared).
+ * gain_stash / quu0_stash: from ttc_lqr_forward, or both NULL (gains recomputed
+ * chunk by chunk inside `workspace`).  workspace_bytes must be at least
+ * ttc_lqr_workspace_bytes(c, ...) for some c >= 1 token; larger workspaces give
+ * fewer, larger passes.  grad_limit: |g| >= grad_limit sets TTC_LQR_STATUS_LARGE
+ * (the reference uses 1e6, fused_lqr.py:245); pass INFINITY to disable. */
+int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const float* R_inv,
+                     const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
+                     const float* log_gamma_Q, const float* h0, const float* d_u,
+                     int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
+                     const float* gain_stash, const float* quu0_stash,
+                     float* grad_A_diag, float* grad_B, float* grad_Q, float* grad_R_inv,
+                     float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,
+                     float* grad_log_gamma_Q, float* grad_h0, void* workspace,
+                     size_t workspace_bytes, float grad_limit, int32_t* status, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTC_LQR_H */

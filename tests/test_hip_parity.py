@@ -1,0 +1,172 @@
+"""GPU parity: the HIP solver (through the C ABI, via the autograd Function) against
+the fp64 oracle, on seeded inputs from every BASELINE configuration.
+
+Tolerance (north_star): per tensor, max|x - x64| / max|x64| <= 1e-4 for ``u`` and
+all nine gradients.  ``Q`` / ``Q_f`` gradients are the symmetric gradients on
+both sides.  Gradients of the stress configuration can exceed the reference's
+1e6 guard, so those cases pass ``grad_limit=inf``.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.inputs import CONFIGS, bench_solver_inputs, layer_solver_inputs, make_x
+from oracle.lqr64 import LQRProblem, solve_grads, solve_u0
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ["A_diag", "B", "Q", "R_inv", "Q_f", "lgA", "lgB", "lgQ", "h0"]
+TOL = 1e-4
+
+
+def _solver():
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+    return hip_lqr_solve
+
+
+def _relerr(x, ref):
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(x - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def run_hip(ins, T, dU, grad_limit=1e6, stash=None):
+    solve = _solver()
+    dev = torch.device("cuda:0")
+    xs = [t.detach().to(dev).float().requires_grad_(True) for t in ins]
+    u = solve(*xs, T, grad_limit=grad_limit, stash=stash)
+    (u * torch.as_tensor(dU, device=dev, dtype=u.dtype)).sum().backward()
+    out = {"u": u.detach().cpu().double().numpy()}
+    for n, t in zip(NAMES, xs):
+        out[n] = t.grad.detach().cpu().double().numpy()
+    return out
+
+
+def check_case(label, ins, T, seed=0, grad_limit=1e6, stash=None, tol=TOL):
+    pb = LQRProblem(*ins, T)
+    g = torch.Generator().manual_seed(seed + 7)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=g).double().numpy()
+    ref = solve_grads(pb, dU)
+    print(f"[{label}] N={pb.N} H={pb.H} d={pb.d} du={pb.du} T={T} stash={stash}", flush=True)
+    out = run_hip(ins, T, dU, grad_limit=grad_limit, stash=stash)
+    errs = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
+    print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+    bad = {k: v for k, v in errs.items() if not (v <= tol)}
+    assert not bad, f"{label}: rel err above {tol}: {bad}"
+    return out
+
+
+def test_reference_correctness_shape():
+    """bench_lqr_solvers.py:173-207 shape: batch 4, heads 4, d 16, T 64."""
+    check_case("bench-check", bench_solver_inputs(4, 4, 16, seed=0), 64)
+
+
+@pytest.mark.parametrize("stash", ["always", "never"])
+def test_config1_layer_slice(stash):
+    c = CONFIGS[1]
+    x = make_x(1, n_tokens=24, seed=0)
+    check_case("cfg1", layer_solver_inputs(1, x), c["T"], stash=stash)
+
+
+def test_config2_layer_slice():
+    c = CONFIGS[2]
+    x = make_x(2, n_tokens=64, seed=1)
+    check_case("cfg2", layer_solver_inputs(2, x), c["T"])
+
+
+def test_config3_layer_slice():
+    c = CONFIGS[3]
+    x = make_x(3, n_tokens=2, seed=2)
+    check_case("cfg3", layer_solver_inputs(3, x), c["T"])
+
+
+def test_config4_layer_slice():
+    c = CONFIGS[4]
+    x = make_x(4, n_tokens=1, seed=3)
+    check_case("cfg4", layer_solver_inputs(4, x), c["T"])
+
+
+@pytest.mark.parametrize("cfg,T", [(5, 64), (5, 1024), ("5b", 1024)])
+def test_config5_stress(cfg, T):
+    x = make_x(cfg, n_tokens=4, seed=5)
+    check_case(f"cfg{cfg}", layer_solver_inputs(cfg, x), T, grad_limit=math.inf)
+
+
+def test_padding_odd_dims_and_ragged_problem_count():
+    """d=12, du=8 (padded to 16 inside), N*H = 21 problems (not a multiple of the block)."""
+    g = torch.Generator().manual_seed(11)
+    N, H, d, du, T = 7, 3, 12, 8, 9
+    ins = bench_solver_inputs(N, H, d, seed=4)
+    B = torch.randn(N, d, du, generator=g) * 0.5
+    R_inv = torch.nn.functional.softplus(torch.rand(N, H, du, generator=g))
+    lgB = -torch.nn.functional.softplus(torch.randn(N, H, du, generator=g)) - 0.3
+    ins = [ins[0], B, ins[2], R_inv, ins[4], ins[5], lgB, ins[7], ins[8]]
+    check_case("pad", ins, T)
+
+
+def test_T1_closed_form():
+    ins = bench_solver_inputs(3, 2, 16, seed=9)
+    check_case("T1", ins, 1)
+
+
+def test_stash_modes_bitwise_equal():
+    x = make_x(2, n_tokens=8, seed=4)
+    ins = layer_solver_inputs(2, x)
+    dU = np.ones((8, 8, 16))
+    a = run_hip(ins, 64, dU, stash="always")
+    b = run_hip(ins, 64, dU, stash="never")
+    for k in a:
+        assert np.array_equal(a[k], b[k]), k
+
+
+def test_nonsymmetric_Q_uses_symmetric_part():
+    ins = bench_solver_inputs(2, 2, 16, seed=3)
+    g = torch.Generator().manual_seed(5)
+    skew = torch.randn(2, 16, 16, generator=g) * 0.01
+    skew = skew - skew.transpose(-1, -2)
+    Qns = ins[2] + skew
+    solve = _solver()
+    dev = torch.device("cuda:0")
+    u_sym = solve(*[t.to(dev) for t in ins], 16)
+    ins2 = list(ins)
+    ins2[2] = Qns
+    u_ns = solve(*[t.to(dev) for t in ins2], 16)
+    torch.testing.assert_close(u_ns, u_sym, rtol=1e-5, atol=1e-6)
+
+
+def test_nan_input_raises():
+    ins = bench_solver_inputs(2, 2, 16, seed=1)
+    ins[8] = ins[8].clone()
+    ins[8][0, 0, 0] = float("nan")
+    solve = _solver()
+    with pytest.raises(RuntimeError, match="Numerical instability"):
+        solve(*[t.cuda() for t in ins], 8)
+
+
+def test_empty_batch():
+    ins = [t[:0] for t in bench_solver_inputs(2, 2, 16, seed=1)]
+    solve = _solver()
+    u = solve(*[t.cuda() for t in ins], 8)
+    assert u.shape == (0, 2, 16)
+
+
+def test_layer_end_to_end_matches_oracle_layer():
+    """TTCLayer(solver_impl='hip') == the oracle layer restatement with the fp64 solver."""
+    from ttc import TTCLayer
+    from oracle.layer_ref import front_end, back_end, LayerParams
+    torch.manual_seed(0)
+    layer = TTCLayer(32, 32, 16, 8, 16, 16, solver_impl="hip").cuda()
+    x = torch.randn(2, 5, 8, 32, device="cuda")
+    y = layer(x, T=16)
+    assert y.shape == (2, 5, 8, 32)
+    # oracle: same weights, fp64 solve on CPU
+    p = LayerParams(32, 32, 16, 8, 16, 16)
+    p.W_in = layer.in_proj.weight.detach().cpu()
+    p.W_out = layer.out_proj.weight.detach().cpu()
+    p.Bs, p.Qs = layer.Bs.detach().cpu(), layer.Qs.detach().cpu()
+    ins, lead = front_end(p, x.cpu())
+    u64 = solve_u0(LQRProblem(*ins, 16))
+    y_ref = back_end(p, torch.from_numpy(u64).float(), ins[8], lead)
+    torch.testing.assert_close(y.cpu(), y_ref, rtol=1e-4, atol=1e-5)

@@ -1,0 +1,60 @@
+"""ctypes binding of ``libttc_lqr.so`` (the C ABI declared in ``include/ttc_lqr.h``).
+
+The library is built in-tree by ``ttc-net_amd/csrc/build.py`` into
+``ttc-net_amd/lib/libttc_lqr.so``.  There is no fallback: if the library is
+missing, importing the HIP solver raises, so a GPU run can never silently
+take another code path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+__all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check"]
+
+LIB_NAME = "libttc_lqr.so"
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_DEFAULT = os.path.normpath(os.path.join(_HERE, "..", "..", "lib", LIB_NAME))
+
+
+class TTCLQRError(RuntimeError):
+    pass
+
+
+def lib_path() -> str:
+    return os.environ.get("TTC_LQR_LIB", _DEFAULT)
+
+
+def _load():
+    path = lib_path()
+    if not os.path.exists(path):
+        raise ImportError(
+            f"{LIB_NAME} not found at {path}; build it with `python ttc-net_amd/csrc/build.py` "
+            "(or __graft_entry__.build()).  The HIP solver has no non-native fallback.")
+    L = ctypes.CDLL(path)
+    f32p = ctypes.c_void_p
+    i64, i32, sz = ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t
+    L.ttc_lqr_version.restype = ctypes.c_char_p
+    L.ttc_lqr_version.argtypes = []
+    L.ttc_lqr_strerror.restype = ctypes.c_char_p
+    L.ttc_lqr_strerror.argtypes = [ctypes.c_int]
+    L.ttc_lqr_supported.restype = ctypes.c_int
+    L.ttc_lqr_supported.argtypes = [i32, i32]
+    L.ttc_lqr_stash_bytes.restype = sz
+    L.ttc_lqr_stash_bytes.argtypes = [i64, i32, i32, i32, i32]
+    L.ttc_lqr_workspace_bytes.restype = sz
+    L.ttc_lqr_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32]
+    L.ttc_lqr_forward.restype = ctypes.c_int
+    L.ttc_lqr_forward.argtypes = [f32p] * 9 + [i64, i32, i32, i32, i32] + [f32p, f32p, f32p, f32p, ctypes.c_void_p]
+    L.ttc_lqr_backward.restype = ctypes.c_int
+    L.ttc_lqr_backward.argtypes = ([f32p] * 10 + [i64, i32, i32, i32, i32] + [f32p, f32p] + [f32p] * 9
+                                   + [ctypes.c_void_p, sz, ctypes.c_float, f32p, ctypes.c_void_p])
+    return L
+
+
+lib = _load()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise TTCLQRError(f"{what} failed: {lib.ttc_lqr_strerror(rc).decode()} (code {rc})")

@@ -1,0 +1,184 @@
+"""HIP (gfx950) LQR solver: the autograd Function behind ``solver_impl="hip"``.
+
+Mirrors the reference ``FusedLQRSolveFunc`` / ``fused_lqr_solve``
+(``ttc/solvers/fused_lqr.py:255-304``): same positional inputs
+``(A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T)``,
+same shape assertions (``fused_lqr.py:37-45``), ``u`` returned in the input dtype,
+gradients for all nine tensors (``grad_B`` / ``grad_Q`` summed over heads, the
+symmetric gradient for ``Q`` / ``Q_f``), ``RuntimeError`` on numerical trouble
+(``fused_lqr.py:101,246``).  The arithmetic runs in the C ABI of
+``libttc_lqr.so`` (``include/ttc_lqr.h``); this module only validates, pads,
+allocates with torch's caching allocator and checks the device status word.
+
+Differences from the reference, by design:
+* ``d`` / ``du`` of any size up to 64: the kernels handle ``d == du`` in
+  {16, 32, 64}; other sizes are zero-padded here (padded states start at 0 and
+  are neither driven nor costed; padded controls act on nothing and cost
+  ``u^2/2``), which leaves the solution unchanged.
+* the backward recomputes the feedback gains in bounded-memory chunks unless the
+  forward kept them ("stash"), see ``TTC_LQR_STASH`` below.
+
+Environment knobs:
+``TTC_LQR_STASH`` = ``auto`` (default: keep the gains from the forward when they
+fit in ``TTC_LQR_STASH_MAX_BYTES``, default 8 GiB) | ``always`` | ``never``.
+``TTC_LQR_WORKSPACE_BYTES``: backward workspace per call (default 4 GiB).
+"""
+from __future__ import annotations
+
+import math
+import os
+
+import torch
+
+from ._lib import lib, check
+
+__all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "padded_dim", "SUPPORTED_DIMS"]
+
+SUPPORTED_DIMS = (16, 32, 64)
+_FWD_MSG = "Numerical instability detected during fused LQR forward recurrence."
+_BWD_MSG = "Numerical instability detected during fused LQR backward pass."
+
+
+def padded_dim(d: int, du: int) -> int:
+    m = max(d, du)
+    for s in SUPPORTED_DIMS:
+        if m <= s:
+            return s
+    raise AssertionError(f"state/control dims up to {SUPPORTED_DIMS[-1]} are supported, got d={d}, du={du}")
+
+
+def _env_bytes(name: str, default: int) -> int:
+    v = os.environ.get(name)
+    return int(float(v)) if v else default
+
+
+def _pad_inputs(ins, d, du, Dp):
+    """Zero-pad the nine solver inputs from (d, du) to (Dp, Dp)."""
+    A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0 = ins
+    if d == Dp and du == Dp:
+        return ins
+    pd, pu = Dp - d, Dp - du
+    F = torch.nn.functional
+    A_diag = F.pad(A_diag, (0, pd))
+    B = F.pad(B, (0, pu, 0, pd))
+    Q = F.pad(Q, (0, pd, 0, pd))
+    R_inv = F.pad(R_inv, (0, pu), value=1.0)
+    Q_f = F.pad(Q_f, (0, pd, 0, pd))
+    lgB = F.pad(lgB, (0, pu))
+    lgQ = F.pad(lgQ, (0, pd))
+    h0 = F.pad(h0, (0, pd))
+    return [t.contiguous() for t in (A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0)]
+
+
+def _stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class HipLQRSolveFunc(torch.autograd.Function):
+
+    @staticmethod
+    def forward(ctx, A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T: int,
+                grad_limit: float = 1e6, stash: str | None = None):
+        ins = [A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0]
+        assert all(x.is_cuda for x in ins), "hip LQR solver inputs must be on a GPU"
+        bs, nh, d = A_diag.shape
+        du = B.shape[-1]
+        T = int(T)
+        assert T > 0
+        assert A_diag.shape == (bs, nh, d)
+        assert Q.shape == (bs, d, d)
+        assert B.shape == (bs, d, du)
+        assert R_inv_diag.shape == (bs, nh, du)
+        assert Q_f.shape == (bs, nh, d, d)
+        assert log_gamma_A.shape == (bs, nh)
+        assert log_gamma_B.shape == (bs, nh, du)
+        assert log_gamma_Q.shape == (bs, nh, d)
+        assert h0.shape == (bs, nh, d)
+        dev = A_diag.device
+        out_dtype = Q.dtype
+        Dp = padded_dim(d, du)
+        f32 = [x.detach().to(torch.float32).contiguous() for x in ins]
+        f32 = _pad_inputs(f32, d, du, Dp)
+        P = bs * nh
+        u = torch.empty(bs, nh, Dp, device=dev, dtype=torch.float32)
+        status = torch.zeros(1, device=dev, dtype=torch.int32)
+
+        policy = stash or os.environ.get("TTC_LQR_STASH", "auto")
+        need_grad = any(ctx.needs_input_grad[:9])
+        stash_bytes = lib.ttc_lqr_stash_bytes(bs, nh, Dp, Dp, T)
+        keep = need_grad and bs > 0 and (
+            policy == "always" or (policy == "auto" and stash_bytes <= _env_bytes("TTC_LQR_STASH_MAX_BYTES", 8 << 30)))
+        if keep:
+            st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32)
+            kst, q0s = st[: P * T * Dp * Dp], st[P * T * Dp * Dp:]
+        else:
+            st = kst = q0s = None
+        with torch.cuda.device(dev):
+            rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, u.data_ptr(),
+                                     None if kst is None else kst.data_ptr(),
+                                     None if q0s is None else q0s.data_ptr(),
+                                     status.data_ptr(), _stream_handle(dev))
+        check(rc, "ttc_lqr_forward")
+        if int(status.item()) != 0:
+            raise RuntimeError(_FWD_MSG)
+        ctx.save_for_backward(*f32, *( [st] if st is not None else []))
+        ctx.meta = (bs, nh, d, du, Dp, T, float(grad_limit), st is not None, [x.dtype for x in ins])
+        return u[..., :du].to(out_dtype)
+
+    @staticmethod
+    def backward(ctx, d_u):
+        bs, nh, d, du, Dp, T, grad_limit, has_stash, dtypes = ctx.meta
+        saved = ctx.saved_tensors
+        f32 = list(saved[:9])
+        st = saved[9] if has_stash else None
+        dev = f32[0].device
+        P = bs * nh
+        dU = torch.zeros(bs, nh, Dp, device=dev, dtype=torch.float32)
+        dU[..., :du] = d_u.to(torch.float32)
+        g = {
+            "A": torch.empty(bs, nh, Dp, device=dev), "B": torch.empty(bs, Dp, Dp, device=dev),
+            "Q": torch.empty(bs, Dp, Dp, device=dev), "R": torch.empty(bs, nh, Dp, device=dev),
+            "Qf": torch.empty(bs, nh, Dp, Dp, device=dev), "lA": torch.empty(bs, nh, device=dev),
+            "lB": torch.empty(bs, nh, Dp, device=dev), "lQ": torch.empty(bs, nh, Dp, device=dev),
+            "h0": torch.empty(bs, nh, Dp, device=dev),
+        }
+        status = torch.zeros(1, device=dev, dtype=torch.int32)
+        if st is not None:
+            kst, q0s = st[: P * T * Dp * Dp], st[P * T * Dp * Dp:]
+        else:
+            kst = q0s = None
+        budget = _env_bytes("TTC_LQR_WORKSPACE_BYTES", 4 << 30)
+        per_tok = lib.ttc_lqr_workspace_bytes(1, nh, Dp, Dp, T, 1 if st is not None else 0)
+        chunk = max(1, min(bs, budget // max(per_tok, 1)))
+        ws_bytes = lib.ttc_lqr_workspace_bytes(chunk, nh, Dp, Dp, T, 1 if st is not None else 0)
+        ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+        limit = grad_limit if math.isfinite(grad_limit) else float("inf")
+        with torch.cuda.device(dev):
+            rc = lib.ttc_lqr_backward(
+                *[t.data_ptr() for t in f32], dU.data_ptr(), bs, nh, Dp, Dp, T,
+                None if kst is None else kst.data_ptr(), None if q0s is None else q0s.data_ptr(),
+                g["A"].data_ptr(), g["B"].data_ptr(), g["Q"].data_ptr(), g["R"].data_ptr(), g["Qf"].data_ptr(),
+                g["lA"].data_ptr(), g["lB"].data_ptr(), g["lQ"].data_ptr(), g["h0"].data_ptr(),
+                ws.data_ptr(), ws.numel(), limit, status.data_ptr(), _stream_handle(dev))
+        check(rc, "ttc_lqr_backward")
+        if int(status.item()) != 0:
+            raise RuntimeError(_BWD_MSG)
+        out = (g["A"][..., :d], g["B"][:, :d, :du], g["Q"][:, :d, :d], g["R"][..., :du], g["Qf"][:, :, :d, :d],
+               g["lA"], g["lB"][..., :du], g["lQ"][..., :d], g["h0"][..., :d])
+        out = tuple(o.to(dt) if need else None for o, dt, need in zip(out, dtypes, ctx.needs_input_grad[:9]))
+        return out + (None, None, None)
+
+
+def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_diag: torch.Tensor,
+                  Q_f: torch.Tensor, log_gamma_A: torch.Tensor, log_gamma_B: torch.Tensor,
+                  log_gamma_Q: torch.Tensor, h0: torch.Tensor, T: int, grad_limit: float = 1e6,
+                  stash: str | None = None) -> torch.Tensor:
+    """First optimal action ``u [N,H,du]`` of every (token, head) LQR problem.
+
+    Drop-in for the reference ``fused_lqr_solve`` (``fused_lqr.py:294-304``).
+    ``grad_limit``: the backward raises when a gradient reaches it (the reference's
+    1e6 guard, ``fused_lqr.py:245``); ``math.inf`` disables the magnitude check.
+    ``stash``: ``"auto" | "always" | "never"`` overrides ``TTC_LQR_STASH``.
+    """
+    return HipLQRSolveFunc.apply(A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T,
+                                 grad_limit, stash)
