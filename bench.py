@@ -1,0 +1,231 @@
+#!/usr/bin/env python
+"""Benchmark of the TTC-Net LQR solver hot path on one MI355X.
+
+Workload: TTCLayer(in=32, out=32, h=16, heads=8, b_rank=16,
+q_rank=16), T=64, x [16, 2048, 8, 32] ~ N(0,1) (seeded, synthetic), random-init
+weights (seed 0).  The layer front-end turns x into the nine solver inputs
+(N = 262144 tokens, P = N*8 = 2097152 LQR problems), which stay resident in HBM.
+A timed *step* is one solver forward + backward over all P problems with the
+upstream gradient d_u that dy ~ N(0,1) induces through the layer back-end.
+
+Prints one JSON line: value = forward+backward LQR solves/s; the forward-only
+rate, tokens/s, the fp32 roofline of the forward kernel (algorithmic flops per
+problem F_fwd = T(4 d^2 du + 2 d^3), timed with HIP events on the launch stream)
+and a CPU baseline (an op-for-op restatement of the reference `riccati` solver,
+fwd and autograd fwd+bwd, on a bounded token sample, all host cores) ride along.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "ttc-net_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "LQR solves/sec fwd & fwd+bwd (h=16,T=64) + % HBM/MFMA roofline, 1×MI355X"
+PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix peak (published)
+PEAK_HBM = 8.0e12
+
+CONFIGS = {
+    2: dict(in_dim=32, out_dim=32, h_dim=16, num_heads=8, b_rank=16, q_rank=16, T=64, x_shape=(16, 2048, 8, 32)),
+    3: dict(in_dim=64, out_dim=64, h_dim=64, num_heads=16, b_rank=32, q_rank=32, T=128, x_shape=(8, 4096, 16, 64)),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--tokens", type=int, default=0, help="override token count (0 = the config's full x)")
+    ap.add_argument("--stash", default=None, choices=["auto", "always", "never"])
+    ap.add_argument("--cpu-sample-tokens", type=int, default=64)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--fwd-only", action="store_true",
+                    help="profiling aid: time only the forward solve (the JSON value is then fwd solves/s)")
+    ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
+                    help="profiling aid: run one plain device copy of this many GiB and exit "
+                         "(scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
+    return ap.parse_args()
+
+
+def traffic_from_profiles(kernel_tag: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE),
+    as recorded in profiles/<kernel_tag>_pmc.md ("traffic_bytes_per_launch: N")."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.md")
+    try:
+        with open(path) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read())
+        return float(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
+def cpu_baseline(ins_cpu, T, H, sample_tokens):
+    """Reference `riccati` restatement (oracle.ref_torch) on the host, fwd and fwd+bwd."""
+    import torch
+    from oracle.ref_torch import riccati_solve
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    sl = [t[:sample_tokens].contiguous() for t in ins_cpu]
+    # the reference solver consumes symmetric Q / Q_f (bench_lqr_solvers.py:125,127)
+    P = sl[0].shape[0] * H
+
+    def fwd():
+        with torch.no_grad():
+            riccati_solve(*sl, T)
+
+    def fwdbwd():
+        xs = [t.clone().requires_grad_(True) for t in sl]
+        u = riccati_solve(*xs, T)
+        torch.autograd.grad(u, xs, torch.ones_like(u))
+
+    res = {}
+    for name, fn, reps in (("fwd", fwd, 5), ("fwd_bwd", fwdbwd, 3)):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        res[name] = P / statistics.median(ts)
+    return {"value": res["fwd_bwd"], "unit": "solves/s", "cores": torch.get_num_threads(), "kind": "port",
+            "fwd_value": res["fwd"],
+            "sample": f"{sample_tokens} tokens x {H} heads = {P} problems of the same workload, T={T}; "
+                      f"oracle/ref_torch.riccati_solve (reference direct_lqr_solve restated), fwd median of 5, "
+                      f"fwd+bwd (autograd) median of 3, torch threads={torch.get_num_threads()}, "
+                      f"os.cpu_count()={cores}"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the LQR problems shard over tokens with no "
+                                   "exchange, so a multi-GPU figure is not produced here (see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    if args.copy_calibration > 0:
+        n = int(args.copy_calibration * (1 << 30)) // 4
+        a = torch.ones(n, device="cuda:0")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 4 * n}))
+        return
+    from ttc import TTCLayer
+    from ttc.layers.ttc_layer import l2norm
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+
+    c = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    layer = TTCLayer(c["in_dim"], c["out_dim"], c["h_dim"], c["num_heads"], c["b_rank"], c["q_rank"],
+                     solver_impl="hip").to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    xshape = c["x_shape"] if args.tokens == 0 else (args.tokens, c["in_dim"])
+    x = torch.randn(xshape, generator=g, device=dev)
+    T, H, d = c["T"], c["num_heads"], c["h_dim"]
+    with torch.no_grad():
+        ins = [t.float().contiguous() for t in layer.solver_inputs(x)]
+    N = ins[0].shape[0]
+    P = N * H
+    # d_u from dy ~ N(0,1) through the layer back-end (l2norm rescale + out_proj)
+    with torch.no_grad():
+        u0 = hip_lqr_solve(*ins, T)
+    u_req = u0.clone().requires_grad_(True)
+    y = layer.out_proj(l2norm(u_req).reshape(*x.shape[:-1], -1))
+    dy = torch.randn(y.shape, generator=g, device=dev)
+    (d_u,) = torch.autograd.grad(y, u_req, dy)
+    d_u = d_u.contiguous()
+    del y, u_req, u0
+    stream = torch.cuda.current_stream(dev)
+
+    # forward only: per-call GPU time with events on the launch stream
+    for _ in range(args.warmup):
+        with torch.no_grad():
+            hip_lqr_solve(*ins, T)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record(stream)
+        with torch.no_grad():
+            hip_lqr_solve(*ins, T)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    fwd_wall = (time.perf_counter() - t0) / args.steps
+    fwd_gpu_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)
+
+    if args.fwd_only:
+        print(json.dumps({"mode": "fwd-only", "fwd_ms": fwd_gpu_ms, "fwd_solves_per_s": P / (fwd_gpu_ms * 1e-3),
+                          "problems": P}), flush=True)
+        return
+
+    # forward + backward (the timed steps)
+    xs = [t.clone().requires_grad_(True) for t in ins]
+
+    def step():
+        u = hip_lqr_solve(*xs, T, stash=args.stash)
+        return torch.autograd.grad(u, xs, d_u)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+
+    F_fwd = T * (4 * d * d * d + 2 * d ** 3)
+    achieved = F_fwd * P / (fwd_gpu_ms * 1e-3)
+    fwd_bytes = 4 * (3 * d + 2 * d + d * d + 1 + d) + 4 * (d * d + d * d) / H
+    traffic = traffic_from_profiles(f"lqr_fwd_cfg{args.config}")
+    out = {
+        "metric": METRIC,
+        "value": P / step_s,
+        "unit": "solves/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_s * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) x, random-init layer weights)",
+        "config": {"workload": f"cfg{args.config}: TTCLayer(in={c['in_dim']},out={c['out_dim']},h={d},heads={H},"
+                               f"b_rank={c['b_rank']},q_rank={c['q_rank']}) T={T}, x{list(xshape)} -> "
+                               f"{N} tokens, {P} LQR problems, solver fwd+bwd",
+                   "tokens": N, "heads": H, "d": d, "du": d, "T": T, "problems": P},
+        "fwd_solves_per_s": P / (fwd_gpu_ms * 1e-3),
+        "fwd_ms": fwd_gpu_ms,
+        "fwd_wall_ms": fwd_wall * 1e3,
+        "tokens_per_s_fwd_bwd": N / step_s,
+        "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
+        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
+                     "kernel": f"lqr_fwd_kernel<{d}>", "flops_per_problem": F_fwd,
+                     "algorithmic_bytes_per_problem": fwd_bytes},
+    }
+    if not args.no_cpu_baseline:
+        ins_cpu = [t.detach().cpu() for t in ins]
+        out["cpu_baseline"] = cpu_baseline(ins_cpu, T, H, min(args.cpu_sample_tokens, N))
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
