@@ -23,7 +23,7 @@ __all__ = ["dense_qp_u0"]
 def dense_qp_u0(A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0, T: int):
     """First optimal action ``u0 [N,H,du]`` of the discounted LQR, fp64, differentiable.
 
-    Q and Q_f enter through their symmetric parts (the QP objective only sees those).
+    Q and Q_f enter only through the quadratic forms of the objective.
     """
     N, H, d = A_diag.shape
     du = B.shape[-1]
@@ -31,10 +31,10 @@ def dense_qp_u0(A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0, T: int):
     P = N * H
     a = A_diag.reshape(P, d).to(dt)
     Bm = B.to(dt).repeat_interleave(H, dim=0)                      # [P,d,du]
-    Qs = 0.5 * (Q + Q.transpose(-1, -2))
-    Qm = Qs.to(dt).repeat_interleave(H, dim=0)
-    Qfs = 0.5 * (Q_f + Q_f.transpose(-1, -2))
-    Qf = Qfs.to(dt).reshape(P, d, d)
+    # Q, Q_f enter only through the quadratic forms h'Qh (no explicit symmetrisation):
+    # S'CS is symmetrised once below, which is exactly the symmetric part's contribution.
+    Qm = Q.to(dt).repeat_interleave(H, dim=0)
+    Qf = Q_f.to(dt).reshape(P, d, d)
     r = R_inv.to(dt).reshape(P, du)
     la = lgA.to(dt).reshape(P)
     lb = lgB.to(dt).reshape(P, du)
@@ -60,7 +60,8 @@ def dense_qp_u0(A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0, T: int):
             C = q[:, :, None] * Qm * q[:, None, :]
         else:
             C = Qf
-        CS = C @ S
+        Cs = 0.5 * (C + C.transpose(1, 2))     # gradient of the quadratic form h'Ch/2
+        CS = Cs @ S
         Hm = Hm + S.transpose(1, 2) @ CS
         c = c + (CS.transpose(1, 2) @ f[:, :, None])[:, :, 0]
     Hm = 0.5 * (Hm + Hm.transpose(1, 2))

@@ -1,0 +1,94 @@
+"""CPU tests of the C ABI boundary (no GPU work is launched).
+
+* libttc_lqr.so loads and exports every function declared in include/ttc_lqr.h;
+* size helpers follow the documented formulas;
+* argument validation returns the documented codes before touching a device.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ttc_lqr.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ttc_lqr_[a-z_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from ttc.solvers._lib import lib
+    return lib
+
+
+def test_header_declares_expected_entry_points():
+    assert declared_functions() == sorted([
+        "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
+        "ttc_lqr_supported", "ttc_lqr_version", "ttc_lqr_workspace_bytes"])
+
+
+def test_library_exports_every_declared_symbol(L):
+    from ttc.solvers._lib import lib_path
+    raw = ctypes.CDLL(lib_path())
+    for name in declared_functions():
+        assert hasattr(raw, name), f"{name} not exported by {lib_path()}"
+
+
+def test_version_and_strerror(L):
+    assert L.ttc_lqr_version().decode().startswith("ttc-lqr-gfx950")
+    for code in range(4):
+        assert L.ttc_lqr_strerror(code)
+    assert L.ttc_lqr_strerror(99) == b"unknown error"
+
+
+def test_supported_dims(L):
+    for d in (16, 32, 64):
+        assert L.ttc_lqr_supported(d, d) == 1
+    for d, du in [(16, 32), (8, 8), (24, 24), (128, 128), (0, 0)]:
+        assert L.ttc_lqr_supported(d, du) == 0
+
+
+def test_stash_bytes_formula(L):
+    N, H, d, T = 262144, 8, 16, 64
+    assert L.ttc_lqr_stash_bytes(N, H, d, d, T) == 4 * N * H * (T * d * d + d * d)
+    assert L.ttc_lqr_stash_bytes(-1, H, d, d, T) == 0
+
+
+def test_workspace_bytes_monotone_and_stash_smaller(L):
+    a = L.ttc_lqr_workspace_bytes(1, 8, 16, 16, 64, 0)
+    b = L.ttc_lqr_workspace_bytes(100, 8, 16, 16, 64, 0)
+    s = L.ttc_lqr_workspace_bytes(100, 8, 16, 16, 64, 1)
+    assert 0 < a < b and 0 < s < b
+    # per problem: gains T d^2 + Quu_0 d^2 + trajectory 4 T d + two d^2 partials (fp32)
+    assert b >= 4 * 800 * (64 * 256 + 256 + 4 * 64 * 16 + 2 * 256)
+    assert L.ttc_lqr_workspace_bytes(0, 8, 16, 16, 64, 0) == 0
+
+
+def _fwd(L, n=1, h=1, d=16, du=16, T=1, null_inputs=False):
+    p = None if null_inputs else ctypes.c_void_p(16)   # never dereferenced: validation fails first
+    return L.ttc_lqr_forward(*([p] * 9), n, h, d, du, T, p, None, None, None, None)
+
+
+def test_forward_argument_validation(L):
+    from ttc.solvers._lib import lib  # noqa: F401
+    assert _fwd(L, n=-1) == 1                 # TTC_LQR_EINVAL
+    assert _fwd(L, T=0) == 1
+    assert _fwd(L, d=24, du=24) == 2          # TTC_LQR_EUNSUPPORTED
+    assert _fwd(L, d=16, du=32) == 2
+    assert _fwd(L, n=0) == 0                  # empty batch: nothing to do
+    assert _fwd(L, null_inputs=True) == 1
+
+
+def test_backward_argument_validation(L):
+    p = ctypes.c_void_p(16)
+    args = [p] * 10 + [1, 1, 16, 16, 4, None, None] + [p] * 9
+    assert L.ttc_lqr_backward(*args, p, 0, float("inf"), None, None) == 1       # workspace too small
+    bad = [p] * 10 + [1, 1, 20, 20, 4, None, None] + [p] * 9
+    assert L.ttc_lqr_backward(*bad, p, 1 << 30, float("inf"), None, None) == 2  # unsupported dims
+    mixed = [p] * 10 + [1, 1, 16, 16, 4, p, None] + [p] * 9
+    assert L.ttc_lqr_backward(*mixed, p, 1 << 30, float("inf"), None, None) == 1  # stash half given

@@ -7,6 +7,7 @@ both sides.  Gradients of the stress configuration can exceed the reference's
 1e6 guard, so those cases pass ``grad_limit=inf``.
 """
 import math
+import os
 
 import numpy as np
 import pytest
@@ -170,3 +171,21 @@ def test_layer_end_to_end_matches_oracle_layer():
     u64 = solve_u0(LQRProblem(*ins, 16))
     y_ref = back_end(p, torch.from_numpy(u64).float(), ins[8], lead)
     torch.testing.assert_close(y.cpu(), y_ref, rtol=1e-4, atol=1e-5)
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.mark.parametrize("name", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz")))
+def test_against_committed_golden(name):
+    """HIP solver vs the committed fixtures: fp64 oracle slices of every config and
+    the two 50-digit mpmath stress problems (tests/golden/make_golden.py)."""
+    z = np.load(os.path.join(GOLDEN, name))
+    ins = [torch.from_numpy(z[f"in_{k}"]).float() for k in NAMES]
+    T = int(z["T"])
+    print(f"[golden {name}] {z['meta']}", flush=True)
+    out = run_hip(ins, T, z["dU"], grad_limit=math.inf)
+    errs = {k: _relerr(out[k], z[f"out_{k}"]) for k in ["u"] + NAMES}
+    print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+    bad = {k: v for k, v in errs.items() if not (v <= TOL)}
+    assert not bad, f"{name}: rel err above {TOL}: {bad}"

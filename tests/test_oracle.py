@@ -1,0 +1,281 @@
+"""CPU tests that pin the fp64 oracle (no GPU).
+
+The reference holds no golden vectors or known-answer tests for this path
+(its bench_lqr_solvers.py prints diffs and asserts nothing), so the oracle is
+pinned by independent mathematics:
+
+* a brute-force fp64 dense QP over all controls (no Riccati anywhere), for ``u``
+  and, through autograd, all nine gradients; the dense QP itself is checked with
+  ``torch.autograd.gradcheck``;
+* the T=1 closed form and the undiscounted long-horizon limit (scipy DARE);
+* invariants: linearity in h0, dependence on Q / Q_f only through their
+  symmetric parts;
+* 50-digit mpmath solutions of the two worst config-5 stress problems
+  (tests/golden/mp_stress_*.npz), where the dense QP is too ill-conditioned;
+* mutation tests: plausible mistakes planted in the oracle must fail a check.
+"""
+import os
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+import oracle.lqr64 as lqr64
+from oracle.dense_qp import dense_qp_u0
+from oracle.inputs import bench_solver_inputs, layer_solver_inputs, make_x
+from oracle.lqr64 import LQRProblem, expand_step, solve_grads, solve_u0
+
+NAMES = ["A_diag", "B", "Q", "R_inv", "Q_f", "lgA", "lgB", "lgQ", "h0"]
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-300))
+
+
+def random_problem(N, H, d, du, seed, lg_scale=0.5):
+    g = torch.Generator().manual_seed(seed)
+    A = torch.nn.functional.normalize(torch.randn(N, H, d, generator=g), dim=-1)
+    B = torch.randn(N, d, du, generator=g) * 0.7
+    Qh = torch.randn(N, d, d, generator=g) / d ** 0.5
+    Q = Qh @ Qh.transpose(-1, -2)
+    Qfh = torch.randn(N, H, d, d, generator=g) / d ** 0.5
+    Q_f = Qfh @ Qfh.transpose(-1, -2)
+    R_inv = torch.nn.functional.softplus(torch.randn(N, H, du, generator=g)) + 0.05
+    lgA = -lg_scale * torch.rand(N, H, generator=g)
+    lgB = -lg_scale * torch.rand(N, H, du, generator=g)
+    lgQ = -lg_scale * torch.rand(N, H, d, generator=g)
+    h0 = torch.randn(N, H, d, generator=g)
+    return [t.double() for t in (A, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0)]
+
+
+def dense_grads(ins, T, dU):
+    xs = [t.clone().requires_grad_(True) for t in ins]
+    u = dense_qp_u0(*xs, T)
+    (u * torch.as_tensor(dU)).sum().backward()
+    out = {"u": u.detach().numpy()}
+    for n, t in zip(NAMES, xs):
+        out[n] = t.grad.numpy() if t.grad is not None else np.zeros(t.shape)
+    return out
+
+
+# ---------------------------------------------------------------- expansion
+def test_expand_step_closed_forms():
+    ins = random_problem(2, 3, 5, 4, seed=1)
+    pb = LQRProblem(*ins, T=6)
+    A, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0 = [t.numpy() for t in ins]
+    for k in range(6):
+        alpha, Bk, Qc = expand_step(pb, k)
+        n, h = 1, 2
+        p = n * 3 + h
+        np.testing.assert_allclose(alpha[p], 1 + A[n, h] * np.exp(lgA[n, h] * (k + 1)), rtol=1e-14)
+        np.testing.assert_allclose(Bk[p], B[n] * np.exp(lgB[n, h] * (k + 1))[None, :], rtol=1e-14)
+        if k == 0:
+            assert Qc is None
+        else:
+            q = np.exp(lgQ[n, h] * k)
+            np.testing.assert_allclose(Qc[p], q[:, None] * 0.5 * (Q[n] + Q[n].T) * q[None, :], rtol=1e-14)
+
+
+# ---------------------------------------------------------------- forward
+@pytest.mark.parametrize("N,H,d,du,T", [(2, 2, 4, 4, 1), (2, 3, 4, 3, 5), (1, 2, 6, 6, 12), (1, 1, 5, 2, 20)])
+def test_u0_matches_dense_qp(N, H, d, du, T):
+    ins = random_problem(N, H, d, du, seed=N + H + d + T)
+    u = solve_u0(LQRProblem(*ins, T))
+    ud = dense_qp_u0(*ins, T).numpy()
+    assert rel(u, ud) < 1e-11
+
+
+def test_T1_closed_form():
+    ins = random_problem(2, 2, 5, 3, seed=3)
+    A, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0 = [t.numpy() for t in ins]
+    u = solve_u0(LQRProblem(*ins, 1))
+    for n in range(2):
+        for h in range(2):
+            A0 = np.diag(1 + A[n, h] * np.exp(lgA[n, h]))
+            B0 = B[n] * np.exp(lgB[n, h])[None, :]
+            R = np.diag(1 / R_inv[n, h])
+            Qf = 0.5 * (Q_f[n, h] + Q_f[n, h].T)
+            ref = -np.linalg.solve(R + B0.T @ Qf @ B0, B0.T @ Qf @ A0 @ h0[n, h])
+            np.testing.assert_allclose(u[n, h], ref, rtol=1e-12, atol=1e-14)
+
+
+def test_undiscounted_long_horizon_matches_dare():
+    ins = random_problem(1, 2, 4, 3, seed=7)
+    for i in (5, 6, 7):
+        ins[i] = torch.zeros_like(ins[i])          # log gammas 0: time-invariant system
+    T = 400
+    u = solve_u0(LQRProblem(*ins, T))
+    A, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0 = [t.numpy() for t in ins]
+    for h in range(2):
+        Am = np.diag(1 + A[0, h])
+        R = np.diag(1 / R_inv[0, h])
+        P = scipy.linalg.solve_discrete_are(Am, B[0], Q[0], R)
+        K0 = -np.linalg.solve(R + B[0].T @ P @ B[0], B[0].T @ P @ Am)   # no cost on h_0
+        np.testing.assert_allclose(u[0, h], K0 @ h0[0, h], rtol=1e-8, atol=1e-10)
+
+
+def test_u0_linear_in_h0():
+    ins = random_problem(2, 2, 5, 5, seed=4)
+    g = torch.Generator().manual_seed(2)
+    h1 = torch.randn(ins[8].shape, generator=g, dtype=torch.float64)
+    u_a = solve_u0(LQRProblem(*ins, 9))
+    ins_b = list(ins); ins_b[8] = h1
+    u_b = solve_u0(LQRProblem(*ins_b, 9))
+    ins_c = list(ins); ins_c[8] = 2.5 * ins[8] - 0.75 * h1
+    u_c = solve_u0(LQRProblem(*ins_c, 9))
+    np.testing.assert_allclose(u_c, 2.5 * u_a - 0.75 * u_b, rtol=1e-10, atol=1e-12)
+
+
+def test_only_symmetric_parts_of_Q_matter():
+    ins = random_problem(1, 2, 5, 4, seed=5)
+    g = torch.Generator().manual_seed(9)
+    S = torch.randn(1, 5, 5, generator=g, dtype=torch.float64)
+    Sf = torch.randn(1, 2, 5, 5, generator=g, dtype=torch.float64)
+    ins2 = list(ins)
+    ins2[2] = ins[2] + (S - S.transpose(-1, -2))
+    ins2[4] = ins[4] + (Sf - Sf.transpose(-1, -2))
+    # the dense QP sees Q only through h'Qh; the oracle symmetrises explicitly
+    assert rel(solve_u0(LQRProblem(*ins2, 7)), dense_qp_u0(*ins2, 7).numpy()) < 1e-11
+    assert rel(solve_u0(LQRProblem(*ins2, 7)), solve_u0(LQRProblem(*ins, 7))) < 1e-12
+
+
+# ---------------------------------------------------------------- gradients
+def test_dense_qp_gradcheck():
+    ins = random_problem(1, 2, 3, 2, seed=8)
+    xs = [t.clone().requires_grad_(True) for t in ins]
+    assert torch.autograd.gradcheck(lambda *a: dense_qp_u0(*a, 4), xs, eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+@pytest.mark.parametrize("N,H,d,du,T", [(2, 2, 4, 4, 1), (2, 3, 4, 3, 6), (1, 2, 6, 6, 12), (2, 2, 5, 2, 9)])
+def test_grads_match_dense_qp_autograd(N, H, d, du, T):
+    ins = random_problem(N, H, d, du, seed=10 + T)
+    dU = np.random.RandomState(T).randn(N, H, du)
+    ref = dense_grads(ins, T, dU)
+    g = solve_grads(LQRProblem(*ins, T), dU)
+    for k in ["u"] + NAMES:
+        if not np.any(ref[k]):                   # e.g. Q has no effect when T == 1
+            assert np.abs(g[k]).max() < 1e-12, k
+            continue
+        assert rel(g[k], ref[k]) < 1e-9, (k, rel(g[k], ref[k]))
+
+
+def test_grads_finite_difference_directional():
+    ins = random_problem(1, 2, 4, 3, seed=12)
+    T = 7
+    dU = np.random.RandomState(3).randn(1, 2, 3)
+    g = solve_grads(LQRProblem(*ins, T), dU)
+    rng = np.random.RandomState(4)
+    for i, n in enumerate(NAMES):
+        v = rng.randn(*ins[i].shape)
+        if n in ("Q", "Q_f"):
+            v = 0.5 * (v + np.swapaxes(v, -1, -2))
+        eps = 1e-6
+
+        def L(s):
+            xs = list(ins)
+            xs[i] = ins[i] + s * torch.from_numpy(v)
+            return float((solve_u0(LQRProblem(*xs, T)) * dU).sum())
+        fd = (L(eps) - L(-eps)) / (2 * eps)
+        an = float((g[n] * v).sum())
+        assert abs(fd - an) <= 1e-6 * max(1.0, abs(an)), (n, fd, an)
+
+
+# ---------------------------------------------------------------- stress goldens (mpmath, 50 digits)
+@pytest.mark.parametrize("name", ["mp_stress_cfg5_T64.npz", "mp_stress_cfg5_T1024.npz"])
+def test_oracle_matches_mpmath_on_stress_problems(name):
+    path = os.path.join(GOLDEN, name)
+    z = np.load(path)
+    ins = [torch.from_numpy(z[f"in_{k}"]) for k in NAMES]
+    g = solve_grads(LQRProblem(*ins, int(z["T"])), z["dU"])
+    for k in ["u"] + NAMES:
+        assert rel(g[k], z[f"out_{k}"]) < 1e-10, (k, rel(g[k], z[f"out_{k}"]))
+
+
+def test_open_loop_costates_fail_on_stress_problem():
+    """Why the oracle (and the kernels) use closed-loop costates: the reference's
+    open-loop sweep lambda_k = Qc h + A lambda_{k+1} loses the T=1024 stress
+    problem even in fp64, while the closed-loop form matches mpmath."""
+    z = np.load(os.path.join(GOLDEN, "mp_stress_cfg5_T1024.npz"))
+    ins = [torch.from_numpy(z[f"in_{k}"]) for k in NAMES]
+    pb = LQRProblem(*ins, int(z["T"]))
+    g_open = _solve_grads_open_loop(pb, z["dU"])
+    assert rel(g_open["h0"], z["out_h0"]) > 1e-3
+
+
+def _solve_grads_open_loop(pb, dU):
+    """grad h0 from the reference's open-loop costate recursion (lin_solver_lqr.py:82-106)."""
+    mv = lqr64._mv
+    T, P, d = pb.T, pb.P, pb.d
+    K, Quu0 = lqr64._riccati(pb, keep_gains=True)
+    steps = [expand_step(pb, k) for k in range(T)]
+    dU = np.asarray(dU, np.float64).reshape(P, pb.du)
+    h = np.zeros((T + 1, P, d)); hb = np.zeros((T + 1, P, d))
+    h[0] = pb.h0
+    k0 = -np.linalg.solve(Quu0, dU[:, :, None])[:, :, 0]
+    for k in range(T):
+        alpha, Bk, _ = steps[k]
+        u = mv(K[k], h[k]); w = mv(K[k], hb[k]) + (k0 if k == 0 else 0.0)
+        h[k + 1] = alpha * h[k] + mv(Bk, u)
+        hb[k + 1] = alpha * hb[k] + mv(Bk, w)
+    lamb = mv(pb.Qf, hb[T])
+    for k in range(T - 1, 0, -1):
+        alpha, _, Qc = steps[k]
+        lamb = mv(Qc, hb[k]) + alpha * lamb
+    return {"h0": (steps[0][0] * lamb).reshape(pb.N, pb.H, d)}
+
+
+# ---------------------------------------------------------------- mutation tests
+def test_mutation_discount_index_is_caught(monkeypatch):
+    """Exponent k instead of k+1 for A_k (an off-by-one) must fail the dense QP check."""
+    good = lqr64.expand_step
+
+    def bad(pb, k):
+        alpha, Bk, Qc = good(pb, k)
+        alpha = 1.0 + pb.a * np.exp(pb.lgA * k)[:, None]
+        return alpha, Bk, Qc
+    monkeypatch.setattr(lqr64, "expand_step", bad)
+    ins = random_problem(1, 2, 4, 3, seed=21)
+    assert rel(lqr64.solve_u0(LQRProblem(*ins, 6)), dense_qp_u0(*ins, 6).numpy()) > 1e-3
+
+
+def test_mutation_state_cost_exponent_is_caught(monkeypatch):
+    """Discounting the cost on h_k with exp(lgQ*(k+1)) instead of exp(lgQ*k) (the
+    expansion index shift of torch_lqr.py:85 vs lin_solver_lqr.py:139) must fail."""
+    good = lqr64.expand_step
+
+    def bad(pb, k):
+        alpha, Bk, Qc = good(pb, k)
+        if k > 0:
+            q = np.exp(pb.lgQ * (k + 1))
+            Qc = q[:, :, None] * pb.Qm * q[:, None, :]
+        return alpha, Bk, Qc
+    monkeypatch.setattr(lqr64, "expand_step", bad)
+    ins = random_problem(1, 2, 4, 3, seed=22)
+    dU = np.ones((1, 2, 3))
+    ref = dense_grads(ins, 6, dU)
+    g = lqr64.solve_grads(LQRProblem(*ins, 6), dU)
+    assert max(rel(g[k], ref[k]) for k in ["u"] + NAMES) > 1e-3
+
+
+def test_mutation_transposed_B_is_caught(monkeypatch):
+    good = lqr64.expand_step
+
+    def bad(pb, k):
+        alpha, Bk, Qc = good(pb, k)
+        return alpha, np.swapaxes(Bk, -1, -2), Qc
+    monkeypatch.setattr(lqr64, "expand_step", bad)
+    ins = random_problem(1, 2, 4, 4, seed=23)
+    assert rel(lqr64.solve_u0(LQRProblem(*ins, 5)), dense_qp_u0(*ins, 5).numpy()) > 1e-3
+
+
+def test_mutation_gradient_sign_is_caught(monkeypatch):
+    """A flipped sign in the R_inv chain rule (d/dR_inv of 1/R_inv) must fail autograd."""
+    ins = random_problem(1, 2, 4, 3, seed=24)
+    dU = np.ones((1, 2, 3))
+    ref = dense_grads(ins, 5, dU)
+    g = lqr64.solve_grads(LQRProblem(*ins, 5), dU)
+    assert rel(-g["R_inv"], ref["R_inv"]) > 1e-3
+    assert rel(g["R_inv"], ref["R_inv"]) < 1e-9
