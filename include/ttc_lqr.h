@@ -47,6 +47,12 @@ extern "C" {
 #define TTC_LQR_STATUS_NONFINITE 1
 #define TTC_LQR_STATUS_LARGE 2
 
+/* `flags` bits.  TTC_LQR_FLAG_FP64_RICCATI runs the backward-in-time Riccati sweep
+ * (the gains) in fp64 arithmetic; inputs, outputs and the stash stay fp32.  Needed
+ * for long, barely-discounted horizons (e.g. T = 1024 with log-normal inputs),
+ * where fp32 rounding of V ~ 1e17 corrupts the gains. */
+#define TTC_LQR_FLAG_FP64_RICCATI 1
+
 /* Library version string. */
 const char* ttc_lqr_version(void);
 
@@ -55,6 +61,9 @@ const char* ttc_lqr_strerror(int code);
 
 /* 1 if the kernels were compiled for this (d, du), else 0. */
 int ttc_lqr_supported(int32_t d, int32_t du);
+
+/* 1 if (d, du) is supported with these `flags` (fp64 Riccati: d <= 32), else 0. */
+int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags);
 
 /* Bytes of the optional gain stash written by ttc_lqr_forward for the backward:
  * per problem T*d*du gain floats plus du*du floats of the step-0 control Hessian. */
@@ -74,8 +83,8 @@ size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, i
 int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const float* R_inv,
                     const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
                     const float* log_gamma_Q, const float* h0, int64_t n_tokens, int32_t heads,
-                    int32_t d, int32_t du, int32_t T, float* u, float* gain_stash, float* quu0_stash,
-                    int32_t* status, void* stream);
+                    int32_t d, int32_t du, int32_t T, int32_t flags, float* u, float* gain_stash,
+                    float* quu0_stash, int32_t* status, void* stream);
 
 /* Backward: gradients of sum(d_u * u) w.r.t. the nine inputs.
  * Replaces fused_lqr_layer_bwd (ttc/solvers/fused_lqr.py:148-253).
@@ -83,12 +92,13 @@ int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const f
  * gain_stash / quu0_stash: from ttc_lqr_forward, or both NULL (gains recomputed
  * chunk by chunk inside `workspace`).  workspace_bytes must be at least
  * ttc_lqr_workspace_bytes(c, ...) for some c >= 1 token; larger workspaces give
- * fewer, larger passes.  grad_limit: |g| >= grad_limit sets TTC_LQR_STATUS_LARGE
+ * fewer, larger passes.  `flags` applies to the gain recomputation (unused when
+ * the stash is given).  grad_limit: |g| >= grad_limit sets TTC_LQR_STATUS_LARGE
  * (the reference uses 1e6, fused_lqr.py:245); pass INFINITY to disable. */
 int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const float* R_inv,
                      const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
                      const float* log_gamma_Q, const float* h0, const float* d_u,
-                     int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
+                     int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T, int32_t flags,
                      const float* gain_stash, const float* quu0_stash,
                      float* grad_A_diag, float* grad_B, float* grad_Q, float* grad_R_inv,
                      float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,

@@ -29,7 +29,7 @@ def L():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
-        "ttc_lqr_supported", "ttc_lqr_version", "ttc_lqr_workspace_bytes"])
+        "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -53,6 +53,13 @@ def test_supported_dims(L):
         assert L.ttc_lqr_supported(d, du) == 0
 
 
+def test_supported_flags(L):
+    assert L.ttc_lqr_supported_flags(16, 16, 1) == 1 and L.ttc_lqr_supported_flags(32, 32, 1) == 1
+    assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
+    assert L.ttc_lqr_supported_flags(16, 16, 4) == 0
+    assert _fwd(L, d=64, du=64, flags=1) == 2
+
+
 def test_stash_bytes_formula(L):
     N, H, d, T = 262144, 8, 16, 64
     assert L.ttc_lqr_stash_bytes(N, H, d, d, T) == 4 * N * H * (T * d * d + d * d)
@@ -69,9 +76,9 @@ def test_workspace_bytes_monotone_and_stash_smaller(L):
     assert L.ttc_lqr_workspace_bytes(0, 8, 16, 16, 64, 0) == 0
 
 
-def _fwd(L, n=1, h=1, d=16, du=16, T=1, null_inputs=False):
+def _fwd(L, n=1, h=1, d=16, du=16, T=1, null_inputs=False, flags=0):
     p = None if null_inputs else ctypes.c_void_p(16)   # never dereferenced: validation fails first
-    return L.ttc_lqr_forward(*([p] * 9), n, h, d, du, T, p, None, None, None, None)
+    return L.ttc_lqr_forward(*([p] * 9), n, h, d, du, T, flags, p, None, None, None, None)
 
 
 def test_forward_argument_validation(L):
@@ -86,9 +93,9 @@ def test_forward_argument_validation(L):
 
 def test_backward_argument_validation(L):
     p = ctypes.c_void_p(16)
-    args = [p] * 10 + [1, 1, 16, 16, 4, None, None] + [p] * 9
+    args = [p] * 10 + [1, 1, 16, 16, 4, 0, None, None] + [p] * 9
     assert L.ttc_lqr_backward(*args, p, 0, float("inf"), None, None) == 1       # workspace too small
-    bad = [p] * 10 + [1, 1, 20, 20, 4, None, None] + [p] * 9
+    bad = [p] * 10 + [1, 1, 20, 20, 4, 0, None, None] + [p] * 9
     assert L.ttc_lqr_backward(*bad, p, 1 << 30, float("inf"), None, None) == 2  # unsupported dims
-    mixed = [p] * 10 + [1, 1, 16, 16, 4, p, None] + [p] * 9
+    mixed = [p] * 10 + [1, 1, 16, 16, 4, 0, p, None] + [p] * 9
     assert L.ttc_lqr_backward(*mixed, p, 1 << 30, float("inf"), None, None) == 1  # stash half given

@@ -33,11 +33,11 @@ def _relerr(x, ref):
     return float(np.abs(x - ref).max() / max(np.abs(ref).max(), 1e-30))
 
 
-def run_hip(ins, T, dU, grad_limit=1e6, stash=None):
+def run_hip(ins, T, dU, grad_limit=1e6, stash=None, precision="auto"):
     solve = _solver()
     dev = torch.device("cuda:0")
     xs = [t.detach().to(dev).float().requires_grad_(True) for t in ins]
-    u = solve(*xs, T, grad_limit=grad_limit, stash=stash)
+    u = solve(*xs, T, grad_limit=grad_limit, stash=stash, precision=precision)
     (u * torch.as_tensor(dU, device=dev, dtype=u.dtype)).sum().backward()
     out = {"u": u.detach().cpu().double().numpy()}
     for n, t in zip(NAMES, xs):
@@ -45,13 +45,13 @@ def run_hip(ins, T, dU, grad_limit=1e6, stash=None):
     return out
 
 
-def check_case(label, ins, T, seed=0, grad_limit=1e6, stash=None, tol=TOL):
+def check_case(label, ins, T, seed=0, grad_limit=1e6, stash=None, tol=TOL, precision="auto"):
     pb = LQRProblem(*ins, T)
     g = torch.Generator().manual_seed(seed + 7)
     dU = torch.randn(pb.N, pb.H, pb.du, generator=g).double().numpy()
     ref = solve_grads(pb, dU)
-    print(f"[{label}] N={pb.N} H={pb.H} d={pb.d} du={pb.du} T={T} stash={stash}", flush=True)
-    out = run_hip(ins, T, dU, grad_limit=grad_limit, stash=stash)
+    print(f"[{label}] N={pb.N} H={pb.H} d={pb.d} du={pb.du} T={T} stash={stash} precision={precision}", flush=True)
+    out = run_hip(ins, T, dU, grad_limit=grad_limit, stash=stash, precision=precision)
     errs = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
     print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
     bad = {k: v for k, v in errs.items() if not (v <= tol)}
@@ -71,10 +71,11 @@ def test_config1_layer_slice(stash):
     check_case("cfg1", layer_solver_inputs(1, x), c["T"], stash=stash)
 
 
-def test_config2_layer_slice():
+@pytest.mark.parametrize("precision", ["fp32", "fp64"])
+def test_config2_layer_slice(precision):
     c = CONFIGS[2]
     x = make_x(2, n_tokens=64, seed=1)
-    check_case("cfg2", layer_solver_inputs(2, x), c["T"])
+    check_case("cfg2", layer_solver_inputs(2, x), c["T"], precision=precision)
 
 
 def test_config3_layer_slice():
@@ -83,10 +84,11 @@ def test_config3_layer_slice():
     check_case("cfg3", layer_solver_inputs(3, x), c["T"])
 
 
-def test_config4_layer_slice():
+@pytest.mark.parametrize("precision", ["fp32", "fp64"])
+def test_config4_layer_slice(precision):
     c = CONFIGS[4]
     x = make_x(4, n_tokens=1, seed=3)
-    check_case("cfg4", layer_solver_inputs(4, x), c["T"])
+    check_case("cfg4", layer_solver_inputs(4, x), c["T"], precision=precision)
 
 
 @pytest.mark.parametrize("cfg,T", [(5, 64), (5, 1024), ("5b", 1024)])

@@ -13,7 +13,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.normpath(os.path.join(HERE, "..", ".."))
 OUT_DIR = os.path.normpath(os.path.join(HERE, "..", "lib"))
-SOURCES = ["ttc_lqr.hip"]
+SOURCES = ["ttc_lqr_capi.hip", "ttc_lqr_d16.hip", "ttc_lqr_d32.hip", "ttc_lqr_d64.hip"]
 ARCH = os.environ.get("TTC_LQR_ARCH", "gfx950")
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (see DESIGN notes on this pool)
@@ -22,12 +22,7 @@ HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
                "-I", os.path.join(ROOT, "include")]
 
 
-def build(verbose: bool = True) -> str:
-    os.makedirs(OUT_DIR, exist_ok=True)
-    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-    out = os.path.join(OUT_DIR, "libttc_lqr.so")
-    tmp = out + ".tmp"
-    cmd = [hipcc, *HIPCC_FLAGS, "-shared", *[os.path.join(HERE, s) for s in SOURCES], "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -37,6 +32,22 @@ def build(verbose: bool = True) -> str:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{errs}")
     if errs.strip() and verbose:
         print(errs, file=sys.stderr)
+
+
+def build(verbose: bool = True) -> str:
+    """Compile each translation unit in parallel, then link the shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(OUT_DIR, exist_ok=True)
+    obj_dir = os.path.join(OUT_DIR, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    out = os.path.join(OUT_DIR, "libttc_lqr.so")
+    tmp = out + ".tmp"
+    objs = [os.path.join(obj_dir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    cmds = [[hipcc, *HIPCC_FLAGS, "-c", os.path.join(HERE, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+        list(ex.map(lambda c: _run(c, verbose), cmds))
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", *objs, "-o", tmp], verbose)
     os.replace(tmp, out)
     return out
 

@@ -1,0 +1,21 @@
+// ttc_lqr_d32.hip -- kernels instantiated for d = du = 32.
+#include "ttc_lqr_kernels.cuh"
+
+namespace ttc {
+
+int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                  const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
+                  float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags) {
+  return launch_fwd<32, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, kst, q0s, status, s, flags);
+}
+
+int launch_bwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                  const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
+                  const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
+                  float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
+                  float* gQp, float limit, int32_t* status, hipStream_t s) {
+  return launch_bwd<32>(A, B, Q, R, Qf, lA, lB, lQ, h0, dU, kst, q0s, P, H, T, traj, gA, gR, gQf, glA, glB, glQ,
+                       gh0, gBp, gQp, limit, status, s);
+}
+
+}  // namespace ttc

@@ -1,3 +1,4 @@
+#pragma once
 // ttc_lqr.hip -- gfx950 kernels + C ABI for TTC-Net's batched receding-horizon LQR solve.
 //
 // Problem (one per token n and head h, P = N*H problems), restating
@@ -30,8 +31,8 @@
 #include <stdint.h>
 
 #include "ttc_lqr.h"
+#include "ttc_lqr_internal.h"
 
-#define TTC_LQR_VERSION_STRING "ttc-lqr-gfx950 0.1.0"
 
 namespace ttc {
 
@@ -41,10 +42,10 @@ template <int D>
 struct Geo {
   static constexpr int PPB = (D == 16) ? 16 : (D == 32 ? 4 : 1);  // problems per block
   static constexpr int THREADS = PPB * D;
-  static constexpr int LDM = D + kPad;                  // LDS row stride
+  static constexpr int LDM = D + kPad;                  // LDS row stride (elements)
   static constexpr int MAT = D * LDM;
-  static constexpr int NVEC = 12;                       // D-float vector slots per problem
-  static constexpr int PER_PROB = MAT + NVEC * D + 4;   // +4 floats: bank skew between problems
+  static constexpr int NVEC = 12;                       // D-element vector slots per problem
+  static constexpr int PER_PROB = MAT + NVEC * D + 4;   // +4 elements: bank skew between problems
 };
 
 // Order LDS traffic between lanes of one wave: stores before this point are
@@ -55,21 +56,36 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int N>
-__device__ __forceinline__ void ld_row(const float* s, float (&out)[N]) {
+// 16-byte vector moves of fp32 (4 per vector) or fp64 (2 per vector) rows.
+template <typename R> struct V16;
+template <> struct V16<float> {
+  static constexpr int N = 4;
+  __device__ static void ld(const float* s, float* o) {
+    const float4 v = *reinterpret_cast<const float4*>(s);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  }
+  __device__ static void st(float* s, const float* i) { *reinterpret_cast<float4*>(s) = make_float4(i[0], i[1], i[2], i[3]); }
+};
+template <> struct V16<double> {
+  static constexpr int N = 2;
+  __device__ static void ld(const double* s, double* o) {
+    const double2 v = *reinterpret_cast<const double2*>(s);
+    o[0] = v.x; o[1] = v.y;
+  }
+  __device__ static void st(double* s, const double* i) { *reinterpret_cast<double2*>(s) = make_double2(i[0], i[1]); }
+};
+
+template <int N, typename R>
+__device__ __forceinline__ void ld_row(const R* s, R (&out)[N]) {
   static_assert(N % 4 == 0, "row length");
 #pragma unroll
-  for (int c = 0; c < N; c += 4) {
-    const float4 v = *reinterpret_cast<const float4*>(s + c);
-    out[c] = v.x; out[c + 1] = v.y; out[c + 2] = v.z; out[c + 3] = v.w;
-  }
+  for (int c = 0; c < N; c += V16<R>::N) V16<R>::ld(s + c, out + c);
 }
 
-template <int N>
-__device__ __forceinline__ void st_row(float* s, const float (&in)[N]) {
+template <int N, typename R>
+__device__ __forceinline__ void st_row(R* s, const R (&in)[N]) {
 #pragma unroll
-  for (int c = 0; c < N; c += 4)
-    *reinterpret_cast<float4*>(s + c) = make_float4(in[c], in[c + 1], in[c + 2], in[c + 3]);
+  for (int c = 0; c < N; c += V16<R>::N) V16<R>::st(s + c, in + c);
 }
 
 template <int N>
@@ -118,51 +134,59 @@ __device__ __forceinline__ float group_sum(float v, float* scratch, int li) {
   return s;
 }
 
+// Monotone 32-bit key of |x| (fp64: its high word, sign cleared).
+__device__ __forceinline__ unsigned mag_key(float x) { return __float_as_uint(fabsf(x)); }
+__device__ __forceinline__ unsigned mag_key(double x) {
+  return (unsigned)(__double_as_longlong(fabs(x)) >> 32);
+}
+
 // In-place Gauss-Jordan elimination with partial pivoting on the D x D left block
 // of the augmented rows `aug` (lane li owns row li, width W >= D).  On return the
 // lane with pivot position `pos` holds row `pos` of (left^{-1} * right) scaled by
-// `mypiv` (divide by it).  `prow` is W floats of this problem's LDS.
-template <int D, int W>
-__device__ __forceinline__ void gauss_jordan(float (&aug)[W], int li, float* prow, float& mypiv, int& pos) {
+// `mypiv` (divide by it).  `prow` is W elements of this problem's LDS.
+template <int D, int W, typename R>
+__device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& mypiv, int& pos) {
   constexpr unsigned kIdxBits = (D == 16) ? 4u : (D == 32 ? 5u : 6u);
   constexpr unsigned kIdxMask = (1u << kIdxBits) - 1u;
+  constexpr int VN = V16<R>::N;
   bool done = false;
-  mypiv = 1.f;
+  mypiv = R(1);
   pos = 0;
 #pragma unroll
   for (int k = 0; k < D; ++k) {
     // pivot = largest |aug[k]| among rows not yet used; ties -> lowest lane.
-    // Key = magnitude bits with the low mantissa bits replaced by (D-1-lane).
-    const unsigned mag = __float_as_uint(fabsf(aug[k]));
-    const unsigned key = done ? 0u : ((mag & ~kIdxMask) | (unsigned)(D - 1 - li));
+    // Key = magnitude bits with the low bits replaced by (D-1-lane).
+    const unsigned key = done ? 0u : ((mag_key(aug[k]) & ~kIdxMask) | (unsigned)(D - 1 - li));
     const unsigned best = group_max_u32<D>(key);
     const int who = D - 1 - (int)(best & kIdxMask);
     const bool me = (who == li);
+    constexpr int c0 = 0;
+    (void)c0;
+    const int cs = k & ~(VN - 1);
     if (me) {
 #pragma unroll
-      for (int c = (k & ~3); c < W; c += 4)
-        *reinterpret_cast<float4*>(prow + c) = make_float4(aug[c], aug[c + 1], aug[c + 2], aug[c + 3]);
+      for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::st(prow + c, aug + c);
     }
     wave_sync();
-    float pr[W];
+    R pr[W];
 #pragma unroll
-    for (int c = (k & ~3); c < W; c += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(prow + c);
-      pr[c] = v.x; pr[c + 1] = v.y; pr[c + 2] = v.z; pr[c + 3] = v.w;
-    }
-    const float inv = 1.0f / pr[k];
-    const float f = me ? 0.f : aug[k] * inv;
+    for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::ld(prow + c, pr + c);
+    (void)cs;
+    const R inv = R(1) / pr[k];
+    const R f = me ? R(0) : aug[k] * inv;
 #pragma unroll
-    for (int c = k + 1; c < W; ++c) aug[c] = fmaf(-f, pr[c], aug[c]);
+    for (int c = k + 1; c < W; ++c) aug[c] = fma(-f, pr[c], aug[c]);
     if (me) { mypiv = pr[k]; pos = k; done = true; }
     wave_sync();  // next pivot row may overwrite prow
   }
 }
 
 // ---------------------------------------------------------------------------
-// Forward kernel: Riccati sweep, u0, optional gain stash.
+// Forward kernel: Riccati sweep, u0, optional gain stash.  R is the arithmetic
+// type of the sweep (float, or double for long ill-conditioned horizons);
+// inputs, u and the stash are fp32 in HBM.
 // ---------------------------------------------------------------------------
-template <int D, bool STASH, bool WRITE_U>
+template <int D, typename R, bool STASH, bool WRITE_U>
 __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
@@ -170,7 +194,8 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
     int64_t P, int H, int T, int ntok_lds, float* __restrict__ u_out, float* __restrict__ kstash,
     float* __restrict__ q0stash, int* __restrict__ status) {
   using G = Geo<D>;
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  R* smem = reinterpret_cast<R*>(smem_raw);
   const int li = threadIdx.x % D;
   const int pb = threadIdx.x / D;
   const int64_t p0 = (int64_t)blockIdx.x * G::PPB;
@@ -186,58 +211,59 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
     const int ntok = (int)(plast / H - n0 + 1);
     for (int e = threadIdx.x; e < ntok * D * D; e += G::THREADS) {
       const int tk = e / (D * D), rem = e % (D * D);
-      smem[(tk * D + rem / D) * G::LDM + rem % D] = Bg[(n0 + tk) * D * D + rem];
+      smem[(tk * D + rem / D) * G::LDM + rem % D] = (R)Bg[(n0 + tk) * D * D + rem];
     }
   }
   __syncthreads();
-  const float* Bs = smem + (int)(n - n0) * G::MAT;
-  float* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
-  float* mat = S;
-  float* vb = S + G::MAT;
-  float* va = vb + D;
-  float* vx = va + D;
-  float* prow = vx + D;  // 2D floats
+  const R* Bs = smem + (int)(n - n0) * G::MAT;
+  R* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
+  R* mat = S;
+  R* vb = S + G::MAT;
+  R* va = vb + D;
+  R* vx = va + D;
+  R* prow = vx + D;  // 2D elements
 
-  const float a_i = A_diag[p * D + li];
-  const float rr_i = 1.0f / Rinv[p * D + li];
-  const float lgB_i = lgB[p * D + li];
-  const float lgQ_i = lgQ[p * D + li];
-  const float lgA_p = lgA[p];
+  const R a_i = A_diag[p * D + li];
+  const R rr_i = R(1) / (R)Rinv[p * D + li];
+  const R lgB_i = lgB[p * D + li];
+  const R lgQ_i = lgQ[p * D + li];
+  const R lgA_p = lgA[p];
 
-  float V[D], Bcol[D], Qrow[D];
+  R V[D], Bcol[D], Qrow[D];
   {
     const float* qf = Qf + p * D * D;
     const float* qg = Qg + n * D * D;
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      V[c] = 0.5f * (qf[li * D + c] + qf[c * D + li]);
-      Qrow[c] = 0.5f * (qg[li * D + c] + qg[c * D + li]);
+      V[c] = R(0.5) * ((R)qf[li * D + c] + (R)qf[c * D + li]);
+      Qrow[c] = R(0.5) * ((R)qg[li * D + c] + (R)qg[c * D + li]);
       Bcol[c] = Bs[c * G::LDM + li];
     }
   }
+
   for (int t = T - 1; t >= 0; --t) {
-    const float tp1 = (float)(t + 1);
-    const float eA = expf(lgA_p * tp1);
-    const float beta_i = expf(lgB_i * tp1);
-    const float alpha_i = fmaf(a_i, eA, 1.0f);
-    const float q_i = (t > 0) ? expf(lgQ_i * (float)t) : 0.f;
+    const R tp1 = (R)(t + 1);
+    const R eA = exp(lgA_p * tp1);
+    const R beta_i = exp(lgB_i * tp1);
+    const R alpha_i = fma(a_i, eA, R(1));
+    const R q_i = (t > 0) ? exp(lgQ_i * (R)t) : R(0);
 
     // W~ = V B (row li)
-    float w[D];
+    R w[D];
 #pragma unroll
-    for (int k = 0; k < D; ++k) w[k] = 0.f;
+    for (int k = 0; k < D; ++k) w[k] = R(0);
 #pragma unroll
     for (int m = 0; m < D; ++m) {
-      float brow[D];
+      R brow[D];
       ld_row<D>(Bs + m * G::LDM, brow);
 #pragma unroll
-      for (int k = 0; k < D; ++k) w[k] = fmaf(V[m], brow[k], w[k]);
+      for (int k = 0; k < D; ++k) w[k] = fma(V[m], brow[k], w[k]);
     }
     wave_sync();
     vb[li] = beta_i;
     va[li] = alpha_i;
     wave_sync();
-    float beta[D], alpha[D];
+    R beta[D], alpha[D];
     ld_row<D>(vb, beta);
     ld_row<D>(va, alpha);
 #pragma unroll
@@ -246,51 +272,51 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
     wave_sync();
 
     // augmented row li: [Quu_li | Qux_li],  Quu = B_k'W + R,  Qux_lc = W_cl * alpha_c
-    float aug[2 * D];
+    R aug[2 * D];
 #pragma unroll
-    for (int k = 0; k < D; ++k) aug[k] = 0.f;
+    for (int k = 0; k < D; ++k) aug[k] = R(0);
 #pragma unroll
     for (int m = 0; m < D; ++m) {
-      float wrow[D];
+      R wrow[D];
       ld_row<D>(mat + m * G::LDM, wrow);
 #pragma unroll
-      for (int k = 0; k < D; ++k) aug[k] = fmaf(Bcol[m], wrow[k], aug[k]);
+      for (int k = 0; k < D; ++k) aug[k] = fma(Bcol[m], wrow[k], aug[k]);
     }
 #pragma unroll
-    for (int k = 0; k < D; ++k) aug[k] = aug[k] * beta_i + ((k == li) ? rr_i : 0.f);
+    for (int k = 0; k < D; ++k) aug[k] = aug[k] * beta_i + ((k == li) ? rr_i : R(0));
 #pragma unroll
     for (int c = 0; c < D; ++c) aug[D + c] = mat[c * G::LDM + li] * alpha[c];
     if (STASH && t == 0) {
       float qrow[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) qrow[k] = aug[k];
+      for (int k = 0; k < D; ++k) qrow[k] = (float)aug[k];
       if (valid) st_global_row<D>(q0stash + (p * D + li) * D, qrow);
     }
 
-    float mypiv;
+    R mypiv;
     int pos;
     gauss_jordan<D, 2 * D>(aug, li, prow, mypiv, pos);
-    float x[D];  // row `pos` of X = Quu^{-1} Qux  (K = -X)
-    const float ipiv = 1.0f / mypiv;
+    R x[D];  // row `pos` of X = Quu^{-1} Qux  (K = -X)
+    const R ipiv = R(1) / mypiv;
 #pragma unroll
     for (int c = 0; c < D; ++c) x[c] = aug[D + c] * ipiv;
     if (STASH && valid) {
       float krow[D];
 #pragma unroll
-      for (int c = 0; c < D; ++c) krow[c] = -x[c];
+      for (int c = 0; c < D; ++c) krow[c] = (float)(-x[c]);
       st_global_row<D>(kstash + (((int64_t)p * T + t) * D + pos) * D, krow);
     }
     if (t == 0) {
       // u0[pos] = K_0[pos,:] . h0
-      float hv[D];
+      R hv[D];
       wave_sync();
-      vx[li] = h0[p * D + li];
+      vx[li] = (R)h0[p * D + li];
       wave_sync();
       ld_row<D>(vx, hv);
-      float s = 0.f;
+      R s = R(0);
 #pragma unroll
-      for (int c = 0; c < D; ++c) s = fmaf(x[c], hv[c], s);
-      const float u0 = -s;
+      for (int c = 0; c < D; ++c) s = fma(x[c], hv[c], s);
+      const float u0 = (float)(-s);
       if (WRITE_U && valid) u_out[p * D + pos] = u0;
       if (status != nullptr && valid && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
       break;  // V_0 is not needed
@@ -299,33 +325,32 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
     st_row<D>(mat + pos * G::LDM, x);
     wave_sync();
     // V <- alpha_i (alpha_m V_im - sum_j W_ij X_jm) + q_i q_m Q_im
-    float acc[D];
+    R acc[D];
 #pragma unroll
-    for (int m = 0; m < D; ++m) acc[m] = 0.f;
+    for (int m = 0; m < D; ++m) acc[m] = R(0);
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      float xrow[D];
+      R xrow[D];
       ld_row<D>(mat + j * G::LDM, xrow);
 #pragma unroll
-      for (int m = 0; m < D; ++m) acc[m] = fmaf(w[j], xrow[m], acc[m]);
+      for (int m = 0; m < D; ++m) acc[m] = fma(w[j], xrow[m], acc[m]);
     }
-    float qv[D];
+    R qv[D];
     vx[li] = q_i;
     wave_sync();
     ld_row<D>(vx, qv);
 #pragma unroll
     for (int m = 0; m < D; ++m)
-      V[m] = fmaf(alpha_i, fmaf(alpha[m], V[m], -acc[m]), (q_i * qv[m]) * Qrow[m]);
+      V[m] = fma(alpha_i, fma(alpha[m], V[m], -acc[m]), (q_i * qv[m]) * Qrow[m]);
     // symmetrise: V_im = (V_im + V_mi) / 2
     wave_sync();
     st_row<D>(mat + li * G::LDM, V);
     wave_sync();
 #pragma unroll
-    for (int m = 0; m < D; ++m) V[m] = 0.5f * (V[m] + mat[m * G::LDM + li]);
+    for (int m = 0; m < D; ++m) V[m] = R(0.5) * (V[m] + mat[m * G::LDM + li]);
     wave_sync();
   }
 }
-
 
 // ---------------------------------------------------------------------------
 // Backward kernel: adjoint feed-forward, closed-loop rollouts of the primal and
@@ -566,61 +591,59 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   }
 }
 
-// grad_B / grad_Q: sum the per-problem partials over the H heads of each token.
-__global__ void headsum_kernel(const float* __restrict__ part, int64_t N, int H, int DD,
-                               float* __restrict__ out, float grad_limit, int* __restrict__ status) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= N * DD) return;
-  const int64_t n = e / DD;
-  const int r = (int)(e % DD);
-  float s = 0.f;
-  for (int h = 0; h < H; ++h) s += part[(n * H + h) * DD + r];
-  out[e] = s;
-  if (status != nullptr) {
-    if (!isfinite(s)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
-    else if (fabsf(s) >= grad_limit) atomicOr(status, TTC_LQR_STATUS_LARGE);
-  }
-}
 
 // ---------------------------------------------------------------------------
-// host side
+// launch helpers (instantiated per D in ttc_lqr_d*.hip)
 // ---------------------------------------------------------------------------
 template <int D>
-static int ntok_lds_for(int H) {
+inline int ntok_lds_for(int H) {
   constexpr int PPB = Geo<D>::PPB;
   const int span = (PPB - 1) / H + 2;
   return span < PPB ? span : PPB;
 }
 
 template <int D>
-static size_t lds_bytes(int H) {
-  return sizeof(float) * ((size_t)ntok_lds_for<D>(H) * Geo<D>::MAT + (size_t)Geo<D>::PPB * Geo<D>::PER_PROB);
+inline size_t lds_bytes(int H, size_t elem = sizeof(float)) {
+  return elem * ((size_t)ntok_lds_for<D>(H) * Geo<D>::MAT + (size_t)Geo<D>::PPB * Geo<D>::PER_PROB);
 }
 
-template <int D>
-static int launch_fwd(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
-                      const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                      int T, float* u, float* kst, float* q0s, int32_t* status, hipStream_t s) {
-  if (P <= 0) return TTC_LQR_OK;
+template <int D, typename RT>
+inline void launch_fwd_t(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
+                         int T, float* u, float* kst, float* q0s, int32_t* status, hipStream_t s) {
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
-  const size_t sh = lds_bytes<D>(H);
+  const size_t sh = lds_bytes<D>(H, sizeof(RT));
   const int nt = ntok_lds_for<D>(H);
   if (kst != nullptr) {
     if (u != nullptr)
-      hipLaunchKernelGGL((lqr_fwd_kernel<D, true, true>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P, H,
-                         T, nt, u, kst, q0s, status);
-    else
-      hipLaunchKernelGGL((lqr_fwd_kernel<D, true, false>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P,
+      hipLaunchKernelGGL((lqr_fwd_kernel<D, RT, true, true>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P,
                          H, T, nt, u, kst, q0s, status);
+    else
+      hipLaunchKernelGGL((lqr_fwd_kernel<D, RT, true, false>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0,
+                         P, H, T, nt, u, kst, q0s, status);
   } else {
-    hipLaunchKernelGGL((lqr_fwd_kernel<D, false, true>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P, H,
-                       T, nt, u, kst, q0s, status);
+    hipLaunchKernelGGL((lqr_fwd_kernel<D, RT, false, true>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P,
+                       H, T, nt, u, kst, q0s, status);
   }
+}
+
+template <int D, bool HAS_FP64>
+inline int launch_fwd(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                      const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
+                      int T, float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags) {
+  if (P <= 0) return TTC_LQR_OK;
+  if (flags & TTC_LQR_FLAG_FP64_RICCATI) {
+    if constexpr (HAS_FP64)
+      launch_fwd_t<D, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, kst, q0s, status, s);
+    else
+      return TTC_LQR_EUNSUPPORTED;
+  } else
+    launch_fwd_t<D, float>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, kst, q0s, status, s);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
 template <int D>
-static int launch_bwd(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+inline int launch_bwd(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                       const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                       const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
                       float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
@@ -633,168 +656,4 @@ static int launch_bwd(const float* A, const float* B, const float* Q, const floa
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
-static int launch_headsum(const float* part, int64_t N, int H, int DD, float* out, float limit, int32_t* status,
-                          hipStream_t s) {
-  const int64_t total = N * DD;
-  if (total <= 0) return TTC_LQR_OK;
-  hipLaunchKernelGGL(headsum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, N, H, DD, out,
-                     limit, status);
-  return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
-}
-
-static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
-
-struct BwdLayout {
-  size_t kst, q0s, traj, gBp, gQp, total;
-};
-
-static BwdLayout bwd_layout(int64_t chunk_tokens, int H, int d, int T, bool with_stash) {
-  const size_t Pc = (size_t)chunk_tokens * (size_t)H;
-  BwdLayout L{};
-  size_t off = 0;
-  L.kst = off;
-  off += with_stash ? 0 : align256(Pc * (size_t)T * d * d * sizeof(float));
-  L.q0s = off;
-  off += with_stash ? 0 : align256(Pc * (size_t)d * d * sizeof(float));
-  L.traj = off;
-  off += align256(Pc * (size_t)T * d * 4 * sizeof(float));
-  L.gBp = off;
-  off += align256(Pc * (size_t)d * d * sizeof(float));
-  L.gQp = off;
-  off += align256(Pc * (size_t)d * d * sizeof(float));
-  L.total = off;
-  return L;
-}
-
 }  // namespace ttc
-
-using namespace ttc;
-
-extern "C" {
-
-const char* ttc_lqr_version(void) { return TTC_LQR_VERSION_STRING; }
-
-const char* ttc_lqr_strerror(int code) {
-  switch (code) {
-    case TTC_LQR_OK: return "ok";
-    case TTC_LQR_EINVAL: return "invalid argument (sizes, null pointer or workspace too small)";
-    case TTC_LQR_EUNSUPPORTED: return "unsupported (d, du): kernels exist for d == du in {16, 32, 64}";
-    case TTC_LQR_ELAUNCH: return "HIP kernel launch failed";
-    default: return "unknown error";
-  }
-}
-
-int ttc_lqr_supported(int32_t d, int32_t du) { return (d == du && (d == 16 || d == 32 || d == 64)) ? 1 : 0; }
-
-size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {
-  if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0 || T <= 0) return 0;
-  const size_t P = (size_t)n_tokens * (size_t)heads;
-  return sizeof(float) * P * ((size_t)T * du * d + (size_t)du * du);
-}
-
-size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
-                               int32_t with_stash) {
-  if (chunk_tokens <= 0 || heads <= 0 || d <= 0 || du != d || T <= 0) return 0;
-  return bwd_layout(chunk_tokens, heads, d, T, with_stash != 0).total;
-}
-
-int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
-                    const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
-                    int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T, float* u, float* gain_stash,
-                    float* quu0_stash, int32_t* status, void* stream) {
-  if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
-  if (!ttc_lqr_supported(d, du)) return TTC_LQR_EUNSUPPORTED;
-  if (n_tokens == 0) return TTC_LQR_OK;
-  if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !u)
-    return TTC_LQR_EINVAL;
-  if ((gain_stash == nullptr) != (quu0_stash == nullptr)) return TTC_LQR_EINVAL;
-  const int64_t P = n_tokens * heads;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (d) {
-    case 16: return launch_fwd<16>(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, gain_stash, quu0_stash, status, s);
-    case 32: return launch_fwd<32>(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, gain_stash, quu0_stash, status, s);
-    case 64: return launch_fwd<64>(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, gain_stash, quu0_stash, status, s);
-  }
-  return TTC_LQR_EUNSUPPORTED;
-}
-
-int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
-                     const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
-                     const float* d_u, int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
-                     const float* gain_stash, const float* quu0_stash, float* grad_A_diag, float* grad_B,
-                     float* grad_Q, float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A,
-                     float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0, void* workspace,
-                     size_t workspace_bytes, float grad_limit, int32_t* status, void* stream) {
-  if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
-  if (!ttc_lqr_supported(d, du)) return TTC_LQR_EUNSUPPORTED;
-  if (n_tokens == 0) return TTC_LQR_OK;
-  if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !d_u ||
-      !grad_A_diag || !grad_B || !grad_Q || !grad_R_inv || !grad_Q_f || !grad_log_gamma_A || !grad_log_gamma_B ||
-      !grad_log_gamma_Q || !grad_h0 || !workspace)
-    return TTC_LQR_EINVAL;
-  if ((gain_stash == nullptr) != (quu0_stash == nullptr)) return TTC_LQR_EINVAL;
-  const bool with_stash = gain_stash != nullptr;
-  const size_t per_token = bwd_layout(1, heads, d, T, with_stash).total;
-  if (workspace_bytes < per_token) return TTC_LQR_EINVAL;
-  // largest chunk whose layout fits (layout is monotone in the chunk size)
-  int64_t chunk = (int64_t)(workspace_bytes / per_token);
-  if (chunk > n_tokens) chunk = n_tokens;
-  while (chunk > 1 && bwd_layout(chunk, heads, d, T, with_stash).total > workspace_bytes) --chunk;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const int64_t dd = (int64_t)d * d;
-  for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
-    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
-    const int64_t p0 = n0 * heads, Pc = nc * heads;
-    const BwdLayout L = bwd_layout(nc, heads, d, T, with_stash);
-    const float* a = A_diag + p0 * d;
-    const float* b = B + n0 * dd;
-    const float* q = Q + n0 * dd;
-    const float* r = R_inv + p0 * du;
-    const float* qf = Q_f + p0 * dd;
-    const float* la = log_gamma_A + p0;
-    const float* lb = log_gamma_B + p0 * du;
-    const float* lq = log_gamma_Q + p0 * d;
-    const float* hz = h0 + p0 * d;
-    const float* dz = d_u + p0 * du;
-    float* kst;
-    float* q0s;
-    int rc = TTC_LQR_OK;
-    if (with_stash) {
-      kst = const_cast<float*>(gain_stash) + p0 * (int64_t)T * dd;
-      q0s = const_cast<float*>(quu0_stash) + p0 * dd;
-    } else {
-      kst = reinterpret_cast<float*>(ws + L.kst);
-      q0s = reinterpret_cast<float*>(ws + L.q0s);
-      switch (d) {
-        case 16: rc = launch_fwd<16>(a, b, q, r, qf, la, lb, lq, hz, Pc, heads, T, nullptr, kst, q0s, nullptr, s); break;
-        case 32: rc = launch_fwd<32>(a, b, q, r, qf, la, lb, lq, hz, Pc, heads, T, nullptr, kst, q0s, nullptr, s); break;
-        case 64: rc = launch_fwd<64>(a, b, q, r, qf, la, lb, lq, hz, Pc, heads, T, nullptr, kst, q0s, nullptr, s); break;
-      }
-      if (rc != TTC_LQR_OK) return rc;
-    }
-    float4* traj = reinterpret_cast<float4*>(ws + L.traj);
-    float* gBp = reinterpret_cast<float*>(ws + L.gBp);
-    float* gQp = reinterpret_cast<float*>(ws + L.gQp);
-    float* gA = grad_A_diag + p0 * d;
-    float* gR = grad_R_inv + p0 * du;
-    float* gQf = grad_Q_f + p0 * dd;
-    float* glA = grad_log_gamma_A + p0;
-    float* glB = grad_log_gamma_B + p0 * du;
-    float* glQ = grad_log_gamma_Q + p0 * d;
-    float* gh = grad_h0 + p0 * d;
-    switch (d) {
-      case 16: rc = launch_bwd<16>(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, heads, T, traj, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, status, s); break;
-      case 32: rc = launch_bwd<32>(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, heads, T, traj, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, status, s); break;
-      case 64: rc = launch_bwd<64>(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, heads, T, traj, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, status, s); break;
-    }
-    if (rc != TTC_LQR_OK) return rc;
-    rc = launch_headsum(gBp, nc, heads, (int)dd, grad_B + n0 * dd, grad_limit, status, s);
-    if (rc != TTC_LQR_OK) return rc;
-    rc = launch_headsum(gQp, nc, heads, (int)dd, grad_Q + n0 * dd, grad_limit, status, s);
-    if (rc != TTC_LQR_OK) return rc;
-  }
-  return TTC_LQR_OK;
-}
-
-}  // extern "C"

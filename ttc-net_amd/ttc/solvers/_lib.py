@@ -10,7 +10,9 @@ from __future__ import annotations
 import ctypes
 import os
 
-__all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check"]
+__all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI"]
+
+FLAG_FP64_RICCATI = 1  # TTC_LQR_FLAG_FP64_RICCATI
 
 LIB_NAME = "libttc_lqr.so"
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -40,14 +42,16 @@ def _load():
     L.ttc_lqr_strerror.argtypes = [ctypes.c_int]
     L.ttc_lqr_supported.restype = ctypes.c_int
     L.ttc_lqr_supported.argtypes = [i32, i32]
+    L.ttc_lqr_supported_flags.restype = ctypes.c_int
+    L.ttc_lqr_supported_flags.argtypes = [i32, i32, i32]
     L.ttc_lqr_stash_bytes.restype = sz
     L.ttc_lqr_stash_bytes.argtypes = [i64, i32, i32, i32, i32]
     L.ttc_lqr_workspace_bytes.restype = sz
     L.ttc_lqr_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32]
     L.ttc_lqr_forward.restype = ctypes.c_int
-    L.ttc_lqr_forward.argtypes = [f32p] * 9 + [i64, i32, i32, i32, i32] + [f32p, f32p, f32p, f32p, ctypes.c_void_p]
+    L.ttc_lqr_forward.argtypes = [f32p] * 9 + [i64, i32, i32, i32, i32, i32] + [f32p, f32p, f32p, f32p, ctypes.c_void_p]
     L.ttc_lqr_backward.restype = ctypes.c_int
-    L.ttc_lqr_backward.argtypes = ([f32p] * 10 + [i64, i32, i32, i32, i32] + [f32p, f32p] + [f32p] * 9
+    L.ttc_lqr_backward.argtypes = ([f32p] * 10 + [i64, i32, i32, i32, i32, i32] + [f32p, f32p] + [f32p] * 9
                                    + [ctypes.c_void_p, sz, ctypes.c_float, f32p, ctypes.c_void_p])
     return L
 

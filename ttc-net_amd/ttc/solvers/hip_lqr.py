@@ -17,10 +17,16 @@ Differences from the reference, by design:
   ``u^2/2``), which leaves the solution unchanged.
 * the backward recomputes the feedback gains in bounded-memory chunks unless the
   forward kept them ("stash"), see ``TTC_LQR_STASH`` below.
+* ``precision``: the Riccati sweep (the feedback gains) runs in fp32 or fp64.
+  ``"auto"`` (default) picks fp64 for horizons ``T >= FP64_HORIZON`` (512): on long,
+  barely discounted horizons the value matrix reaches ~1e17 and fp32 rounding
+  corrupts the gains (the reference's own fp32 solvers lose the gradients
+  entirely there).  Everything else (rollouts, costates, gradients) is fp32.
 
 Environment knobs:
 ``TTC_LQR_STASH`` = ``auto`` (default: keep the gains from the forward when they
-fit in ``TTC_LQR_STASH_MAX_BYTES``, default 8 GiB) | ``always`` | ``never``.
+fit in half of the device memory free at forward time, capped by
+``TTC_LQR_STASH_MAX_BYTES`` if set) | ``always`` | ``never``.
 ``TTC_LQR_WORKSPACE_BYTES``: backward workspace per call (default 4 GiB).
 """
 from __future__ import annotations
@@ -30,11 +36,12 @@ import os
 
 import torch
 
-from ._lib import lib, check
+from ._lib import lib, check, FLAG_FP64_RICCATI
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "padded_dim", "SUPPORTED_DIMS"]
 
 SUPPORTED_DIMS = (16, 32, 64)
+FP64_HORIZON = 512
 _FWD_MSG = "Numerical instability detected during fused LQR forward recurrence."
 _BWD_MSG = "Numerical instability detected during fused LQR backward pass."
 
@@ -70,6 +77,25 @@ def _pad_inputs(ins, d, du, Dp):
     return [t.contiguous() for t in (A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, h0)]
 
 
+def riccati_flags(precision: str, T: int, Dp: int) -> int:
+    """Kernel flags for the requested Riccati arithmetic (fp64 kernels exist for d <= 32)."""
+    assert precision in ("fp32", "fp64", "auto"), f"unknown precision {precision}"
+    if precision == "fp64":
+        assert lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_RICCATI), \
+            f"fp64 Riccati kernels exist for state dims up to 32, got {Dp}"
+        return FLAG_FP64_RICCATI
+    if precision == "auto" and T >= FP64_HORIZON and lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_RICCATI):
+        return FLAG_FP64_RICCATI
+    return 0
+
+
+def _stash_budget(device) -> int:
+    free, _total = torch.cuda.mem_get_info(device)
+    budget = free // 2
+    cap = os.environ.get("TTC_LQR_STASH_MAX_BYTES")
+    return min(budget, int(float(cap))) if cap else budget
+
+
 def _stream_handle(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -78,7 +104,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T: int,
-                grad_limit: float = 1e6, stash: str | None = None):
+                grad_limit: float = 1e6, stash: str | None = None, precision: str = "auto"):
         ins = [A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0]
         assert all(x.is_cuda for x in ins), "hip LQR solver inputs must be on a GPU"
         bs, nh, d = A_diag.shape
@@ -97,6 +123,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
         dev = A_diag.device
         out_dtype = Q.dtype
         Dp = padded_dim(d, du)
+        flags = riccati_flags(precision, T, Dp)
         f32 = [x.detach().to(torch.float32).contiguous() for x in ins]
         f32 = _pad_inputs(f32, d, du, Dp)
         P = bs * nh
@@ -106,15 +133,14 @@ class HipLQRSolveFunc(torch.autograd.Function):
         policy = stash or os.environ.get("TTC_LQR_STASH", "auto")
         need_grad = any(ctx.needs_input_grad[:9])
         stash_bytes = lib.ttc_lqr_stash_bytes(bs, nh, Dp, Dp, T)
-        keep = need_grad and bs > 0 and (
-            policy == "always" or (policy == "auto" and stash_bytes <= _env_bytes("TTC_LQR_STASH_MAX_BYTES", 8 << 30)))
+        keep = need_grad and bs > 0 and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev)))
         if keep:
             st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32)
             kst, q0s = st[: P * T * Dp * Dp], st[P * T * Dp * Dp:]
         else:
             st = kst = q0s = None
         with torch.cuda.device(dev):
-            rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, u.data_ptr(),
+            rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, flags, u.data_ptr(),
                                      None if kst is None else kst.data_ptr(),
                                      None if q0s is None else q0s.data_ptr(),
                                      status.data_ptr(), _stream_handle(dev))
@@ -122,12 +148,12 @@ class HipLQRSolveFunc(torch.autograd.Function):
         if int(status.item()) != 0:
             raise RuntimeError(_FWD_MSG)
         ctx.save_for_backward(*f32, *( [st] if st is not None else []))
-        ctx.meta = (bs, nh, d, du, Dp, T, float(grad_limit), st is not None, [x.dtype for x in ins])
+        ctx.meta = (bs, nh, d, du, Dp, T, float(grad_limit), st is not None, [x.dtype for x in ins], flags)
         return u[..., :du].to(out_dtype)
 
     @staticmethod
     def backward(ctx, d_u):
-        bs, nh, d, du, Dp, T, grad_limit, has_stash, dtypes = ctx.meta
+        bs, nh, d, du, Dp, T, grad_limit, has_stash, dtypes, flags = ctx.meta
         saved = ctx.saved_tensors
         f32 = list(saved[:9])
         st = saved[9] if has_stash else None
@@ -155,7 +181,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         with torch.cuda.device(dev):
             rc = lib.ttc_lqr_backward(
-                *[t.data_ptr() for t in f32], dU.data_ptr(), bs, nh, Dp, Dp, T,
+                *[t.data_ptr() for t in f32], dU.data_ptr(), bs, nh, Dp, Dp, T, flags,
                 None if kst is None else kst.data_ptr(), None if q0s is None else q0s.data_ptr(),
                 g["A"].data_ptr(), g["B"].data_ptr(), g["Q"].data_ptr(), g["R"].data_ptr(), g["Qf"].data_ptr(),
                 g["lA"].data_ptr(), g["lB"].data_ptr(), g["lQ"].data_ptr(), g["h0"].data_ptr(),
@@ -166,19 +192,20 @@ class HipLQRSolveFunc(torch.autograd.Function):
         out = (g["A"][..., :d], g["B"][:, :d, :du], g["Q"][:, :d, :d], g["R"][..., :du], g["Qf"][:, :, :d, :d],
                g["lA"], g["lB"][..., :du], g["lQ"][..., :d], g["h0"][..., :d])
         out = tuple(o.to(dt) if need else None for o, dt, need in zip(out, dtypes, ctx.needs_input_grad[:9]))
-        return out + (None, None, None)
+        return out + (None, None, None, None)
 
 
 def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_diag: torch.Tensor,
                   Q_f: torch.Tensor, log_gamma_A: torch.Tensor, log_gamma_B: torch.Tensor,
                   log_gamma_Q: torch.Tensor, h0: torch.Tensor, T: int, grad_limit: float = 1e6,
-                  stash: str | None = None) -> torch.Tensor:
+                  stash: str | None = None, precision: str = "auto") -> torch.Tensor:
     """First optimal action ``u [N,H,du]`` of every (token, head) LQR problem.
 
     Drop-in for the reference ``fused_lqr_solve`` (``fused_lqr.py:294-304``).
     ``grad_limit``: the backward raises when a gradient reaches it (the reference's
     1e6 guard, ``fused_lqr.py:245``); ``math.inf`` disables the magnitude check.
     ``stash``: ``"auto" | "always" | "never"`` overrides ``TTC_LQR_STASH``.
+    ``precision``: ``"auto" | "fp32" | "fp64"`` arithmetic of the Riccati sweep.
     """
     return HipLQRSolveFunc.apply(A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T,
-                                 grad_limit, stash)
+                                 grad_limit, stash, precision)
