@@ -52,6 +52,10 @@ extern "C" {
  * for long, barely-discounted horizons (e.g. T = 1024 with log-normal inputs),
  * where fp32 rounding of V ~ 1e17 corrupts the gains. */
 #define TTC_LQR_FLAG_FP64_RICCATI 1
+/* TTC_LQR_FLAG_ROW_KERNEL selects the row-layout (vector-ALU only) fp32 kernel where a
+ * matrix-core kernel exists (d = 16).  Results agree to fp32 rounding; it serves as an
+ * independent cross-check and as a fallback. */
+#define TTC_LQR_FLAG_ROW_KERNEL 2
 
 /* Library version string. */
 const char* ttc_lqr_version(void);
@@ -62,7 +66,8 @@ const char* ttc_lqr_strerror(int code);
 /* 1 if the kernels were compiled for this (d, du), else 0. */
 int ttc_lqr_supported(int32_t d, int32_t du);
 
-/* 1 if (d, du) is supported with these `flags` (fp64 Riccati: d <= 32), else 0. */
+/* 1 if (d, du) is supported with these `flags` (fp64 Riccati: d <= 32), else 0.
+ * TTC_LQR_FLAG_ROW_KERNEL is accepted for every supported (d, du). */
 int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags);
 
 /* Bytes of the optional gain stash written by ttc_lqr_forward for the backward:

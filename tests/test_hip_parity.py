@@ -71,7 +71,7 @@ def test_config1_layer_slice(stash):
     check_case("cfg1", layer_solver_inputs(1, x), c["T"], stash=stash)
 
 
-@pytest.mark.parametrize("precision", ["fp32", "fp64"])
+@pytest.mark.parametrize("precision", ["fp32", "fp32-row", "fp64"])
 def test_config2_layer_slice(precision):
     c = CONFIGS[2]
     x = make_x(2, n_tokens=64, seed=1)
@@ -107,6 +107,27 @@ def test_padding_odd_dims_and_ragged_problem_count():
     lgB = -torch.nn.functional.softplus(torch.randn(N, H, du, generator=g)) - 0.3
     ins = [ins[0], B, ins[2], R_inv, ins[4], ins[5], lgB, ins[7], ins[8]]
     check_case("pad", ins, T)
+
+
+def _indefinite_terminal_inputs(s, seed=2):
+    """Problem 1 of 8 gets Q_f = -s I with a strong, barely discounted B: Quu turns
+    indefinite (nonsingular), so the matrix-core kernel's Cholesky guard fires for the
+    wave holding problems 0-3 and that wave finishes on the pivoted row-layout sweep,
+    while problems 4-7 stay on the matrix cores.  s = 2: indefinite from the last step
+    (t = T-1) on; s = 0.2: positive definite until t = 0 (a mid-horizon switch)."""
+    ins = bench_solver_inputs(2, 4, 16, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    B = torch.randn(2, 16, 16, generator=g) * 0.25
+    lgB = torch.full((2, 4, 16), -0.01)
+    Qf = ins[4].clone()
+    Qf[0, 1] = -s * torch.eye(16)
+    return [ins[0], B, ins[2], ins[3], Qf, ins[5], lgB, ins[7], ins[8]]
+
+
+@pytest.mark.parametrize("s", [2.0, 0.2])
+@pytest.mark.parametrize("stash", ["always", "never"])
+def test_indefinite_Quu_switches_to_pivoted_sweep(s, stash):
+    check_case(f"indef{s}", _indefinite_terminal_inputs(s), 6, stash=stash, precision="fp32")
 
 
 def test_T1_closed_form():

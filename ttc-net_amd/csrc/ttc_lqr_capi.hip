@@ -83,7 +83,7 @@ int ttc_lqr_supported(int32_t d, int32_t du) { return (d == du && (d == 16 || d 
 int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if (!ttc_lqr_supported(d, du)) return 0;
   if ((flags & TTC_LQR_FLAG_FP64_RICCATI) && d > 32) return 0;
-  return (flags & ~TTC_LQR_FLAG_FP64_RICCATI) ? 0 : 1;
+  return (flags & ~(TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL)) ? 0 : 1;
 }
 
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {

@@ -7,6 +7,9 @@ namespace ttc {
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags);
+int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
+                        int T, float* u, float* kst, float* q0s, int32_t* status, hipStream_t s);
 int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,

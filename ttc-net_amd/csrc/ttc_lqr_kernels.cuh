@@ -182,41 +182,20 @@ __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& my
 }
 
 // ---------------------------------------------------------------------------
-// Forward kernel: Riccati sweep, u0, optional gain stash.  R is the arithmetic
-// type of the sweep (float, or double for long ill-conditioned horizons);
-// inputs, u and the stash are fp32 in HBM.
+// Row-layout Riccati sweep from step t_start down to 0: u0, optional gain stash.
+// R is the arithmetic type of the sweep (float, or double for long ill-conditioned
+// horizons); inputs, u and the stash are fp32 in HBM.  The D lanes of a problem
+// enter with V = V_{t_start+1} (lane li holds row li); Bs holds the problem's B
+// (row stride Geo<D>::LDM) and S is the problem's Geo<D>::PER_PROB-element scratch.
 // ---------------------------------------------------------------------------
 template <int D, typename R, bool STASH, bool WRITE_U>
-__global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
-    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
-    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
-    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
-    int64_t P, int H, int T, int ntok_lds, float* __restrict__ u_out, float* __restrict__ kstash,
+__device__ __forceinline__ void rpl_sweep(
+    const float* __restrict__ A_diag, const float* __restrict__ Qg, const float* __restrict__ Rinv,
+    const float* __restrict__ lgA, const float* __restrict__ lgB, const float* __restrict__ lgQ,
+    const float* __restrict__ h0, const R* Bs, R* S, int li, int64_t p, bool valid, int64_t n, int T,
+    int t_start, R (&V)[D], float* __restrict__ u_out, float* __restrict__ kstash,
     float* __restrict__ q0stash, int* __restrict__ status) {
   using G = Geo<D>;
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  R* smem = reinterpret_cast<R*>(smem_raw);
-  const int li = threadIdx.x % D;
-  const int pb = threadIdx.x / D;
-  const int64_t p0 = (int64_t)blockIdx.x * G::PPB;
-  int64_t p = p0 + pb;
-  const bool valid = p < P;
-  if (!valid) p = P - 1;  // idle lanes recompute a real problem, never store
-  const int64_t n = p / H;
-  const int64_t n0 = p0 / H;
-
-  // stage the block's token-shared B matrices in LDS
-  {
-    const int64_t plast = (p0 + G::PPB - 1 < P) ? (p0 + G::PPB - 1) : (P - 1);
-    const int ntok = (int)(plast / H - n0 + 1);
-    for (int e = threadIdx.x; e < ntok * D * D; e += G::THREADS) {
-      const int tk = e / (D * D), rem = e % (D * D);
-      smem[(tk * D + rem / D) * G::LDM + rem % D] = (R)Bg[(n0 + tk) * D * D + rem];
-    }
-  }
-  __syncthreads();
-  const R* Bs = smem + (int)(n - n0) * G::MAT;
-  R* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
   R* mat = S;
   R* vb = S + G::MAT;
   R* va = vb + D;
@@ -229,19 +208,17 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
   const R lgQ_i = lgQ[p * D + li];
   const R lgA_p = lgA[p];
 
-  R V[D], Bcol[D], Qrow[D];
+  R Bcol[D], Qrow[D];
   {
-    const float* qf = Qf + p * D * D;
     const float* qg = Qg + n * D * D;
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      V[c] = R(0.5) * ((R)qf[li * D + c] + (R)qf[c * D + li]);
       Qrow[c] = R(0.5) * ((R)qg[li * D + c] + (R)qg[c * D + li]);
       Bcol[c] = Bs[c * G::LDM + li];
     }
   }
 
-  for (int t = T - 1; t >= 0; --t) {
+  for (int t = t_start; t >= 0; --t) {
     const R tp1 = (R)(t + 1);
     const R eA = exp(lgA_p * tp1);
     const R beta_i = exp(lgB_i * tp1);
@@ -350,6 +327,51 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
     for (int m = 0; m < D; ++m) V[m] = R(0.5) * (V[m] + mat[m * G::LDM + li]);
     wave_sync();
   }
+}
+
+// ---------------------------------------------------------------------------
+// Forward kernel (row layout): stage B, V_T = sym(Q_f), full sweep.
+// ---------------------------------------------------------------------------
+template <int D, typename R, bool STASH, bool WRITE_U>
+__global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    int64_t P, int H, int T, int ntok_lds, float* __restrict__ u_out, float* __restrict__ kstash,
+    float* __restrict__ q0stash, int* __restrict__ status) {
+  using G = Geo<D>;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  R* smem = reinterpret_cast<R*>(smem_raw);
+  const int li = threadIdx.x % D;
+  const int pb = threadIdx.x / D;
+  const int64_t p0 = (int64_t)blockIdx.x * G::PPB;
+  int64_t p = p0 + pb;
+  const bool valid = p < P;
+  if (!valid) p = P - 1;  // idle lanes recompute a real problem, never store
+  const int64_t n = p / H;
+  const int64_t n0 = p0 / H;
+
+  // stage the block's token-shared B matrices in LDS
+  {
+    const int64_t plast = (p0 + G::PPB - 1 < P) ? (p0 + G::PPB - 1) : (P - 1);
+    const int ntok = (int)(plast / H - n0 + 1);
+    for (int e = threadIdx.x; e < ntok * D * D; e += G::THREADS) {
+      const int tk = e / (D * D), rem = e % (D * D);
+      smem[(tk * D + rem / D) * G::LDM + rem % D] = (R)Bg[(n0 + tk) * D * D + rem];
+    }
+  }
+  __syncthreads();
+  const R* Bs = smem + (int)(n - n0) * G::MAT;
+  R* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
+
+  R V[D];
+  {
+    const float* qf = Qf + p * D * D;
+#pragma unroll
+    for (int c = 0; c < D; ++c) V[c] = R(0.5) * ((R)qf[li * D + c] + (R)qf[c * D + li]);
+  }
+  rpl_sweep<D, R, STASH, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, Bs, S, li, p, valid, n, T, T - 1, V,
+                                  u_out, kstash, q0stash, status);
 }
 
 // ---------------------------------------------------------------------------

@@ -10,9 +10,10 @@ from __future__ import annotations
 import ctypes
 import os
 
-__all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI"]
+__all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI", "FLAG_ROW_KERNEL"]
 
 FLAG_FP64_RICCATI = 1  # TTC_LQR_FLAG_FP64_RICCATI
+FLAG_ROW_KERNEL = 2    # TTC_LQR_FLAG_ROW_KERNEL
 
 LIB_NAME = "libttc_lqr.so"
 _HERE = os.path.dirname(os.path.abspath(__file__))

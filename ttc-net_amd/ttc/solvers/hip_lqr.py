@@ -22,6 +22,8 @@ Differences from the reference, by design:
   barely discounted horizons the value matrix reaches ~1e17 and fp32 rounding
   corrupts the gains (the reference's own fp32 solvers lose the gradients
   entirely there).  Everything else (rollouts, costates, gradients) is fp32.
+  For d = 16 the fp32 sweep runs on the matrix cores (MFMA); ``"fp32-row"`` selects
+  the vector-ALU row-layout kernel instead.
 
 Environment knobs:
 ``TTC_LQR_STASH`` = ``auto`` (default: keep the gains from the forward when they
@@ -36,7 +38,7 @@ import os
 
 import torch
 
-from ._lib import lib, check, FLAG_FP64_RICCATI
+from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "padded_dim", "SUPPORTED_DIMS"]
 
@@ -78,8 +80,16 @@ def _pad_inputs(ins, d, du, Dp):
 
 
 def riccati_flags(precision: str, T: int, Dp: int) -> int:
-    """Kernel flags for the requested Riccati arithmetic (fp64 kernels exist for d <= 32)."""
-    assert precision in ("fp32", "fp64", "auto"), f"unknown precision {precision}"
+    """Kernel flags for the requested Riccati arithmetic (fp64 kernels exist for d <= 32).
+
+    ``"fp32"``: the fastest fp32 kernel (matrix cores where one exists, d = 16);
+    ``"fp32-row"``: the row-layout fp32 kernel (vector ALU only) -- an independent
+    cross-check of the matrix-core kernel; ``"fp64"``: fp64 sweep; ``"auto"``: fp64
+    for T >= FP64_HORIZON where available, else fp32.
+    """
+    assert precision in ("fp32", "fp32-row", "fp64", "auto"), f"unknown precision {precision}"
+    if precision == "fp32-row":
+        return FLAG_ROW_KERNEL
     if precision == "fp64":
         assert lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_RICCATI), \
             f"fp64 Riccati kernels exist for state dims up to 32, got {Dp}"
@@ -205,7 +215,8 @@ def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_
     ``grad_limit``: the backward raises when a gradient reaches it (the reference's
     1e6 guard, ``fused_lqr.py:245``); ``math.inf`` disables the magnitude check.
     ``stash``: ``"auto" | "always" | "never"`` overrides ``TTC_LQR_STASH``.
-    ``precision``: ``"auto" | "fp32" | "fp64"`` arithmetic of the Riccati sweep.
+    ``precision``: ``"auto" | "fp32" | "fp32-row" | "fp64"`` arithmetic (and, for
+    ``"fp32-row"``, kernel) of the Riccati sweep; see ``riccati_flags``.
     """
     return HipLQRSolveFunc.apply(A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T,
                                  grad_limit, stash, precision)
