@@ -37,6 +37,9 @@ PEAK_HBM = 8.0e12
 CONFIGS = {
     2: dict(in_dim=32, out_dim=32, h_dim=16, num_heads=8, b_rank=16, q_rank=16, T=64, x_shape=(16, 2048, 8, 32)),
     3: dict(in_dim=64, out_dim=64, h_dim=64, num_heads=16, b_rank=32, q_rank=32, T=128, x_shape=(8, 4096, 16, 64)),
+    # x stored bf16, N(0,1) * 0.02 (post-norm activations); the solver computes in fp32
+    4: dict(in_dim=64, out_dim=64, h_dim=32, num_heads=32, b_rank=32, q_rank=32, T=256, x_shape=(4, 8192, 32, 64),
+            x_scale=0.02, x_bf16=True),
 }
 
 
@@ -134,7 +137,9 @@ def main():
                      solver_impl="hip").to(dev)
     g = torch.Generator(device=dev).manual_seed(0)
     xshape = c["x_shape"] if args.tokens == 0 else (args.tokens, c["in_dim"])
-    x = torch.randn(xshape, generator=g, device=dev)
+    x = torch.randn(xshape, generator=g, device=dev) * c.get("x_scale", 1.0)
+    if c.get("x_bf16"):
+        x = x.to(torch.bfloat16).float()
     T, H, d = c["T"], c["num_heads"], c["h_dim"]
     with torch.no_grad():
         ins = [t.float().contiguous() for t in layer.solver_inputs(x)]

@@ -25,6 +25,8 @@
 // Gauss-Jordan on [Quu | Qux], rpl_sweep).  Keeping the two phases apart keeps their
 // register footprints from adding up.
 #pragma once
+#include <utility>
+
 #include "ttc_lqr_kernels.cuh"
 
 namespace ttc {
@@ -52,6 +54,22 @@ template <int N>
 __device__ __forceinline__ float ror16f(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + N, 0xF, 0xF, false));
 }
+// Lane K of each 16-lane row to the whole row (DPP row_newbcast).
+template <int K>
+__device__ __forceinline__ float bcast16(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + K, 0xF, 0xF, false));
+}
+
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(std::integral_constant<int, 0>) ... f(std::integral_constant<int, N-1>), in order.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 __device__ __forceinline__ float row16_min(float v) {
   v = fminf(v, ror16f<8>(v));
   v = fminf(v, ror16f<4>(v));
@@ -138,10 +156,11 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
     rrc[q] = 1.0f / Rinv[pid[q] * 16 + c];
   }
 
-  int t_fb = -1;  // step at which the wave switched to the row-layout sweep
-  for (int t = T - 1; t >= 0; --t) {
-    const bool last = (t == 0);
-    const bool need_k = STASH || last;  // wave-uniform
+  // One Riccati step; NEED_K: also form the gains K_t (stored steps, and t = 0 for u0).
+  // Returns false when the Cholesky guard fired (nothing of the step was kept).
+  auto step = [&](auto need_k_c, const int t) -> bool {
+    constexpr bool NEED_K = decltype(need_k_c)::value;
+    const bool last = NEED_K && t == 0;
     const float tp1 = (float)(t + 1);
     const float my_beta = expf(lgB_c * tp1);
     const float my_alpha = fmaf(a_c, expf(lgA_o * tp1), 1.0f);
@@ -189,56 +208,45 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
       for (int k = 0; k < 16; ++k) wr[k] *= be[k];
     }
     if (STASH && last && own_valid) st_global_row<16>(q0stash + (po * 16 + c) * 16, qr);
+    if constexpr (NEED_K) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) ir[k] = (k == c) ? 1.0f : 0.0f;
+      for (int k = 0; k < 16; ++k) ir[k] = (k == c) ? 1.0f : 0.0f;
+    }
     bool bad = false;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      if (c == k) {
-#pragma unroll
-        for (int m = (k & ~3); m < 16; m += 4) V16<float>::st(vpr + m, qr + m);
-      }
-      wave_sync();
-      float pr[16];
-#pragma unroll
-      for (int m = (k & ~3); m < 16; m += 4) V16<float>::ld(vpr + m, pr + m);
-      const float piv = pr[k];
+    static_for<16>([&](auto kc) {
+      constexpr int k = decltype(kc)::value;
+      // row k of my problem's trailing matrix, broadcast from lane (g, k) by DPP
+      const float piv = bcast16<k>(qr[k]);
       bad |= !(piv >= piv_floor);  // also catches NaN
       const float rs = rsqrtf(fmaxf(piv, 1e-30f));
       const float ip = rs * rs;
       const float fq = qr[k] * ip;
       const float fw = wr[k] * ip;
+      const float fi = NEED_K ? ir[k] * ip : 0.f;
       wr[k] *= rs;  // M[c][k]
+      if constexpr (NEED_K) ir[k] *= rs;  // U[c][k]
 #pragma unroll
       for (int m = k + 1; m < 16; ++m) {
-        qr[m] = fmaf(-fq, pr[m], qr[m]);
-        wr[m] = fmaf(-fw, pr[m], wr[m]);
-      }
-      if (need_k) {
-        const float fi = ir[k] * ip;
-        ir[k] *= rs;  // U[c][k]
-#pragma unroll
-        for (int m = k + 1; m < 16; ++m) ir[m] = fmaf(-fi, pr[m], ir[m]);
-        pin_row(ir);
+        const float pm = bcast16<k>(qr[m]);
+        qr[m] = fmaf(-fq, pm, qr[m]);
+        wr[m] = fmaf(-fw, pm, wr[m]);
+        if constexpr (NEED_K) ir[m] = fmaf(-fi, pm, ir[m]);
       }
       pin_row(wr);
-      wave_sync();
-    }
-    if (__any(bad)) {
-      t_fb = t;
-      break;
-    }
+      if constexpr (NEED_K) pin_row(ir);
+    });
+    if (__any(bad)) return false;
     {
       // ---- M rows -> tile A, U rows -> tile B; S = M M', K = -U M' diag(a) -------------
       st_row<16>(own + c * M16::LD, wr);
-      if (need_k) st_row<16>(own + M16::OFF_B + c * M16::LD, ir);
+      if constexpr (NEED_K) st_row<16>(own + M16::OFF_B + c * M16::LD, ir);
       wave_sync();
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const v4f m4 = ld4(buf[q] + c * M16::LD + 4 * g);  // M[c][4g+s]
         const float* av = buf[q] + M16::OFF_VEC + 16;
         const float acol = av[c];
-        if (need_k) {
+        if constexpr (NEED_K) {
           const v4f u4 = ld4(buf[q] + M16::OFF_B + c * M16::LD + 4 * g);  // U[c][4g+s]
           v4f kt = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -277,7 +285,16 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
           Vc[q][r] = fmaf(arow[r] * acol, Vc[q][r] - S[r], (qrow4[r] * qcol) * Qc[q][r]);
       }
       wave_sync();
-      if (last) break;
+    }
+    return true;
+  };
+
+  int t_fb = -1;  // step at which the wave switched to the row-layout sweep
+  for (int t = T - 1; t >= 0; --t) {
+    const bool ok = (STASH || t == 0) ? step(std::true_type{}, t) : step(std::false_type{}, t);
+    if (!ok) {
+      t_fb = t;
+      break;
     }
   }
 

@@ -27,7 +27,8 @@ Differences from the reference, by design:
 
 Environment knobs:
 ``TTC_LQR_STASH`` = ``auto`` (default: keep the gains from the forward when they
-fit in half of the device memory free at forward time, capped by
+fit in half of the device memory free at forward time (free on the device plus
+held unallocated by torch's caching allocator), capped by
 ``TTC_LQR_STASH_MAX_BYTES`` if set) | ``always`` | ``never``.
 ``TTC_LQR_WORKSPACE_BYTES``: backward workspace per call (default 4 GiB).
 """
@@ -100,8 +101,11 @@ def riccati_flags(precision: str, T: int, Dp: int) -> int:
 
 
 def _stash_budget(device) -> int:
+    """Half of the memory available to new tensors: free on the device plus what torch's
+    caching allocator holds unallocated (e.g. the previous step's freed stash)."""
     free, _total = torch.cuda.mem_get_info(device)
-    budget = free // 2
+    cached = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+    budget = (free + max(cached, 0)) // 2
     cap = os.environ.get("TTC_LQR_STASH_MAX_BYTES")
     return min(budget, int(float(cap))) if cap else budget
 
