@@ -18,8 +18,9 @@
  *   - The kernels implement d == du in {16, 32, 64}; other sizes are padded by
  *     the caller (zero state rows / unit-cost dummy controls leave the solution
  *     unchanged).  Anything else returns TTC_LQR_EUNSUPPORTED.
- *   - Nothing here allocates device memory, throws, or synchronises the device.
- *     All work is enqueued on `stream` (a hipStream_t, NULL = default stream).
+ *   - Nothing here allocates device memory or throws.  All work is enqueued on
+ *     `stream` (a hipStream_t, NULL = default stream); only ttc_lqr_backward
+ *     synchronises it (once per token chunk, to size its fallback).
  *   - `status` (device int32, caller-zeroed, may be NULL) receives bit flags:
  *     TTC_LQR_STATUS_NONFINITE if any output is NaN/Inf, TTC_LQR_STATUS_LARGE if
  *     a gradient has |g| >= grad_limit.  The caller reads it after the stream
@@ -56,6 +57,15 @@ extern "C" {
  * matrix-core kernel exists (d = 16).  Results agree to fp32 rounding; it serves as an
  * independent cross-check and as a fallback. */
 #define TTC_LQR_FLAG_ROW_KERNEL 2
+/* TTC_LQR_FLAG_STABLE_BWD makes ttc_lqr_backward take the stable path for every problem
+ * (feedback gains recomputed and stored per step, closed-loop costates) instead of the
+ * certified Hamiltonian rollout.  Same results to fp32 rounding; slower. */
+#define TTC_LQR_FLAG_STABLE_BWD 4
+
+/* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
+ * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds
+ * for the primal and the adjoint trajectory and every gradient is finite. */
+#define TTC_LQR_CERT_TOL 1e-5f
 
 /* Library version string. */
 const char* ttc_lqr_version(void);
@@ -67,48 +77,57 @@ const char* ttc_lqr_strerror(int code);
 int ttc_lqr_supported(int32_t d, int32_t du);
 
 /* 1 if (d, du) is supported with these `flags` (fp64 Riccati: d <= 32), else 0.
- * TTC_LQR_FLAG_ROW_KERNEL is accepted for every supported (d, du). */
+ * TTC_LQR_FLAG_ROW_KERNEL and TTC_LQR_FLAG_STABLE_BWD are accepted for every supported (d, du). */
 int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags);
 
-/* Bytes of the optional gain stash written by ttc_lqr_forward for the backward:
- * per problem T*d*du gain floats plus du*du floats of the step-0 control Hessian. */
+/* Bytes of the stash ttc_lqr_forward can leave for ttc_lqr_backward: per problem the
+ * value matrix V_1 (d*d floats, the cost-to-go Hessian at step 1) and the step-0 control
+ * Hessian Quu_0 (du*du floats).  `T` is accepted for signature stability (unused). */
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T);
 
 /* Workspace bytes ttc_lqr_backward needs to process `chunk_tokens` tokens per pass
  * (it loops over the tokens in chunks of that size).  `with_stash` != 0 when the
- * forward stash is passed to the backward (then the gains are not recomputed). */
+ * forward's stash is passed to the backward (then V_1 / Quu_0 are not recomputed).
+ * Includes a fixed-size region (<= 256 MiB) for problems the certificate rejects. */
 size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
                                int32_t with_stash);
 
 /* Forward: u = first optimal action [N,H,du] of every problem.
  * Replaces fused_lqr_layer_fwd (ttc/solvers/fused_lqr.py:18-146).
- * gain_stash / quu0_stash: NULL, or ttc_lqr_stash_bytes() of device memory split as
- *   gain_stash [P,T,du,d] (feedback gains K_t, row-major) and quu0_stash [P,du,du].
- * Pass them to ttc_lqr_backward to skip the gain recomputation. */
+ * stash: NULL, or ttc_lqr_stash_bytes() of device memory, laid out as
+ *   V_1 [P,d,d] (row-major) followed by Quu_0 [P,du,du];
+ * pass it to ttc_lqr_backward to skip their recomputation (the reference keeps
+ * lam0 / LU / Y3 for the same purpose, fused_lqr.py:272). */
 int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const float* R_inv,
                     const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
                     const float* log_gamma_Q, const float* h0, int64_t n_tokens, int32_t heads,
-                    int32_t d, int32_t du, int32_t T, int32_t flags, float* u, float* gain_stash,
-                    float* quu0_stash, int32_t* status, void* stream);
+                    int32_t d, int32_t du, int32_t T, int32_t flags, float* u, float* stash,
+                    int32_t* status, void* stream);
 
 /* Backward: gradients of sum(d_u * u) w.r.t. the nine inputs.
  * Replaces fused_lqr_layer_bwd (ttc/solvers/fused_lqr.py:148-253).
+ * u: the forward's output (needed by the fast path; may be NULL with
+ * TTC_LQR_FLAG_STABLE_BWD).  stash: from ttc_lqr_forward, or NULL (V_1 and Quu_0 are
+ * then recomputed by one forward sweep inside `workspace`).
+ * Fast path: a Hamiltonian rollout per problem (the reference's fused backward,
+ * symplectic_iter.py:542-885) with a terminal certificate (TTC_LQR_CERT_TOL); problems
+ * that fail it are recomputed by the stable path (gains stored per step in the
+ * workspace, closed-loop costates).  *n_fallback (host, may be NULL) receives the
+ * number of problems that took the stable path.  Reading that count synchronises
+ * `stream` once per token chunk.
  * grad_B / grad_Q are summed over heads (B and Q are head-shared).
- * gain_stash / quu0_stash: from ttc_lqr_forward, or both NULL (gains recomputed
- * chunk by chunk inside `workspace`).  workspace_bytes must be at least
- * ttc_lqr_workspace_bytes(c, ...) for some c >= 1 token; larger workspaces give
- * fewer, larger passes.  `flags` applies to the gain recomputation (unused when
- * the stash is given).  grad_limit: |g| >= grad_limit sets TTC_LQR_STATUS_LARGE
+ * workspace_bytes must be at least ttc_lqr_workspace_bytes(1, ...); larger workspaces
+ * give fewer, larger passes.  grad_limit: |g| >= grad_limit sets TTC_LQR_STATUS_LARGE
  * (the reference uses 1e6, fused_lqr.py:245); pass INFINITY to disable. */
 int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const float* R_inv,
                      const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
-                     const float* log_gamma_Q, const float* h0, const float* d_u,
+                     const float* log_gamma_Q, const float* h0, const float* u, const float* d_u,
                      int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T, int32_t flags,
-                     const float* gain_stash, const float* quu0_stash,
-                     float* grad_A_diag, float* grad_B, float* grad_Q, float* grad_R_inv,
-                     float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,
-                     float* grad_log_gamma_Q, float* grad_h0, void* workspace,
-                     size_t workspace_bytes, float grad_limit, int32_t* status, void* stream);
+                     const float* stash, float* grad_A_diag, float* grad_B, float* grad_Q,
+                     float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A,
+                     float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0, void* workspace,
+                     size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
+                     void* stream);
 
 #ifdef __cplusplus
 }

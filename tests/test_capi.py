@@ -56,29 +56,36 @@ def test_supported_dims(L):
 def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(16, 16, 1) == 1 and L.ttc_lqr_supported_flags(32, 32, 1) == 1
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
-    assert L.ttc_lqr_supported_flags(16, 16, 4) == 0
+    assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
+    assert L.ttc_lqr_supported_flags(16, 16, 8) == 0
     assert _fwd(L, d=64, du=64, flags=1) == 2
 
 
 def test_stash_bytes_formula(L):
+    # per problem: V_1 (d x d) + Quu_0 (du x du), fp32 -- independent of T
     N, H, d, T = 262144, 8, 16, 64
-    assert L.ttc_lqr_stash_bytes(N, H, d, d, T) == 4 * N * H * (T * d * d + d * d)
+    assert L.ttc_lqr_stash_bytes(N, H, d, d, T) == 4 * N * H * (d * d + d * d)
+    assert L.ttc_lqr_stash_bytes(N, H, d, d, 1024) == L.ttc_lqr_stash_bytes(N, H, d, d, T)
     assert L.ttc_lqr_stash_bytes(-1, H, d, d, T) == 0
 
 
 def test_workspace_bytes_monotone_and_stash_smaller(L):
     a = L.ttc_lqr_workspace_bytes(1, 8, 16, 16, 64, 0)
-    b = L.ttc_lqr_workspace_bytes(100, 8, 16, 16, 64, 0)
-    s = L.ttc_lqr_workspace_bytes(100, 8, 16, 16, 64, 1)
+    b = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 0)
+    s = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 1)
     assert 0 < a < b and 0 < s < b
-    # per problem: gains T d^2 + Quu_0 d^2 + trajectory 4 T d + two d^2 partials (fp32)
-    assert b >= 4 * 800 * (64 * 256 + 256 + 4 * 64 * 16 + 2 * 256)
+    # per problem: two d^2 gradient partials + list entry, plus (no stash) V_1 and Quu_0
+    assert s >= 4 * 800000 * (2 * 256 + 1)
+    assert b - s >= 4 * 800000 * (2 * 256)
+    # the fallback region is capped (256 MiB + alignment), so large chunks grow linearly
+    c = L.ttc_lqr_workspace_bytes(200000, 8, 16, 16, 64, 1)
+    assert abs((c - s) - 4 * 800000 * (2 * 256 + 1)) < 4096
     assert L.ttc_lqr_workspace_bytes(0, 8, 16, 16, 64, 0) == 0
 
 
 def _fwd(L, n=1, h=1, d=16, du=16, T=1, null_inputs=False, flags=0):
     p = None if null_inputs else ctypes.c_void_p(16)   # never dereferenced: validation fails first
-    return L.ttc_lqr_forward(*([p] * 9), n, h, d, du, T, flags, p, None, None, None, None)
+    return L.ttc_lqr_forward(*([p] * 9), n, h, d, du, T, flags, p, None, None, None)
 
 
 def test_forward_argument_validation(L):
@@ -93,9 +100,15 @@ def test_forward_argument_validation(L):
 
 def test_backward_argument_validation(L):
     p = ctypes.c_void_p(16)
-    args = [p] * 10 + [1, 1, 16, 16, 4, 0, None, None] + [p] * 9
-    assert L.ttc_lqr_backward(*args, p, 0, float("inf"), None, None) == 1       # workspace too small
-    bad = [p] * 10 + [1, 1, 20, 20, 4, 0, None, None] + [p] * 9
-    assert L.ttc_lqr_backward(*bad, p, 1 << 30, float("inf"), None, None) == 2  # unsupported dims
-    mixed = [p] * 10 + [1, 1, 16, 16, 4, 0, p, None] + [p] * 9
-    assert L.ttc_lqr_backward(*mixed, p, 1 << 30, float("inf"), None, None) == 1  # stash half given
+    head = [p] * 11                      # nine inputs, u, d_u
+    tail = [float("inf"), None, None, None]   # grad_limit, status, n_fallback, stream
+    args = head + [1, 1, 16, 16, 4, 0, None] + [p] * 9
+    assert L.ttc_lqr_backward(*args, p, 0, *tail) == 1            # workspace too small
+    bad = head + [1, 1, 20, 20, 4, 0, None] + [p] * 9
+    assert L.ttc_lqr_backward(*bad, p, 1 << 30, *tail) == 2       # unsupported dims
+    no_u = [p] * 9 + [None, p] + [1, 1, 16, 16, 4, 0, None] + [p] * 9
+    assert L.ttc_lqr_backward(*no_u, p, 1 << 30, *tail) == 1      # fast path needs u
+    n_fb = ctypes.c_int64(-7)
+    empty = head + [0, 1, 16, 16, 4, 0, None] + [p] * 9
+    assert L.ttc_lqr_backward(*empty, p, 0, float("inf"), None, ctypes.byref(n_fb), None) == 0
+    assert n_fb.value == 0

@@ -33,27 +33,31 @@ def _relerr(x, ref):
     return float(np.abs(x - ref).max() / max(np.abs(ref).max(), 1e-30))
 
 
-def run_hip(ins, T, dU, grad_limit=1e6, stash=None, precision="auto"):
+def run_hip(ins, T, dU, grad_limit=1e6, stash=None, precision="auto", stable=False):
     solve = _solver()
+    from ttc.solvers.hip_lqr import last_backward_stats
     dev = torch.device("cuda:0")
     xs = [t.detach().to(dev).float().requires_grad_(True) for t in ins]
-    u = solve(*xs, T, grad_limit=grad_limit, stash=stash, precision=precision)
+    u = solve(*xs, T, grad_limit=grad_limit, stash=stash, precision=precision, stable_backward=stable)
     (u * torch.as_tensor(dU, device=dev, dtype=u.dtype)).sum().backward()
     out = {"u": u.detach().cpu().double().numpy()}
     for n, t in zip(NAMES, xs):
         out[n] = t.grad.detach().cpu().double().numpy()
+    out["_fallback"] = last_backward_stats["fallback"]
     return out
 
 
-def check_case(label, ins, T, seed=0, grad_limit=1e6, stash=None, tol=TOL, precision="auto"):
+def check_case(label, ins, T, seed=0, grad_limit=1e6, stash=None, tol=TOL, precision="auto", stable=False):
     pb = LQRProblem(*ins, T)
     g = torch.Generator().manual_seed(seed + 7)
     dU = torch.randn(pb.N, pb.H, pb.du, generator=g).double().numpy()
     ref = solve_grads(pb, dU)
-    print(f"[{label}] N={pb.N} H={pb.H} d={pb.d} du={pb.du} T={T} stash={stash} precision={precision}", flush=True)
-    out = run_hip(ins, T, dU, grad_limit=grad_limit, stash=stash, precision=precision)
+    print(f"[{label}] N={pb.N} H={pb.H} d={pb.d} du={pb.du} T={T} stash={stash} precision={precision} "
+          f"stable={stable}", flush=True)
+    out = run_hip(ins, T, dU, grad_limit=grad_limit, stash=stash, precision=precision, stable=stable)
     errs = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
-    print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+    print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()) + f"  fallback={out['_fallback']}/{pb.P}",
+          flush=True)
     bad = {k: v for k, v in errs.items() if not (v <= tol)}
     assert not bad, f"{label}: rel err above {tol}: {bad}"
     return out
@@ -75,7 +79,33 @@ def test_config1_layer_slice(stash):
 def test_config2_layer_slice(precision):
     c = CONFIGS[2]
     x = make_x(2, n_tokens=64, seed=1)
-    check_case("cfg2", layer_solver_inputs(2, x), c["T"], precision=precision)
+    out = check_case("cfg2", layer_solver_inputs(2, x), c["T"], precision=precision)
+    assert out["_fallback"] == 0  # nominal inputs: every problem passes the certificate
+
+
+@pytest.mark.parametrize("cfg,n_tok", [(2, 32), (3, 2), (4, 1)])
+def test_stable_backward_path(cfg, n_tok):
+    """The stable path alone (per-step gains + closed-loop costates) on nominal configs."""
+    x = make_x(cfg, n_tokens=n_tok, seed=6)
+    out = check_case(f"cfg{cfg}-stable", layer_solver_inputs(cfg, x), CONFIGS[cfg]["T"], stable=True)
+    assert out["_fallback"] == out["u"].shape[0] * out["u"].shape[1]
+
+
+def test_certificate_rejects_stress_problems_and_fallback():
+    """Config-5 inputs at T=64: some problems fail the certificate and take the stable
+    path; the mixed result agrees with the all-stable run and the fp64 oracle."""
+    x = make_x(5, n_tokens=16, seed=5)
+    ins = layer_solver_inputs(5, x)
+    pb = LQRProblem(*ins, 64)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(3)).double().numpy()
+    fast = run_hip(ins, 64, dU, grad_limit=math.inf)
+    slow = run_hip(ins, 64, dU, grad_limit=math.inf, stable=True)
+    print(f"fallback {fast['_fallback']}/{pb.P}", flush=True)
+    assert 0 < fast["_fallback"] < pb.P
+    ref = solve_grads(pb, dU)
+    for k in ["u"] + NAMES:
+        assert _relerr(fast[k], ref[k]) <= TOL, k
+        assert _relerr(fast[k], slow[k]) <= TOL, k
 
 
 def test_config3_layer_slice():

@@ -1,5 +1,6 @@
 // ttc_lqr_capi.hip -- C ABI of libttc_lqr.so (see include/ttc_lqr.h): argument
-// validation, backward chunking and workspace layout, dispatch to the per-D kernels.
+// validation, workspace layouts, the backward's fast path and its per-problem
+// fallback, dispatch to the per-D kernels.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -7,9 +8,12 @@
 #include "ttc_lqr.h"
 #include "ttc_lqr_internal.h"
 
-#define TTC_LQR_VERSION_STRING "ttc-lqr-gfx950 0.2.0"
+#define TTC_LQR_VERSION_STRING "ttc-lqr-gfx950 0.3.0"
 
 namespace ttc {
+
+constexpr int kStashV1 = 2;     // STASH_V1 of ttc_lqr_kernels.cuh
+constexpr int kStashGains = 1;  // STASH_GAINS
 
 // grad_B / grad_Q: sum the per-problem partials over the H heads of each token.
 __global__ void headsum_kernel(const float* __restrict__ part, int64_t N, int H, int DD,
@@ -27,6 +31,57 @@ __global__ void headsum_kernel(const float* __restrict__ part, int64_t N, int H,
   }
 }
 
+__global__ void set_i32_kernel(int* p, int v) { *p = v; }
+
+// The nine inputs and d_u of the listed problems (chunk-local indices), gathered into
+// contiguous arrays of `cnt` one-head problems (the head-shared B and Q are copied per
+// problem), so the stable path can recompute them as cnt tokens with H = 1.
+struct Compact {
+  float *A, *B, *Q, *R, *Qf, *lA, *lB, *lQ, *h0, *dU;               // inputs
+  float *gA, *gB, *gQ, *gR, *gQf, *glA, *glB, *glQ, *gh0;            // gradients
+};
+
+__device__ __forceinline__ void copy_span(float* __restrict__ dst, const float* __restrict__ src, int n) {
+  for (int e = threadIdx.x; e < n; e += blockDim.x) dst[e] = src[e];
+}
+
+__global__ void gather_kernel(const int* __restrict__ list, int64_t base, int H, int d, int du,
+                              const float* __restrict__ A, const float* __restrict__ B, const float* __restrict__ Q,
+                              const float* __restrict__ R, const float* __restrict__ Qf, const float* __restrict__ lA,
+                              const float* __restrict__ lB, const float* __restrict__ lQ,
+                              const float* __restrict__ h0, const float* __restrict__ dU, Compact c) {
+  const int64_t i = blockIdx.x;
+  const int64_t p = list[base + i];
+  const int64_t n = p / H;
+  copy_span(c.A + i * d, A + p * d, d);
+  copy_span(c.B + i * d * du, B + n * d * du, d * du);
+  copy_span(c.Q + i * d * d, Q + n * d * d, d * d);
+  copy_span(c.R + i * du, R + p * du, du);
+  copy_span(c.Qf + i * d * d, Qf + p * d * d, d * d);
+  copy_span(c.lA + i, lA + p, 1);
+  copy_span(c.lB + i * du, lB + p * du, du);
+  copy_span(c.lQ + i * d, lQ + p * d, d);
+  copy_span(c.h0 + i * d, h0 + p * d, d);
+  copy_span(c.dU + i * du, dU + p * du, du);
+}
+
+__global__ void scatter_kernel(const int* __restrict__ list, int64_t base, int d, int du, Compact c,
+                               float* __restrict__ gA, float* __restrict__ gR, float* __restrict__ gQf,
+                               float* __restrict__ glA, float* __restrict__ glB, float* __restrict__ glQ,
+                               float* __restrict__ gh0, float* __restrict__ gBp, float* __restrict__ gQp) {
+  const int64_t i = blockIdx.x;
+  const int64_t p = list[base + i];
+  copy_span(gA + p * d, c.gA + i * d, d);
+  copy_span(gR + p * du, c.gR + i * du, du);
+  copy_span(gQf + p * d * d, c.gQf + i * d * d, d * d);
+  copy_span(glA + p, c.glA + i, 1);
+  copy_span(glB + p * du, c.glB + i * du, du);
+  copy_span(glQ + p * d, c.glQ + i * d, d);
+  copy_span(gh0 + p * d, c.gh0 + i * d, d);
+  copy_span(gBp + p * d * du, c.gB + i * d * du, d * du);  // one-head problems: grad_B is the partial
+  copy_span(gQp + p * d * d, c.gQ + i * d * d, d * d);
+}
+
 static int launch_headsum(const float* part, int64_t N, int H, int DD, float* out, float limit, int32_t* status,
                           hipStream_t s) {
   const int64_t total = N * DD;
@@ -38,18 +93,19 @@ static int launch_headsum(const float* part, int64_t N, int H, int DD, float* ou
 
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-struct BwdLayout {
+// ---- stable path: gains recomputed (or stashed), closed-loop costates ----------------
+struct StableLayout {
   size_t kst, q0s, traj, gBp, gQp, total;
 };
 
-static BwdLayout bwd_layout(int64_t chunk_tokens, int H, int d, int T, bool with_stash) {
+static StableLayout stable_layout(int64_t chunk_tokens, int H, int d, int T) {
   const size_t Pc = (size_t)chunk_tokens * (size_t)H;
-  BwdLayout L{};
+  StableLayout L{};
   size_t off = 0;
   L.kst = off;
-  off += with_stash ? 0 : align256(Pc * (size_t)T * d * d * sizeof(float));
+  off += align256(Pc * (size_t)T * d * d * sizeof(float));
   L.q0s = off;
-  off += with_stash ? 0 : align256(Pc * (size_t)d * d * sizeof(float));
+  off += align256(Pc * (size_t)d * d * sizeof(float));
   L.traj = off;
   off += align256(Pc * (size_t)T * d * 4 * sizeof(float));
   L.gBp = off;
@@ -58,6 +114,125 @@ static BwdLayout bwd_layout(int64_t chunk_tokens, int H, int d, int T, bool with
   off += align256(Pc * (size_t)d * d * sizeof(float));
   L.total = off;
   return L;
+}
+
+static int fwd_d(int d, const float* a, const float* b, const float* q, const float* r, const float* qf,
+                 const float* la, const float* lb, const float* lq, const float* hz, int64_t P, int H, int T, float* u,
+                 float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
+  switch (d) {
+    case 16: return launch_fwd_d16(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags);
+    case 32: return launch_fwd_d32(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags);
+    case 64: return launch_fwd_d64(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags);
+  }
+  return TTC_LQR_EUNSUPPORTED;
+}
+
+// Gradients of every problem by the stable path, token chunk by token chunk inside ws.
+static int stable_backward(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                           const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
+                           int64_t n_tokens, int H, int d, int T, int flags, float* gA, float* gB, float* gQ,
+                           float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, char* ws,
+                           size_t ws_bytes, float limit, int32_t* status, hipStream_t s) {
+  if (ws_bytes < stable_layout(1, H, d, T).total) return TTC_LQR_EINVAL;
+  int64_t chunk = 1, hi = n_tokens;  // largest token chunk whose layout fits
+  while (chunk < hi) {
+    const int64_t mid = chunk + (hi - chunk + 1) / 2;
+    if (stable_layout(mid, H, d, T).total <= ws_bytes) chunk = mid;
+    else hi = mid - 1;
+  }
+  const int64_t dd = (int64_t)d * d;
+  for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
+    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
+    const int64_t p0 = n0 * H, Pc = nc * H;
+    const StableLayout L = stable_layout(nc, H, d, T);
+    const float *a = A + p0 * d, *b = B + n0 * dd, *q = Q + n0 * dd, *r = R + p0 * d, *qf = Qf + p0 * dd;
+    const float *la = lA + p0, *lb = lB + p0 * d, *lq = lQ + p0 * d, *hz = h0 + p0 * d, *dz = dU + p0 * d;
+    float* kst = reinterpret_cast<float*>(ws + L.kst);
+    float* q0s = reinterpret_cast<float*>(ws + L.q0s);
+    int rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, Pc, H, T, nullptr, kst, q0s, kStashGains, nullptr, s, flags);
+    if (rc != TTC_LQR_OK) return rc;
+    float4* traj = reinterpret_cast<float4*>(ws + L.traj);
+    float* gBp = reinterpret_cast<float*>(ws + L.gBp);
+    float* gQp = reinterpret_cast<float*>(ws + L.gQp);
+    switch (d) {
+      case 16: rc = launch_bwd_d16(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
+      case 32: rc = launch_bwd_d32(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
+      case 64: rc = launch_bwd_d64(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
+      default: return TTC_LQR_EUNSUPPORTED;
+    }
+    if (rc != TTC_LQR_OK) return rc;
+    rc = launch_headsum(gBp, nc, H, (int)dd, gB + n0 * dd, limit, status, s);
+    if (rc != TTC_LQR_OK) return rc;
+    rc = launch_headsum(gQp, nc, H, (int)dd, gQ + n0 * dd, limit, status, s);
+    if (rc != TTC_LQR_OK) return rc;
+  }
+  return TTC_LQR_OK;
+}
+
+// ---- fast path: Hamiltonian rollout, fallback region for the problems it rejects ----
+static size_t compact_floats(int d, int du) {  // inputs + gradients of one problem
+  const size_t in = (size_t)d + d * du + d * d + du + d * d + 1 + du + d + d + du;
+  const size_t out = (size_t)d + d * du + d * d + du + d * d + 1 + du + d + d;
+  return in + out;
+}
+
+static int64_t fallback_capacity(int64_t Pc, int d, int du, int T) {
+  const size_t per = compact_floats(d, du) * sizeof(float) + 19 * 256 + stable_layout(1, 1, d, T).total;
+  int64_t cap = (int64_t)((size_t)256 << 20) / (int64_t)per;
+  if (cap < 1) cap = 1;
+  return Pc < cap ? Pc : cap;
+}
+
+struct FastLayout {
+  size_t v1, q0, gBp, gQp, list, cnt, fb, fb_stable, total;
+  int64_t F;
+};
+
+static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash) {
+  const size_t Pc = (size_t)chunk_tokens * (size_t)H;
+  FastLayout L{};
+  size_t off = 0;
+  L.v1 = off;
+  off += with_stash ? 0 : align256(Pc * (size_t)d * d * sizeof(float));
+  L.q0 = off;
+  off += with_stash ? 0 : align256(Pc * (size_t)du * du * sizeof(float));
+  L.gBp = off;
+  off += align256(Pc * (size_t)d * du * sizeof(float));
+  L.gQp = off;
+  off += align256(Pc * (size_t)d * d * sizeof(float));
+  L.list = off;
+  off += align256(Pc * sizeof(int32_t));
+  L.cnt = off;
+  off += 256;
+  L.F = fallback_capacity((int64_t)Pc, d, du, T);
+  L.fb = off;
+  // 19 compact arrays, each rounded up to 256 bytes
+  const size_t F = (size_t)L.F;
+  const size_t sizes[19] = {F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d, F * du,
+                            F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d};
+  for (size_t k = 0; k < 19; ++k) off += align256(sizes[k] * sizeof(float));
+  L.fb_stable = off;
+  off += stable_layout(L.F, 1, d, T).total;
+  L.total = off;
+  return L;
+}
+
+static Compact compact_at(char* base, int64_t F64, int d, int du) {
+  const size_t F = (size_t)F64;
+  const size_t sizes[19] = {F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d, F * du,
+                            F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d};
+  float* ptr[19];
+  size_t off = 0;
+  for (int k = 0; k < 19; ++k) {
+    ptr[k] = reinterpret_cast<float*>(base + off);
+    off += align256(sizes[k] * sizeof(float));
+  }
+  Compact c;
+  c.A = ptr[0]; c.B = ptr[1]; c.Q = ptr[2]; c.R = ptr[3]; c.Qf = ptr[4]; c.lA = ptr[5]; c.lB = ptr[6];
+  c.lQ = ptr[7]; c.h0 = ptr[8]; c.dU = ptr[9];
+  c.gA = ptr[10]; c.gB = ptr[11]; c.gQ = ptr[12]; c.gR = ptr[13]; c.gQf = ptr[14]; c.glA = ptr[15];
+  c.glB = ptr[16]; c.glQ = ptr[17]; c.gh0 = ptr[18];
+  return c;
 }
 
 }  // namespace ttc
@@ -83,117 +258,137 @@ int ttc_lqr_supported(int32_t d, int32_t du) { return (d == du && (d == 16 || d 
 int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if (!ttc_lqr_supported(d, du)) return 0;
   if ((flags & TTC_LQR_FLAG_FP64_RICCATI) && d > 32) return 0;
-  return (flags & ~(TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL)) ? 0 : 1;
+  const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD;
+  return (flags & ~known) ? 0 : 1;
 }
 
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {
   if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0 || T <= 0) return 0;
   const size_t P = (size_t)n_tokens * (size_t)heads;
-  return sizeof(float) * P * ((size_t)T * du * d + (size_t)du * du);
+  return sizeof(float) * P * ((size_t)d * d + (size_t)du * du);
 }
 
 size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
                                int32_t with_stash) {
   if (chunk_tokens <= 0 || heads <= 0 || d <= 0 || du != d || T <= 0) return 0;
-  return bwd_layout(chunk_tokens, heads, d, T, with_stash != 0).total;
+  return fast_layout(chunk_tokens, heads, d, du, T, with_stash != 0).total;
 }
 
 int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
                     const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
                     int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T, int32_t flags, float* u,
-                    float* gain_stash, float* quu0_stash, int32_t* status, void* stream) {
+                    float* stash, int32_t* status, void* stream) {
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
   if (n_tokens == 0) return TTC_LQR_OK;
   if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !u)
     return TTC_LQR_EINVAL;
-  if ((gain_stash == nullptr) != (quu0_stash == nullptr)) return TTC_LQR_EINVAL;
   const int64_t P = n_tokens * heads;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (d) {
-    case 16: return launch_fwd_d16(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, gain_stash, quu0_stash, status, s, flags);
-    case 32: return launch_fwd_d32(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, gain_stash, quu0_stash, status, s, flags);
-    case 64: return launch_fwd_d64(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, gain_stash, quu0_stash, status, s, flags);
-  }
-  return TTC_LQR_EUNSUPPORTED;
+  float* v1 = stash;
+  float* q0 = stash ? stash + P * (int64_t)d * d : nullptr;
+  return fwd_d(d, A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, v1, q0,
+               stash ? kStashV1 : 0, status, s, flags);
 }
 
 int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
                      const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
-                     const float* d_u, int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
-                     int32_t flags, const float* gain_stash, const float* quu0_stash, float* grad_A_diag, float* grad_B,
-                     float* grad_Q, float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A,
-                     float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0, void* workspace,
-                     size_t workspace_bytes, float grad_limit, int32_t* status, void* stream) {
+                     const float* u, const float* d_u, int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
+                     int32_t T, int32_t flags, const float* stash, float* grad_A_diag, float* grad_B, float* grad_Q,
+                     float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,
+                     float* grad_log_gamma_Q, float* grad_h0, void* workspace, size_t workspace_bytes,
+                     float grad_limit, int32_t* status, int64_t* n_fallback, void* stream) {
+  if (n_fallback) *n_fallback = 0;
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
   if (n_tokens == 0) return TTC_LQR_OK;
+  const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
   if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !d_u ||
       !grad_A_diag || !grad_B || !grad_Q || !grad_R_inv || !grad_Q_f || !grad_log_gamma_A || !grad_log_gamma_B ||
-      !grad_log_gamma_Q || !grad_h0 || !workspace)
+      !grad_log_gamma_Q || !grad_h0 || !workspace || (!stable && !u))
     return TTC_LQR_EINVAL;
-  if ((gain_stash == nullptr) != (quu0_stash == nullptr)) return TTC_LQR_EINVAL;
-  const bool with_stash = gain_stash != nullptr;
-  const size_t per_token = bwd_layout(1, heads, d, T, with_stash).total;
-  if (workspace_bytes < per_token) return TTC_LQR_EINVAL;
-  // largest chunk whose layout fits (layout is monotone in the chunk size)
-  int64_t chunk = (int64_t)(workspace_bytes / per_token);
-  if (chunk > n_tokens) chunk = n_tokens;
-  while (chunk > 1 && bwd_layout(chunk, heads, d, T, with_stash).total > workspace_bytes) --chunk;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  const int H = heads;
+  if (stable) {
+    if (n_fallback) *n_fallback = n_tokens * heads;
+    return stable_backward(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, d_u, n_tokens, H, d,
+                           T, flags, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f, grad_log_gamma_A,
+                           grad_log_gamma_B, grad_log_gamma_Q, grad_h0, ws, workspace_bytes, grad_limit, status, s);
+  }
+  const bool with_stash = stash != nullptr;
+  // largest token chunk whose layout fits the workspace (the layout grows with the chunk)
+  if (workspace_bytes < fast_layout(1, H, d, du, T, with_stash).total) return TTC_LQR_EINVAL;
+  int64_t chunk = 1, hi = n_tokens;
+  while (chunk < hi) {
+    const int64_t mid = chunk + (hi - chunk + 1) / 2;
+    if (fast_layout(mid, H, d, du, T, with_stash).total <= workspace_bytes) chunk = mid;
+    else hi = mid - 1;
+  }
   const int64_t dd = (int64_t)d * d;
+  const float tau = TTC_LQR_CERT_TOL;
+  int64_t total_fb = 0;
   for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
-    const int64_t p0 = n0 * heads, Pc = nc * heads;
-    const BwdLayout L = bwd_layout(nc, heads, d, T, with_stash);
-    const float* a = A_diag + p0 * d;
-    const float* b = B + n0 * dd;
-    const float* q = Q + n0 * dd;
-    const float* r = R_inv + p0 * du;
-    const float* qf = Q_f + p0 * dd;
-    const float* la = log_gamma_A + p0;
-    const float* lb = log_gamma_B + p0 * du;
-    const float* lq = log_gamma_Q + p0 * d;
-    const float* hz = h0 + p0 * d;
-    const float* dz = d_u + p0 * du;
-    float* kst;
-    float* q0s;
+    const int64_t p0 = n0 * H, Pc = nc * H;
+    const FastLayout L = fast_layout(nc, H, d, du, T, with_stash);
+    const float *a = A_diag + p0 * d, *b = B + n0 * dd, *q = Q + n0 * dd, *r = R_inv + p0 * du;
+    const float *qf = Q_f + p0 * dd, *la = log_gamma_A + p0, *lb = log_gamma_B + p0 * du;
+    const float *lq = log_gamma_Q + p0 * d, *hz = h0 + p0 * d, *dz = d_u + p0 * du, *uz = u + p0 * du;
+    float *gA = grad_A_diag + p0 * d, *gR = grad_R_inv + p0 * du, *gQf = grad_Q_f + p0 * dd;
+    float *glA = grad_log_gamma_A + p0, *glB = grad_log_gamma_B + p0 * du, *glQ = grad_log_gamma_Q + p0 * d;
+    float* gh = grad_h0 + p0 * d;
+    const float *v1, *q0;
     int rc = TTC_LQR_OK;
     if (with_stash) {
-      kst = const_cast<float*>(gain_stash) + p0 * (int64_t)T * dd;
-      q0s = const_cast<float*>(quu0_stash) + p0 * dd;
+      v1 = stash + p0 * dd;
+      q0 = stash + n_tokens * H * dd + p0 * (int64_t)du * du;
     } else {
-      kst = reinterpret_cast<float*>(ws + L.kst);
-      q0s = reinterpret_cast<float*>(ws + L.q0s);
-      switch (d) {
-        case 16: rc = launch_fwd_d16(a, b, q, r, qf, la, lb, lq, hz, Pc, heads, T, nullptr, kst, q0s, nullptr, s, flags); break;
-        case 32: rc = launch_fwd_d32(a, b, q, r, qf, la, lb, lq, hz, Pc, heads, T, nullptr, kst, q0s, nullptr, s, flags); break;
-        case 64: rc = launch_fwd_d64(a, b, q, r, qf, la, lb, lq, hz, Pc, heads, T, nullptr, kst, q0s, nullptr, s, flags); break;
-      }
+      float* v1w = reinterpret_cast<float*>(ws + L.v1);
+      float* q0w = reinterpret_cast<float*>(ws + L.q0);
+      rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, Pc, H, T, nullptr, v1w, q0w, kStashV1, nullptr, s, flags);
       if (rc != TTC_LQR_OK) return rc;
+      v1 = v1w;
+      q0 = q0w;
     }
-    float4* traj = reinterpret_cast<float4*>(ws + L.traj);
     float* gBp = reinterpret_cast<float*>(ws + L.gBp);
     float* gQp = reinterpret_cast<float*>(ws + L.gQp);
-    float* gA = grad_A_diag + p0 * d;
-    float* gR = grad_R_inv + p0 * du;
-    float* gQf = grad_Q_f + p0 * dd;
-    float* glA = grad_log_gamma_A + p0;
-    float* glB = grad_log_gamma_B + p0 * du;
-    float* glQ = grad_log_gamma_Q + p0 * d;
-    float* gh = grad_h0 + p0 * d;
+    int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
+    int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
+    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
     switch (d) {
-      case 16: rc = launch_bwd_d16(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, heads, T, traj, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, status, s); break;
-      case 32: rc = launch_bwd_d32(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, heads, T, traj, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, status, s); break;
-      case 64: rc = launch_bwd_d64(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, heads, T, traj, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, status, s); break;
+      case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
+      case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
+      case 64: rc = launch_ham_d64(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
+      default: return TTC_LQR_EUNSUPPORTED;
     }
     if (rc != TTC_LQR_OK) return rc;
-    rc = launch_headsum(gBp, nc, heads, (int)dd, grad_B + n0 * dd, grad_limit, status, s);
+    // how many problems the certificate rejected (one stream synchronisation per chunk)
+    int32_t nfail = 0;
+    if (hipMemcpyAsync(&nfail, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;
+    if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
+    if (nfail < 0 || nfail > Pc) return TTC_LQR_ELAUNCH;
+    total_fb += nfail;
+    const Compact c = compact_at(ws + L.fb, L.F, d, du);
+    for (int64_t f0 = 0; f0 < nfail; f0 += L.F) {
+      const int64_t fc = (f0 + L.F <= nfail) ? L.F : (nfail - f0);
+      hipLaunchKernelGGL(gather_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q, r, qf, la,
+                         lb, lq, hz, dz, c);
+      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+      rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags, c.gA, c.gB,
+                           c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable,
+                           L.total - L.fb_stable, grad_limit, status, s);
+      if (rc != TTC_LQR_OK) return rc;
+      hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
+                         glB, glQ, gh, gBp, gQp);
+      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+    }
+    rc = launch_headsum(gBp, nc, H, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
     if (rc != TTC_LQR_OK) return rc;
-    rc = launch_headsum(gQp, nc, heads, (int)dd, grad_Q + n0 * dd, grad_limit, status, s);
+    rc = launch_headsum(gQp, nc, H, (int)dd, grad_Q + n0 * dd, grad_limit, status, s);
     if (rc != TTC_LQR_OK) return rc;
   }
+  if (n_fallback) *n_fallback = total_fb;
   return TTC_LQR_OK;
 }
 

@@ -5,11 +5,11 @@ namespace ttc {
 
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags) {
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
   // fp32 sweeps run on the matrix-core kernel unless the row-layout kernel is asked for
   if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL)))
-    return launch_fwd_d16_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, kst, q0s, status, s);
-  return launch_fwd<16, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, kst, q0s, status, s, flags);
+    return launch_fwd_d16_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
+  return launch_fwd<16, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);
 }
 
 int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
@@ -19,6 +19,16 @@ int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* 
                   float* gQp, float limit, int32_t* status, hipStream_t s) {
   return launch_bwd<16>(A, B, Q, R, Qf, lA, lB, lQ, h0, dU, kst, q0s, P, H, T, traj, gA, gR, gQf, glA, glB, glQ,
                        gh0, gBp, gQp, limit, status, s);
+}
+
+int launch_ham_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                  const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
+                  const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
+                  float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
+                  float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
+                  hipStream_t s) {
+  return launch_ham<16>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
 }
 
 }  // namespace ttc

@@ -1,34 +1,55 @@
 // ttc_lqr_internal.h -- per-D kernel launchers shared by the translation units of libttc_lqr.so.
+//
+// Forward launchers take a stash mode `sm` (STASH_NONE / STASH_GAINS / STASH_V1, see
+// ttc_lqr_kernels.cuh) and its two buffers st_a (gains or V_1) and st_b (Quu_0).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace ttc {
-int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
-                  const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags);
 int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                        int T, float* u, float* kst, float* q0s, int32_t* status, hipStream_t s);
+                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s);
+int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                  const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
 int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s);
+int launch_ham_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                  const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
+                  const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
+                  float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
+                  float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
+                  hipStream_t s);
 int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags);
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
 int launch_bwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s);
+int launch_ham_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                  const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
+                  const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
+                  float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
+                  float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
+                  hipStream_t s);
 int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags);
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
 int launch_bwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s);
+int launch_ham_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                  const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
+                  const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
+                  float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
+                  float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
+                  hipStream_t s);
 }  // namespace ttc

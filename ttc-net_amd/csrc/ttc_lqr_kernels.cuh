@@ -38,6 +38,11 @@ namespace ttc {
 
 constexpr int kPad = 4;  // LDS row padding (floats): keeps rows 16-byte aligned, staggers banks
 
+// Forward stash modes.
+constexpr int STASH_NONE = 0;   // u only
+constexpr int STASH_GAINS = 1;  // every gain K_t [P,T,du,d] + Quu_0 [P,du,du] (stable backward)
+constexpr int STASH_V1 = 2;     // V_1 [P,d,d] + Quu_0 [P,du,du] (fast backward)
+
 template <int D>
 struct Geo {
   static constexpr int PPB = (D == 16) ? 16 : (D == 32 ? 4 : 1);  // problems per block
@@ -182,13 +187,15 @@ __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& my
 }
 
 // ---------------------------------------------------------------------------
-// Row-layout Riccati sweep from step t_start down to 0: u0, optional gain stash.
+// Row-layout Riccati sweep from step t_start down to 0: u0 and the stash of mode SM
+// (STASH_NONE; STASH_GAINS: all gains K_t [P,T,du,d] into `kstash` and Quu_0; STASH_V1:
+// V_1 [P,d,d] into `kstash` and Quu_0 -- the compact stash of the fast backward).
 // R is the arithmetic type of the sweep (float, or double for long ill-conditioned
 // horizons); inputs, u and the stash are fp32 in HBM.  The D lanes of a problem
 // enter with V = V_{t_start+1} (lane li holds row li); Bs holds the problem's B
 // (row stride Geo<D>::LDM) and S is the problem's Geo<D>::PER_PROB-element scratch.
 // ---------------------------------------------------------------------------
-template <int D, typename R, bool STASH, bool WRITE_U>
+template <int D, typename R, int SM, bool WRITE_U>
 __device__ __forceinline__ void rpl_sweep(
     const float* __restrict__ A_diag, const float* __restrict__ Qg, const float* __restrict__ Rinv,
     const float* __restrict__ lgA, const float* __restrict__ lgB, const float* __restrict__ lgQ,
@@ -219,6 +226,12 @@ __device__ __forceinline__ void rpl_sweep(
   }
 
   for (int t = t_start; t >= 0; --t) {
+    if (SM == STASH_V1 && t == 0 && valid) {
+      float vrow[D];
+#pragma unroll
+      for (int c = 0; c < D; ++c) vrow[c] = (float)V[c];
+      st_global_row<D>(kstash + (p * D + li) * D, vrow);
+    }
     const R tp1 = (R)(t + 1);
     const R eA = exp(lgA_p * tp1);
     const R beta_i = exp(lgB_i * tp1);
@@ -263,7 +276,7 @@ __device__ __forceinline__ void rpl_sweep(
     for (int k = 0; k < D; ++k) aug[k] = aug[k] * beta_i + ((k == li) ? rr_i : R(0));
 #pragma unroll
     for (int c = 0; c < D; ++c) aug[D + c] = mat[c * G::LDM + li] * alpha[c];
-    if (STASH && t == 0) {
+    if (SM != STASH_NONE && t == 0) {
       float qrow[D];
 #pragma unroll
       for (int k = 0; k < D; ++k) qrow[k] = (float)aug[k];
@@ -277,7 +290,7 @@ __device__ __forceinline__ void rpl_sweep(
     const R ipiv = R(1) / mypiv;
 #pragma unroll
     for (int c = 0; c < D; ++c) x[c] = aug[D + c] * ipiv;
-    if (STASH && valid) {
+    if (SM == STASH_GAINS && valid) {
       float krow[D];
 #pragma unroll
       for (int c = 0; c < D; ++c) krow[c] = (float)(-x[c]);
@@ -332,7 +345,7 @@ __device__ __forceinline__ void rpl_sweep(
 // ---------------------------------------------------------------------------
 // Forward kernel (row layout): stage B, V_T = sym(Q_f), full sweep.
 // ---------------------------------------------------------------------------
-template <int D, typename R, bool STASH, bool WRITE_U>
+template <int D, typename R, int SM, bool WRITE_U>
 __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
@@ -370,7 +383,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
 #pragma unroll
     for (int c = 0; c < D; ++c) V[c] = R(0.5) * ((R)qf[li * D + c] + (R)qf[c * D + li]);
   }
-  rpl_sweep<D, R, STASH, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, Bs, S, li, p, valid, n, T, T - 1, V,
+  rpl_sweep<D, R, SM, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, Bs, S, li, p, valid, n, T, T - 1, V,
                                   u_out, kstash, q0stash, status);
 }
 
@@ -613,6 +626,293 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fast backward: forward Hamiltonian rollout with a terminal certificate.
+//
+// From V_1 and Quu_0 (the forward's compact stash) and the forward output u_0:
+//   w_0 = -Quu_0^{-1} d_u,  h_1 = A_0 h_0 + B_0 u_0,  h~_1 = B_0 w_0,
+//   lambda_1 = V_1 h_1,     lambda~_1 = V_1 h~_1,
+// and for t = 1..T-1 the costate recursion of lin_solver_lqr.py:82-98 solved for
+// lambda_{t+1}, with the stationarity condition R u_t + B_t' lambda_{t+1} = 0:
+//   lambda_{t+1} = A_t^{-1} (lambda_t - Qc_t h_t),   u_t = -R^{-1} B_t' lambda_{t+1},
+//   h_{t+1} = A_t h_t + B_t u_t                      (same for the adjoint, w_t).
+// This is the reference's fused backward rollout (symplectic_iter.py:764-885):
+// no per-step gains are needed and every gradient term of step t is formed when
+// step t is rolled.  The recursion amplifies rounding along the unstable modes of
+// the Hamiltonian map, so every problem carries a certificate: the terminal
+// condition lambda_T = Q_f h_T must hold for both trajectories to relative
+// accuracy `tau` (max-norm over the D entries, relative to |Q_f h_T| + |lambda_T|)
+// and every gradient must be finite.  A problem that misses it writes nothing and is
+// appended to fail_list (chunk-local index); the caller recomputes it with the
+// stable path (stored gains, closed-loop costates).  grad_B / grad_Q partials go to
+// gBp / gQp for headsum_kernel, as in lqr_bwd_kernel.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    const float* __restrict__ u0g, const float* __restrict__ dU, const float* __restrict__ v1s,
+    const float* __restrict__ q0s, int64_t P, int H, int T, int ntok_lds, float tau, float* __restrict__ gA,
+    float* __restrict__ gRinv, float* __restrict__ gQf, float* __restrict__ glgA, float* __restrict__ glgB,
+    float* __restrict__ glgQ, float* __restrict__ gh0, float* __restrict__ gBp, float* __restrict__ gQp,
+    float grad_limit, int* __restrict__ fail_list, int* __restrict__ fail_count, int* __restrict__ status) {
+  using G = Geo<D>;
+  extern __shared__ float smem[];
+  const int li = threadIdx.x % D;
+  const int pb = threadIdx.x / D;
+  const int64_t p0 = (int64_t)blockIdx.x * G::PPB;
+  int64_t p = p0 + pb;
+  const bool valid = p < P;
+  if (!valid) p = P - 1;  // idle lanes recompute a real problem, never store
+  const int64_t n = p / H;
+  const int64_t n0 = p0 / H;
+  {
+    const int64_t plast = (p0 + G::PPB - 1 < P) ? (p0 + G::PPB - 1) : (P - 1);
+    const int ntok = (int)(plast / H - n0 + 1);
+    for (int e = threadIdx.x; e < ntok * D * D; e += G::THREADS) {
+      const int tk = e / (D * D), rem = e % (D * D);
+      smem[(tk * D + rem / D) * G::LDM + rem % D] = Bg[(n0 + tk) * D * D + rem];
+    }
+  }
+  __syncthreads();
+  const float* Bs = smem + (int)(n - n0) * G::MAT;
+  float* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
+  float* v0 = S + G::MAT;  // 6 vectors of D floats, then the pivot row
+  float* v1 = v0 + D;
+  float* v2 = v1 + D;
+  float* v3 = v2 + D;
+  float* v4 = v3 + D;
+  float* v5 = v4 + D;
+  float* prow = v5 + D;    // D + 4 floats
+
+  const float a_i = A_diag[p * D + li];
+  const float r_i = Rinv[p * D + li];
+  const float rr_i = 1.0f / r_i;
+  const float lgB_i = lgB[p * D + li];
+  const float lgQ_i = lgQ[p * D + li];
+  const float lgA_p = lgA[p];
+  float Brow[D], Bcol[D], Qrow[D];
+  {
+    const float* qg = Qg + n * D * D;
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+      Brow[c] = Bs[li * G::LDM + c];
+      Bcol[c] = Bs[c * G::LDM + li];
+      Qrow[c] = 0.5f * (qg[li * D + c] + qg[c * D + li]);
+    }
+  }
+
+  // t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (pivoted elimination)
+  float w_i;
+  {
+    float aug[D + 4];
+    ld_global_row<D>(q0s + (p * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
+    aug[D] = dU[p * D + li];
+    aug[D + 1] = aug[D + 2] = aug[D + 3] = 0.f;
+    float piv;
+    int pos;
+    gauss_jordan<D, D + 4>(aug, li, prow, piv, pos);
+    v0[pos] = -aug[D] / piv;
+    wave_sync();
+    w_i = v0[li];
+    wave_sync();
+  }
+
+  float h_i = h0[p * D + li], hb_i = 0.f, lam_i, lamb_i;
+  float gA_i, glgA_part, glgB_i, gr_i, gh0_i, glgQ_i = 0.f;
+  float gBrow[D], gQrow[D];
+  {
+    const float u_i = u0g[p * D + li];
+    const float eA = expf(lgA_p);
+    const float alpha_i = fmaf(a_i, eA, 1.0f);
+    const float beta_i = expf(lgB_i);
+    v2[li] = beta_i * u_i;
+    v3[li] = beta_i * w_i;
+    wave_sync();
+    float bu[D], bw[D];
+    ld_row<D>(v2, bu);
+    ld_row<D>(v3, bw);
+    float hn = alpha_i * h_i, hbn = 0.f;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      hn = fmaf(Brow[j], bu[j], hn);
+      hbn = fmaf(Brow[j], bw[j], hbn);
+    }
+    v0[li] = hn;
+    v1[li] = hbn;
+    wave_sync();
+    float hv[D], hbv[D], vrow[D];
+    ld_row<D>(v0, hv);
+    ld_row<D>(v1, hbv);
+    ld_global_row<D>(v1s + (p * D + li) * D, vrow);
+    float lam = 0.f, lamb = 0.f;
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+      lam = fmaf(vrow[c], hv[c], lam);
+      lamb = fmaf(vrow[c], hbv[c], lamb);
+    }
+    v4[li] = lam;
+    v5[li] = lamb;
+    wave_sync();
+    float lv[D], lbv[D];
+    ld_row<D>(v4, lv);
+    ld_row<D>(v5, lbv);
+    float btl = 0.f, btlb = 0.f;
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+      gBrow[c] = fmaf(lamb, bu[c], lam * bw[c]);  // torch_lqr.py:53 chained through B_0 = B diag(beta_0)
+      gQrow[c] = 0.f;
+      btl = fmaf(Bcol[c], lv[c], btl);
+      btlb = fmaf(Bcol[c], lbv[c], btlb);
+    }
+    const float gAt = h_i * lamb;  // h~_0 = 0   (torch_lqr.py:51)
+    gA_i = gAt * eA;
+    glgA_part = gAt * a_i * eA;
+    glgB_i = beta_i * fmaf(u_i, btlb, w_i * btl);
+    gr_i = -u_i * w_i * rr_i * rr_i;  // d(1/R_inv)/dR_inv  (torch_lqr.py:59)
+    gh0_i = alpha_i * lamb;           // torch_lqr.py:61
+    h_i = hn;
+    hb_i = hbn;
+    lam_i = lam;
+    lamb_i = lamb;
+    wave_sync();
+  }
+
+  for (int t = 1; t < T; ++t) {
+    const float tf = (float)t;
+    // state cost on h_t:  Qc_t = D_t Q D_t,  D_t = diag(exp(lgQ t))   (torch_lqr.py:55 + chain rule)
+    const float q_i = expf(lgQ_i * tf);
+    v0[li] = q_i * h_i;
+    v1[li] = q_i * hb_i;
+    wave_sync();
+    float qh[D], qhb[D];
+    ld_row<D>(v0, qh);
+    ld_row<D>(v1, qhb);
+    float Qh = 0.f, Qhb = 0.f;
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+      Qh = fmaf(Qrow[c], qh[c], Qh);
+      Qhb = fmaf(Qrow[c], qhb[c], Qhb);
+      gQrow[c] = fmaf(0.5f * q_i, fmaf(h_i, qhb[c], hb_i * qh[c]), gQrow[c]);
+    }
+    Qh *= q_i;
+    Qhb *= q_i;
+    glgQ_i = fmaf(tf, fmaf(h_i, Qhb, hb_i * Qh), glgQ_i);
+    // step t dynamics
+    const float tp1 = tf + 1.0f;
+    const float eA = expf(lgA_p * tp1);
+    const float alpha_i = fmaf(a_i, eA, 1.0f);
+    const float beta_i = expf(lgB_i * tp1);
+    const float ia = 1.0f / alpha_i;
+    const float lam_n = (lam_i - Qh) * ia;
+    const float lamb_n = (lamb_i - Qhb) * ia;
+    v2[li] = lam_n;
+    v3[li] = lamb_n;
+    wave_sync();
+    float lv[D], lbv[D];
+    ld_row<D>(v2, lv);
+    ld_row<D>(v3, lbv);
+    float btl = 0.f, btlb = 0.f;
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+      btl = fmaf(Bcol[c], lv[c], btl);
+      btlb = fmaf(Bcol[c], lbv[c], btlb);
+    }
+    const float u_i = -r_i * beta_i * btl;
+    const float w_i2 = -r_i * beta_i * btlb;
+    v4[li] = beta_i * u_i;
+    v5[li] = beta_i * w_i2;
+    wave_sync();
+    float bu[D], bw[D];
+    ld_row<D>(v4, bu);
+    ld_row<D>(v5, bw);
+    float hn = alpha_i * h_i, hbn = alpha_i * hb_i;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      hn = fmaf(Brow[j], bu[j], hn);
+      hbn = fmaf(Brow[j], bw[j], hbn);
+      gBrow[j] = fmaf(lamb_n, bu[j], fmaf(lam_n, bw[j], gBrow[j]));
+    }
+    const float gAt = fmaf(h_i, lamb_n, hb_i * lam_n);
+    gA_i = fmaf(gAt, eA, gA_i);
+    glgA_part = fmaf(gAt * a_i, tp1 * eA, glgA_part);
+    glgB_i = fmaf(tp1 * beta_i, fmaf(u_i, btlb, w_i2 * btl), glgB_i);
+    gr_i = fmaf(-u_i * w_i2, rr_i * rr_i, gr_i);
+    h_i = hn;
+    hb_i = hbn;
+    lam_i = lam_n;
+    lamb_i = lamb_n;
+    wave_sync();
+  }
+
+  // terminal cost: grad Q_f = sym(h_T h~_T'); certificate lambda_T = Q_f h_T
+  float gq[D];
+  float e1, e2, m1, m2, m3, m4;
+  {
+    v0[li] = h_i;
+    v1[li] = hb_i;
+    wave_sync();
+    float hv[D], hbv[D];
+    ld_row<D>(v0, hv);
+    ld_row<D>(v1, hbv);
+    const float* qfp = Qf + p * D * D;
+    float fh = 0.f, fhb = 0.f;
+#pragma unroll
+    for (int c = 0; c < D; ++c) {
+      const float qf = 0.5f * (qfp[li * D + c] + qfp[c * D + li]);
+      fh = fmaf(qf, hv[c], fh);
+      fhb = fmaf(qf, hbv[c], fhb);
+      gq[c] = 0.5f * fmaf(h_i, hbv[c], hb_i * hv[c]);
+    }
+    e1 = fabsf(lam_i - fh);
+    e2 = fabsf(lamb_i - fhb);
+    m1 = fabsf(fh) + fabsf(lam_i);
+    m2 = fabsf(fhb) + fabsf(lamb_i);
+    wave_sync();
+  }
+  const float glgA_p = group_sum<D>(glgA_part, v0, li);
+  // every accumulator finite <=> this sum is (a sum of finite values overflows only near 1e38)
+  float fin = fabsf(gA_i) + fabsf(gr_i) + fabsf(glgB_i) + fabsf(glgQ_i) + fabsf(gh0_i) + fabsf(glgA_p);
+#pragma unroll
+  for (int c = 0; c < D; ++c) fin += fabsf(gBrow[c]) + fabsf(gQrow[c]) + fabsf(gq[c]);
+  // group maxima of non-negative floats via their bit patterns (NaN sorts above +inf)
+  const float E1 = __uint_as_float(group_max_u32<D>(__float_as_uint(e1)));
+  const float E2 = __uint_as_float(group_max_u32<D>(__float_as_uint(e2)));
+  m3 = __uint_as_float(group_max_u32<D>(__float_as_uint(m1)));
+  m4 = __uint_as_float(group_max_u32<D>(__float_as_uint(m2)));
+  const unsigned bad_lane = isfinite(fin) ? 0u : 1u;
+  const bool ok = group_max_u32<D>(bad_lane) == 0u && E1 <= tau * m3 && E2 <= tau * m4;
+  if (!valid) return;
+  if (!ok) {
+    if (li == 0) fail_list[atomicAdd(fail_count, 1)] = (int)p;
+    return;
+  }
+  int flags = 0;
+#pragma unroll
+  for (int c = 0; c < D; ++c) {
+    flag_value<D>(gBrow[c], grad_limit, flags);
+    flag_value<D>(gQrow[c], grad_limit, flags);
+    flag_value<D>(gq[c], grad_limit, flags);
+  }
+  flag_value<D>(gA_i, grad_limit, flags);
+  flag_value<D>(glgB_i, grad_limit, flags);
+  flag_value<D>(gr_i, grad_limit, flags);
+  flag_value<D>(glgQ_i, grad_limit, flags);
+  flag_value<D>(gh0_i, grad_limit, flags);
+  flag_value<D>(glgA_p, grad_limit, flags);
+  gA[p * D + li] = gA_i;
+  gRinv[p * D + li] = gr_i;
+  glgB[p * D + li] = glgB_i;
+  glgQ[p * D + li] = glgQ_i;
+  gh0[p * D + li] = gh0_i;
+  if (li == 0) glgA[p] = glgA_p;
+  st_global_row<D>(gQf + (p * D + li) * D, gq);
+  st_global_row<D>(gBp + (p * D + li) * D, gBrow);
+  st_global_row<D>(gQp + (p * D + li) * D, gQrow);
+  if (flags && status != nullptr) atomicOr(status, flags);
+}
+
 
 // ---------------------------------------------------------------------------
 // launch helpers (instantiated per D in ttc_lqr_d*.hip)
@@ -629,38 +929,70 @@ inline size_t lds_bytes(int H, size_t elem = sizeof(float)) {
   return elem * ((size_t)ntok_lds_for<D>(H) * Geo<D>::MAT + (size_t)Geo<D>::PPB * Geo<D>::PER_PROB);
 }
 
-template <int D, typename RT>
-inline void launch_fwd_t(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+template <int D, typename RT, int SM, bool WU>
+inline void launch_fwd_k(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                          const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                         int T, float* u, float* kst, float* q0s, int32_t* status, hipStream_t s) {
+                         int T, float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
-  const size_t sh = lds_bytes<D>(H, sizeof(RT));
-  const int nt = ntok_lds_for<D>(H);
-  if (kst != nullptr) {
-    if (u != nullptr)
-      hipLaunchKernelGGL((lqr_fwd_kernel<D, RT, true, true>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P,
-                         H, T, nt, u, kst, q0s, status);
-    else
-      hipLaunchKernelGGL((lqr_fwd_kernel<D, RT, true, false>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0,
-                         P, H, T, nt, u, kst, q0s, status);
-  } else {
-    hipLaunchKernelGGL((lqr_fwd_kernel<D, RT, false, true>), grid, block, sh, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P,
-                       H, T, nt, u, kst, q0s, status);
+  hipLaunchKernelGGL((lqr_fwd_kernel<D, RT, SM, WU>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf,
+                     lA, lB, lQ, h0, P, H, T, ntok_lds_for<D>(H), u, st_a, st_b, status);
+}
+
+// Forward launch by stash mode: sm = STASH_NONE (u), STASH_GAINS (gains + Quu_0 into
+// st_a / st_b, no u) or STASH_V1 (V_1 + Quu_0 into st_a / st_b, u when u != nullptr).
+template <int D, typename RT>
+inline int launch_fwd_t(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
+                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s) {
+  switch (sm) {
+    case STASH_NONE:
+      launch_fwd_k<D, RT, STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      break;
+    case STASH_GAINS:
+      launch_fwd_k<D, RT, STASH_GAINS, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      break;
+    case STASH_V1:
+      if (u != nullptr)
+        launch_fwd_k<D, RT, STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      else
+        launch_fwd_k<D, RT, STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      break;
+    default:
+      return TTC_LQR_EINVAL;
   }
+  return TTC_LQR_OK;
 }
 
 template <int D, bool HAS_FP64>
 inline int launch_fwd(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                       const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                      int T, float* u, float* kst, float* q0s, int32_t* status, hipStream_t s, int flags) {
+                      int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
   if (P <= 0) return TTC_LQR_OK;
+  int rc;
   if (flags & TTC_LQR_FLAG_FP64_RICCATI) {
     if constexpr (HAS_FP64)
-      launch_fwd_t<D, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, kst, q0s, status, s);
+      rc = launch_fwd_t<D, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
     else
       return TTC_LQR_EUNSUPPORTED;
-  } else
-    launch_fwd_t<D, float>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, kst, q0s, status, s);
+  } else {
+    rc = launch_fwd_t<D, float>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
+  }
+  if (rc != TTC_LQR_OK) return rc;
+  return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+}
+
+template <int D>
+inline int launch_ham(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                      const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
+                      const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
+                      float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
+                      float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
+                      hipStream_t s) {
+  if (P <= 0) return TTC_LQR_OK;
+  const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
+  hipLaunchKernelGGL((lqr_ham_bwd_kernel<D>), grid, block, lds_bytes<D>(H), s, A, B, Q, R, Qf, lA, lB, lQ, h0, u0,
+                     dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB, glQ, gh0, gBp, gQp,
+                     limit, fail_list, fail_count, status);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 

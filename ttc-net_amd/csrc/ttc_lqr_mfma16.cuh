@@ -102,7 +102,7 @@ __device__ __forceinline__ void st4(float* p, v4f v) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-template <bool STASH, bool WRITE_U>
+template <int SM, bool WRITE_U>
 __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
@@ -165,6 +165,17 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
     const float my_beta = expf(lgB_c * tp1);
     const float my_alpha = fmaf(a_c, expf(lgA_o * tp1), 1.0f);
     const float my_q = last ? 0.0f : expf(lgQ_c * (float)t);
+    if (SM == STASH_V1 && last) {
+      // compact stash: V_1 (the value entering step 0), rows 4g..4g+3 of column c
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (pbase + q < P) {
+          float* vp = kstash + (pid[q] * 16 + 4 * g) * 16 + c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vp[r * 16] = Vc[q][r];
+        }
+      }
+    }
     vbeta[c] = my_beta;
     valpha[c] = my_alpha;
     vq[c] = my_q;
@@ -207,7 +218,7 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
 #pragma unroll
       for (int k = 0; k < 16; ++k) wr[k] *= be[k];
     }
-    if (STASH && last && own_valid) st_global_row<16>(q0stash + (po * 16 + c) * 16, qr);
+    if (SM != STASH_NONE && last && own_valid) st_global_row<16>(q0stash + (po * 16 + c) * 16, qr);
     if constexpr (NEED_K) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) ir[k] = (k == c) ? 1.0f : 0.0f;
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
           const bool qvalid = pbase + q < P;
 #pragma unroll
           for (int r = 0; r < 4; ++r) kt[r] *= -acol;  // K[4g+r][c]
-          if (STASH && qvalid) {
+          if (SM == STASH_GAINS && qvalid) {
             float* kp = kstash + ((pid[q] * T + t) * 16 + 4 * g) * 16 + c;
 #pragma unroll
             for (int r = 0; r < 4; ++r) kp[r * 16] = kt[r];
@@ -291,7 +302,7 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
 
   int t_fb = -1;  // step at which the wave switched to the row-layout sweep
   for (int t = T - 1; t >= 0; --t) {
-    const bool ok = (STASH || t == 0) ? step(std::true_type{}, t) : step(std::false_type{}, t);
+    const bool ok = (SM == STASH_GAINS || t == 0) ? step(std::true_type{}, t) : step(std::false_type{}, t);
     if (!ok) {
       t_fb = t;
       break;
@@ -312,7 +323,7 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
 #pragma unroll
     for (int m = 0; m < 16; ++m) fb[m * Geo<16>::LDM + c] = bn[m * 16 + c];
     wave_sync();
-    rpl_sweep<16, float, STASH, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, fb, fb + Geo<16>::MAT, c, po,
+    rpl_sweep<16, float, SM, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, fb, fb + Geo<16>::MAT, c, po,
                                          own_valid, po / H, T, t_fb, V, u_out, kstash, q0stash, status);
   }
 }

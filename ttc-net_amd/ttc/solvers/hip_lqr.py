@@ -15,8 +15,14 @@ Differences from the reference, by design:
   {16, 32, 64}; other sizes are zero-padded here (padded states start at 0 and
   are neither driven nor costed; padded controls act on nothing and cost
   ``u^2/2``), which leaves the solution unchanged.
-* the backward recomputes the feedback gains in bounded-memory chunks unless the
-  forward kept them ("stash"), see ``TTC_LQR_STASH`` below.
+* backward: the forward keeps a small stash per problem (``V_1``, the step-1 value
+  matrix, and ``Quu_0``; d^2 + du^2 floats) and the backward rolls the optimal
+  primal and adjoint trajectories forward with the Hamiltonian recursion, as the
+  reference's fused backward does (``symplectic_iter.py:542-885``), but every
+  problem is certified (the terminal condition ``lambda_T = Q_f h_T`` must hold to
+  ``TTC_LQR_CERT_TOL``) and problems that fail are recomputed by the stable path
+  (per-step gains, closed-loop costates).  ``stable_backward=True`` uses the stable
+  path for every problem.
 * ``precision``: the Riccati sweep (the feedback gains) runs in fp32 or fp64.
   ``"auto"`` (default) picks fp64 for horizons ``T >= FP64_HORIZON`` (512): on long,
   barely discounted horizons the value matrix reaches ~1e17 and fp32 rounding
@@ -26,27 +32,32 @@ Differences from the reference, by design:
   the vector-ALU row-layout kernel instead.
 
 Environment knobs:
-``TTC_LQR_STASH`` = ``auto`` (default: keep the gains from the forward when they
-fit in half of the device memory free at forward time (free on the device plus
+``TTC_LQR_STASH`` = ``auto`` (default: keep the stash from the forward when it fits
+in half of the device memory available at forward time (free on the device plus
 held unallocated by torch's caching allocator), capped by
-``TTC_LQR_STASH_MAX_BYTES`` if set) | ``always`` | ``never``.
+``TTC_LQR_STASH_MAX_BYTES`` if set) | ``always`` | ``never`` (the backward then
+recomputes it with one forward sweep).
 ``TTC_LQR_WORKSPACE_BYTES``: backward workspace per call (default 4 GiB).
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 
 import torch
 
-from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL
+from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD
 
-__all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "padded_dim", "SUPPORTED_DIMS"]
+__all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "padded_dim", "SUPPORTED_DIMS", "last_backward_stats"]
 
 SUPPORTED_DIMS = (16, 32, 64)
 FP64_HORIZON = 512
 _FWD_MSG = "Numerical instability detected during fused LQR forward recurrence."
 _BWD_MSG = "Numerical instability detected during fused LQR backward pass."
+
+# problems / fallback problems of the most recent backward call (observability)
+last_backward_stats = {"problems": 0, "fallback": 0}
 
 
 def padded_dim(d: int, du: int) -> int:
@@ -118,7 +129,8 @@ class HipLQRSolveFunc(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T: int,
-                grad_limit: float = 1e6, stash: str | None = None, precision: str = "auto"):
+                grad_limit: float = 1e6, stash: str | None = None, precision: str = "auto",
+                stable_backward: bool = False):
         ins = [A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0]
         assert all(x.is_cuda for x in ins), "hip LQR solver inputs must be on a GPU"
         bs, nh, d = A_diag.shape
@@ -140,29 +152,26 @@ class HipLQRSolveFunc(torch.autograd.Function):
         flags = riccati_flags(precision, T, Dp)
         f32 = [x.detach().to(torch.float32).contiguous() for x in ins]
         f32 = _pad_inputs(f32, d, du, Dp)
-        P = bs * nh
         u = torch.empty(bs, nh, Dp, device=dev, dtype=torch.float32)
         status = torch.zeros(1, device=dev, dtype=torch.int32)
 
         policy = stash or os.environ.get("TTC_LQR_STASH", "auto")
+        assert policy in ("auto", "always", "never"), f"unknown stash policy {policy}"
         need_grad = any(ctx.needs_input_grad[:9])
         stash_bytes = lib.ttc_lqr_stash_bytes(bs, nh, Dp, Dp, T)
-        keep = need_grad and bs > 0 and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev)))
-        if keep:
-            st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32)
-            kst, q0s = st[: P * T * Dp * Dp], st[P * T * Dp * Dp:]
-        else:
-            st = kst = q0s = None
+        keep = (need_grad and bs > 0 and not stable_backward
+                and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev))))
+        st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32) if keep else None
         with torch.cuda.device(dev):
             rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, flags, u.data_ptr(),
-                                     None if kst is None else kst.data_ptr(),
-                                     None if q0s is None else q0s.data_ptr(),
-                                     status.data_ptr(), _stream_handle(dev))
+                                     None if st is None else st.data_ptr(), status.data_ptr(), _stream_handle(dev))
         check(rc, "ttc_lqr_forward")
         if int(status.item()) != 0:
             raise RuntimeError(_FWD_MSG)
-        ctx.save_for_backward(*f32, *( [st] if st is not None else []))
-        ctx.meta = (bs, nh, d, du, Dp, T, float(grad_limit), st is not None, [x.dtype for x in ins], flags)
+        if need_grad:
+            ctx.save_for_backward(*f32, u, *([st] if st is not None else []))
+        ctx.meta = (bs, nh, d, du, Dp, T, float(grad_limit), st is not None, [x.dtype for x in ins],
+                    flags | (FLAG_STABLE_BWD if stable_backward else 0))
         return u[..., :du].to(out_dtype)
 
     @staticmethod
@@ -170,9 +179,9 @@ class HipLQRSolveFunc(torch.autograd.Function):
         bs, nh, d, du, Dp, T, grad_limit, has_stash, dtypes, flags = ctx.meta
         saved = ctx.saved_tensors
         f32 = list(saved[:9])
-        st = saved[9] if has_stash else None
+        u = saved[9]
+        st = saved[10] if has_stash else None
         dev = f32[0].device
-        P = bs * nh
         dU = torch.zeros(bs, nh, Dp, device=dev, dtype=torch.float32)
         dU[..., :du] = d_u.to(torch.float32)
         g = {
@@ -183,36 +192,36 @@ class HipLQRSolveFunc(torch.autograd.Function):
             "h0": torch.empty(bs, nh, Dp, device=dev),
         }
         status = torch.zeros(1, device=dev, dtype=torch.int32)
-        if st is not None:
-            kst, q0s = st[: P * T * Dp * Dp], st[P * T * Dp * Dp:]
-        else:
-            kst = q0s = None
         budget = _env_bytes("TTC_LQR_WORKSPACE_BYTES", 4 << 30)
-        per_tok = lib.ttc_lqr_workspace_bytes(1, nh, Dp, Dp, T, 1 if st is not None else 0)
-        chunk = max(1, min(bs, budget // max(per_tok, 1)))
-        ws_bytes = lib.ttc_lqr_workspace_bytes(chunk, nh, Dp, Dp, T, 1 if st is not None else 0)
+        with_st = 1 if st is not None else 0
+        # one pass over all tokens when it fits the budget; the library picks the largest
+        # token chunk that fits whatever it is given (at least one token's worth)
+        full = lib.ttc_lqr_workspace_bytes(bs, nh, Dp, Dp, T, with_st)
+        ws_bytes = max(min(full, budget), lib.ttc_lqr_workspace_bytes(1, nh, Dp, Dp, T, with_st))
         ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
+        n_fb = ctypes.c_int64(0)
         with torch.cuda.device(dev):
             rc = lib.ttc_lqr_backward(
-                *[t.data_ptr() for t in f32], dU.data_ptr(), bs, nh, Dp, Dp, T, flags,
-                None if kst is None else kst.data_ptr(), None if q0s is None else q0s.data_ptr(),
+                *[t.data_ptr() for t in f32], u.data_ptr(), dU.data_ptr(), bs, nh, Dp, Dp, T, flags,
+                None if st is None else st.data_ptr(),
                 g["A"].data_ptr(), g["B"].data_ptr(), g["Q"].data_ptr(), g["R"].data_ptr(), g["Qf"].data_ptr(),
                 g["lA"].data_ptr(), g["lB"].data_ptr(), g["lQ"].data_ptr(), g["h0"].data_ptr(),
-                ws.data_ptr(), ws.numel(), limit, status.data_ptr(), _stream_handle(dev))
+                ws.data_ptr(), ws.numel(), limit, status.data_ptr(), ctypes.byref(n_fb), _stream_handle(dev))
         check(rc, "ttc_lqr_backward")
+        last_backward_stats.update(problems=bs * nh, fallback=int(n_fb.value))
         if int(status.item()) != 0:
             raise RuntimeError(_BWD_MSG)
         out = (g["A"][..., :d], g["B"][:, :d, :du], g["Q"][:, :d, :d], g["R"][..., :du], g["Qf"][:, :, :d, :d],
                g["lA"], g["lB"][..., :du], g["lQ"][..., :d], g["h0"][..., :d])
         out = tuple(o.to(dt) if need else None for o, dt, need in zip(out, dtypes, ctx.needs_input_grad[:9]))
-        return out + (None, None, None, None)
+        return out + (None, None, None, None, None)
 
 
 def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_diag: torch.Tensor,
                   Q_f: torch.Tensor, log_gamma_A: torch.Tensor, log_gamma_B: torch.Tensor,
                   log_gamma_Q: torch.Tensor, h0: torch.Tensor, T: int, grad_limit: float = 1e6,
-                  stash: str | None = None, precision: str = "auto") -> torch.Tensor:
+                  stash: str | None = None, precision: str = "auto", stable_backward: bool = False) -> torch.Tensor:
     """First optimal action ``u [N,H,du]`` of every (token, head) LQR problem.
 
     Drop-in for the reference ``fused_lqr_solve`` (``fused_lqr.py:294-304``).
@@ -221,6 +230,8 @@ def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_
     ``stash``: ``"auto" | "always" | "never"`` overrides ``TTC_LQR_STASH``.
     ``precision``: ``"auto" | "fp32" | "fp32-row" | "fp64"`` arithmetic (and, for
     ``"fp32-row"``, kernel) of the Riccati sweep; see ``riccati_flags``.
+    ``stable_backward``: skip the certified Hamiltonian rollout and compute every
+    problem's gradients with the stable path.
     """
     return HipLQRSolveFunc.apply(A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T,
-                                 grad_limit, stash, precision)
+                                 grad_limit, stash, precision, stable_backward)
