@@ -1,32 +1,42 @@
 // ttc_lqr_mfma16.cuh -- d = du = 16 forward kernel with the per-step products on
 // the matrix cores (v_mfma_f32_16x16x4f32).
 //
-// One wave holds 4 LQR problems (q = 0..3).  Per Riccati step and problem:
-//   W~ = V B,  G = B' W~                 8 MFMA, operands straight from registers
-//   Quu = diag(b) G diag(b) + diag(1/r),  W = W~ diag(b)
-//   right-looking Cholesky of Quu applied to the rows of [Quu; W; I]  (row layout)
-//     -> M = W L^{-T} and U = L^{-T}
-//   S = M M'                             4 MFMA
-//   V <- diag(a) (V - S) diag(a) + diag(q) Q diag(q)
-//   K = -Quu^{-1} Qux = -U M' diag(a)    4 MFMA (only when the gains are stored, and at t = 0)
+// One wave holds 4 LQR problems (q = 0..3).  The registers carry the negated value
+// matrix N = -V (so that no step needs a separate negation).  Per Riccati step and
+// problem:
+//   B_k = B diag(beta_k)                  4 VALU multiplies (the MFMA operand, scaled)
+//   -W = N B_k,  -Quu = B_k'(-W) - R      8 MFMA (-R enters as the accumulator)
+//   Cholesky-scaled elimination of -Quu applied to the rows of [-Quu; -W; I]
+//     (row layout, fused DPP updates)  ->  -M = -W L^{-T},  U = L^{-T}
+//   N + M M' = -(V - W Quu^{-1} W')       4 MFMA (N enters as the accumulator)
+//   N <- diag(a) (N + M M') diag(a) - diag(q) Q diag(q)
+//   K = -Quu^{-1} Qux = U (-M)' diag(a)   4 MFMA (stored steps and t = 0 only)
+// M M' is formed as a product of one operand with itself, so the value matrix stays
+// exactly symmetric; an unsymmetric split such as (W L'^{-T} D^{-1})(W L'^{-T})'
+// drifts and loses long-horizon stress problems.
+//
+// On gfx950 the fp32 matrix core and the vector ALU do not overlap (a measured
+// property of this part: the time of a loop is the sum of both), so the design
+// minimises vector instructions: the step scalings are folded into MFMA operands and
+// accumulators and the elimination multiplies are DPP-fused (ttc_lqr_elim16.h).
 //
 // Matrix-core layout of a 16x16 tile X (the MFMA C/D layout): lane 16g + c holds
 // X[4g + r][c], r = 0..3.  Each MFMA sums over k = 4g + s in lane group g (s = the
 // instruction index), so the A operand of lane (g, c) is X[c][4g + s] and the B
-// operand is Y[4g + s][c].  With V symmetric, V[c][4g + s] is the lane's own
-// V[4g + s][c]; the MFMA result W~[4g + s][c] is again the lane's own register, so
-// V -> W~ -> G never leaves the registers.  The row layout (lane (g, c) owns row c of
-// problem g) is reached through wave-private LDS.
+// operand is Y[4g + s][c].  With N symmetric, N[c][4g + s] is the lane's own
+// N[4g + s][c]; the MFMA result W[4g + s][c] is again the lane's own register, so
+// N -> W -> Quu never leaves the registers.  The row layout (lane (g, c) owns row c
+// of problem g) is reached through wave-private LDS.
 //
-// Cholesky breakdown guard: in exact arithmetic every pivot of Quu = R + B'VB is at
-// least min_j 1/R_inv_j (Quu >= R).  A pivot below half of that, or not finite, means
-// fp32 rounding has made V indefinite; the wave then leaves the matrix-core loop and
-// redoes this step and all remaining ones with the row-layout sweep (partially pivoted
-// Gauss-Jordan on [Quu | Qux], rpl_sweep).  Keeping the two phases apart keeps their
-// register footprints from adding up.
+// Breakdown guard: in exact arithmetic every pivot of Quu = R + B'VB is at least
+// min_j 1/R_inv_j (Quu >= R).  A pivot below half of that, or not finite, means fp32
+// rounding has made V indefinite; the wave then leaves the matrix-core loop and redoes
+// this step and all remaining ones with the row-layout sweep (partially pivoted
+// Gauss-Jordan on [Quu | Qux], rpl_sweep).
 #pragma once
 #include <utility>
 
+#include "ttc_lqr_elim16.h"
 #include "ttc_lqr_kernels.cuh"
 
 namespace ttc {
@@ -34,15 +44,21 @@ namespace ttc {
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 struct M16 {
-  static constexpr int LD = 20;                      // LDS row stride of a 16x16 tile (floats)
-  static constexpr int MAT = 16 * LD;                // 320 floats
-  static constexpr int OFF_B = MAT;                  // tile A at 0, tile B at MAT
-  static constexpr int OFF_VEC = 2 * MAT;            // beta, alpha, q (16 each), pivot row (32)
-  static constexpr int PER_PROB = OFF_VEC + 80 + 4;  // +4: bank skew between problems
-  static constexpr int THREADS = 64;                 // one wave per block
+  static constexpr int LD = 20;                 // LDS row stride of a 16x16 tile (floats)
+  static constexpr int MAT = 16 * LD;           // 320 floats
+  static constexpr int OFF_A = 0;               // -Quu
+  static constexpr int OFF_B = MAT;             // -W, then -M
+  static constexpr int OFF_U = 2 * MAT;         // U (steps that form the gains), else V for the fallback
+  static constexpr int PER_PROB = 3 * MAT + 4;  // +4: bank skew between problems
+  static constexpr int THREADS = 64;            // one wave per block
   // row-layout fallback: per problem B (Geo<16>::MAT) + rpl_sweep scratch (Geo<16>::PER_PROB)
   static constexpr int FB_PER_PROB = Geo<16>::MAT + Geo<16>::PER_PROB;
-  static constexpr int LDS_FLOATS = 4 * (PER_PROB > FB_PER_PROB ? PER_PROB : FB_PER_PROB);
+  static_assert(FB_PER_PROB <= PER_PROB, "fallback scratch must fit the tile region");
+  // per-step vectors alpha, beta, q of the 4 problems, as [q][i] (row reads) and [i][q]
+  // (column reads)
+  static constexpr int OFF_VEC = 4 * PER_PROB;
+  static constexpr int VEC = 64;
+  static constexpr int LDS_FLOATS = OFF_VEC + 5 * VEC;
   static constexpr size_t LDS_BYTES = LDS_FLOATS * sizeof(float);
 };
 
@@ -85,15 +101,6 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-// Pin a row of registers at this program point.  Keeps the compiler from sinking the
-// Cholesky updates of the W / I rows into the branch that consumes them, which would
-// keep every broadcast pivot row alive at once.
-template <int N>
-__device__ __forceinline__ void pin_row(float (&r)[N]) {
-#pragma unroll
-  for (int i = 0; i < N; i += 4) asm volatile("" : "+v"(r[i]), "+v"(r[i + 1]), "+v"(r[i + 2]), "+v"(r[i + 3]));
-}
-
 __device__ __forceinline__ v4f ld4(const float* p) {
   const float4 v = *reinterpret_cast<const float4*>(p);
   return v4f{v.x, v.y, v.z, v.w};
@@ -103,13 +110,14 @@ __device__ __forceinline__ void st4(float* p, v4f v) {
 }
 
 template <int SM, bool WRITE_U>
-__global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
+__global__ __launch_bounds__(M16::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void lqr_fwd16_mfma_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
     int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
     float* __restrict__ q0stash, int* __restrict__ status) {
   extern __shared__ __align__(16) float sm[];
+  constexpr float kLog2e = 1.4426950408889634f;
   const int lane = threadIdx.x;
   const int g = lane >> 4;  // lane group: MFMA row block, and "my problem" in the row layout
   const int c = lane & 15;  // MFMA column, and "my row" in the row layout
@@ -124,47 +132,59 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
   }
   const bool own_valid = pbase + g < P;
   const int64_t po = pid[g];
-  float* own = sm + g * M16::PER_PROB;
-  float* vbeta = own + M16::OFF_VEC;
-  float* valpha = vbeta + 16;
-  float* vq = valpha + 16;
-  float* vpr = vq + 16;  // 32 floats
+  float* own = sm + g * M16::PER_PROB;  // (not buf[g]: a dynamically indexed pointer loses its LDS address space)
+  float* vA = sm + M16::OFF_VEC;  // alpha [q][i]
+  float* vQ = vA + M16::VEC;      // q     [q][i]
+  float* vAT = vQ + M16::VEC;     // alpha [i][q]
+  float* vBT = vAT + M16::VEC;    // beta  [i][q]
+  float* vQT = vBT + M16::VEC;    // q     [i][q]
 
+  // discount exponents in base 2: exp(l * n) = exp2(l * log2(e) * n)
   const float a_c = A_diag[po * 16 + c];
-  const float lgB_c = lgB[po * 16 + c];
-  const float lgQ_c = lgQ[po * 16 + c];
-  const float lgA_o = lgA[po];
+  const float lb2_c = lgB[po * 16 + c] * kLog2e;
+  const float lq2_c = lgQ[po * 16 + c] * kLog2e;
+  const float la2_o = lgA[po] * kLog2e;
   const float piv_floor = 0.5f * row16_min(1.0f / Rinv[po * 16 + c]);
 
-  float Bop[4][4];  // B_q[4g+s][c]: B operand of V B, A operand (B') of B' W~
-  float Qc[4][4];   // sym(Q_q)[4g+r][c]
-  v4f Vc[4];        // V_q[4g+r][c]
-  float rrc[4];     // 1/R_inv_q[c]
+  float Bop[4][4];  // B_q[4g+s][c]: B operand of N B, A operand (B') of B' W
+  float Qn[4][4];   // -sym(Q_q)[4g+r][c]
+  v4f Nc[4];        // N_q[4g+r][c] = -V_q[4g+r][c]
+  v4f dR[4];        // -R_q = -diag(1/R_inv_q) in the tile layout (the -Quu accumulator)
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int64_t n = pid[q] / H;
     const float* bq = Bg + n * 256;
     const float* qq = Qg + n * 256;
     const float* fq = Qf + pid[q] * 256;
+    const float rr = 1.0f / Rinv[pid[q] * 16 + c];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int i = 4 * g + s;
       Bop[q][s] = bq[i * 16 + c];
-      Qc[q][s] = 0.5f * (qq[i * 16 + c] + qq[c * 16 + i]);
-      Vc[q][s] = 0.5f * (fq[i * 16 + c] + fq[c * 16 + i]);
+      Qn[q][s] = -0.5f * (qq[i * 16 + c] + qq[c * 16 + i]);
+      Nc[q][s] = -0.5f * (fq[i * 16 + c] + fq[c * 16 + i]);
+      dR[q][s] = (i == c) ? -rr : 0.0f;
     }
-    rrc[q] = 1.0f / Rinv[pid[q] * 16 + c];
   }
 
   // One Riccati step; NEED_K: also form the gains K_t (stored steps, and t = 0 for u0).
-  // Returns false when the Cholesky guard fired (nothing of the step was kept).
+  // Returns true when the breakdown guard fired.  V entering the step is then in tile U
+  // for the row-layout sweep; the registers may hold garbage (steps without gains run to
+  // their end regardless, which keeps their loop a single-exit loop).
   auto step = [&](auto need_k_c, const int t) -> bool {
     constexpr bool NEED_K = decltype(need_k_c)::value;
     const bool last = NEED_K && t == 0;
     const float tp1 = (float)(t + 1);
-    const float my_beta = expf(lgB_c * tp1);
-    const float my_alpha = fmaf(a_c, expf(lgA_o * tp1), 1.0f);
-    const float my_q = last ? 0.0f : expf(lgQ_c * (float)t);
+    {
+      const float beta = __builtin_amdgcn_exp2f(lb2_c * tp1);
+      const float alpha = fmaf(a_c, __builtin_amdgcn_exp2f(la2_o * tp1), 1.0f);
+      const float qd = last ? 0.0f : __builtin_amdgcn_exp2f(lq2_c * (float)t);
+      vA[g * 16 + c] = alpha;
+      vQ[g * 16 + c] = qd;
+      vAT[c * 4 + g] = alpha;
+      vBT[c * 4 + g] = beta;
+      vQT[c * 4 + g] = qd;
+    }
     if (SM == STASH_V1 && last) {
       // compact stash: V_1 (the value entering step 0), rows 4g..4g+3 of column c
 #pragma unroll
@@ -172,53 +192,49 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
         if (pbase + q < P) {
           float* vp = kstash + (pid[q] * 16 + 4 * g) * 16 + c;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) vp[r * 16] = Vc[q][r];
+          for (int r = 0; r < 4; ++r) vp[r * 16] = -Nc[q][r];
         }
       }
     }
-    vbeta[c] = my_beta;
-    valpha[c] = my_alpha;
-    vq[c] = my_q;
+    if constexpr (!NEED_K) {
+      // N entering the step, for the row-layout sweep should this step break down
+      // (tile U is unused by steps that do not form the gains)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) st4(buf[q] + M16::OFF_U + c * M16::LD + 4 * g, Nc[q]);
+    }
+    wave_sync();
+    const v4f bcol = ld4(vBT + c * 4);  // beta_q[c], q = 0..3
 
-    // ---- W~ = V B -> tile B (row-major);  G = B' W~ ---------------------------------
-    v4f Gq[4];
+    // ---- -W = N B_k -> tile B (row-major);  -Quu = B_k'(-W) - R -> tile A ----------------
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
+      float bk[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) bk[s] = Bop[q][s] * bcol[q];
       v4f w = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) w = mfma16x16x4(Vc[q][s], Bop[q][s], w);
+      for (int s = 0; s < 4; ++s) w = mfma16x16x4(Nc[q][s], bk[s], w);
 #pragma unroll
       for (int r = 0; r < 4; ++r) buf[q][M16::OFF_B + (4 * g + r) * M16::LD + c] = w[r];
-      v4f gg = v4f{0.f, 0.f, 0.f, 0.f};
+      v4f quu = dR[q];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) gg = mfma16x16x4(Bop[q][s], w[s], gg);
-      Gq[q] = gg;
-    }
-    wave_sync();
-    // ---- Quu = diag(b) G diag(b) + diag(1/r): column fragment = row fragment -> tile A
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float* bv = buf[q] + M16::OFF_VEC;
-      const v4f brow = ld4(bv + 4 * g);
-      const float bcol = bv[c];
-      v4f quu;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) quu[r] = fmaf(brow[r] * bcol, Gq[q][r], (4 * g + r == c) ? rrc[q] : 0.f);
-      st4(buf[q] + c * M16::LD + 4 * g, quu);
+      for (int s = 0; s < 4; ++s) quu = mfma16x16x4(bk[s], w[s], quu);
+      st4(buf[q] + M16::OFF_A + c * M16::LD + 4 * g, quu);  // symmetric: column fragment = row fragment
     }
     wave_sync();
 
-    // ---- row layout: Cholesky of Quu on the rows [Quu; W; I] ---------------------------
+    // ---- row layout: elimination on the rows [-Quu; -W; I] -----------------------------
+    // Pivot k of -Quu is -d_k (d_k > 0 the pivot of Quu); every row x is updated with the
+    // multiplier x[k] / d_k, and column k of the -W rows is scaled by 1/sqrt(d_k) once final.
     float qr[16], wr[16], ir[16];
-    {
-      float be[16];
-      ld_row<16>(own + c * M16::LD, qr);
-      ld_row<16>(own + M16::OFF_B + c * M16::LD, wr);
-      ld_row<16>(vbeta, be);
+    ld_row<16>(own + M16::OFF_A + c * M16::LD, qr);
+    ld_row<16>(own + M16::OFF_B + c * M16::LD, wr);
+    if (SM != STASH_NONE && last && own_valid) {
+      float quu_row[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) wr[k] *= be[k];
+      for (int k = 0; k < 16; ++k) quu_row[k] = -qr[k];
+      st_global_row<16>(q0stash + (po * 16 + c) * 16, quu_row);
     }
-    if (SM != STASH_NONE && last && own_valid) st_global_row<16>(q0stash + (po * 16 + c) * 16, qr);
     if constexpr (NEED_K) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) ir[k] = (k == c) ? 1.0f : 0.0f;
@@ -226,105 +242,117 @@ __global__ __launch_bounds__(M16::THREADS) void lqr_fwd16_mfma_kernel(
     bool bad = false;
     static_for<16>([&](auto kc) {
       constexpr int k = decltype(kc)::value;
-      // row k of my problem's trailing matrix, broadcast from lane (g, k) by DPP
-      const float piv = bcast16<k>(qr[k]);
-      bad |= !(piv >= piv_floor);  // also catches NaN
-      const float rs = rsqrtf(fmaxf(piv, 1e-30f));
+      // pivot: diagonal entry k of the trailing matrix, held by lane (g, k)
+      const float npiv = bcast16<k>(qr[k]);  // -d_k
+      bad |= !(-npiv >= piv_floor);          // also catches NaN
+      const float rs = __builtin_amdgcn_rsqf(-npiv);  // raw v_rsq_f32 (pivots are >= piv_floor, never denormal)
       const float ip = rs * rs;
-      const float fq = qr[k] * ip;
-      const float fw = wr[k] * ip;
-      const float fi = NEED_K ? ir[k] * ip : 0.f;
-      wr[k] *= rs;  // M[c][k]
+      const float nw = wr[k] * ip;
+      float ni = 0.f;
+      if constexpr (NEED_K) ni = ir[k] * ip;
+      if constexpr (k < 15) {
+        const float nq = qr[k] * ip;
+        if constexpr (NEED_K)
+          Elim16<k>::qwi(qr, wr, ir, nq, nw, ni);
+        else
+          Elim16<k>::qw(qr, wr, nq, nw);
+      }
+      wr[k] *= rs;                        // -M[c][k]
       if constexpr (NEED_K) ir[k] *= rs;  // U[c][k]
-#pragma unroll
-      for (int m = k + 1; m < 16; ++m) {
-        const float pm = bcast16<k>(qr[m]);
-        qr[m] = fmaf(-fq, pm, qr[m]);
-        wr[m] = fmaf(-fw, pm, wr[m]);
-        if constexpr (NEED_K) ir[m] = fmaf(-fi, pm, ir[m]);
-      }
-      pin_row(wr);
-      if constexpr (NEED_K) pin_row(ir);
     });
-    if (__any(bad)) return false;
-    {
-      // ---- M rows -> tile A, U rows -> tile B; S = M M', K = -U M' diag(a) -------------
-      st_row<16>(own + c * M16::LD, wr);
-      if constexpr (NEED_K) st_row<16>(own + M16::OFF_B + c * M16::LD, ir);
-      wave_sync();
+    const bool failed = __any(bad);
+    if constexpr (NEED_K) {
+      if (failed) {
+        // hand N (unchanged by this step) to the row-layout sweep through tile U
+        wave_sync();
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const v4f m4 = ld4(buf[q] + c * M16::LD + 4 * g);  // M[c][4g+s]
-        const float* av = buf[q] + M16::OFF_VEC + 16;
-        const float acol = av[c];
-        if constexpr (NEED_K) {
-          const v4f u4 = ld4(buf[q] + M16::OFF_B + c * M16::LD + 4 * g);  // U[c][4g+s]
-          v4f kt = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int s = 0; s < 4; ++s) kt = mfma16x16x4(u4[s], m4[s], kt);
-          const bool qvalid = pbase + q < P;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) kt[r] *= -acol;  // K[4g+r][c]
-          if (SM == STASH_GAINS && qvalid) {
-            float* kp = kstash + ((pid[q] * T + t) * 16 + 4 * g) * 16 + c;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) kp[r * 16] = kt[r];
-          }
-          if (last) {
-            // u0[4g+r] = sum_c K[4g+r][c] h0[c]
-            const float hc = h0[pid[q] * 16 + c];
-            v4f u;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) u[r] = row16_sum(kt[r] * hc);
-            if (c == 0 && qvalid) {
-              if (WRITE_U) st4(u_out + pid[q] * 16 + 4 * g, u);
-              if (status != nullptr && !(isfinite(u[0]) && isfinite(u[1]) && isfinite(u[2]) && isfinite(u[3])))
-                atomicOr(status, TTC_LQR_STATUS_NONFINITE);
-            }
-            continue;
-          }
-        }
-        v4f S = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) S = mfma16x16x4(m4[s], m4[s], S);
-        const float* qvv = buf[q] + M16::OFF_VEC + 32;
-        const v4f arow = ld4(av + 4 * g);
-        const v4f qrow4 = ld4(qvv + 4 * g);
-        const float qcol = qvv[c];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          Vc[q][r] = fmaf(arow[r] * acol, Vc[q][r] - S[r], (qrow4[r] * qcol) * Qc[q][r]);
+        for (int q = 0; q < 4; ++q) st4(buf[q] + M16::OFF_U + c * M16::LD + 4 * g, Nc[q]);
+        wave_sync();
+        return true;
       }
-      wave_sync();
     }
-    return true;
+    st_row<16>(own + M16::OFF_B + c * M16::LD, wr);  // -M rows
+    if constexpr (NEED_K) st_row<16>(own + M16::OFF_U + c * M16::LD, ir);  // U rows
+    wave_sync();
+
+    // ---- N + M M' (N as accumulator);  K = U (-M)' diag(a) -----------------------------
+    const v4f acol = ld4(vAT + c * 4);  // alpha_q[c]
+    const v4f qcol = ld4(vQT + c * 4);  // q_q[c]
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const v4f m4 = ld4(buf[q] + M16::OFF_B + c * M16::LD + 4 * g);  // -M[c][4g+s]
+      if constexpr (NEED_K) {
+        const v4f u4 = ld4(buf[q] + M16::OFF_U + c * M16::LD + 4 * g);  // U[c][4g+s]
+        v4f kt = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) kt = mfma16x16x4(u4[s], m4[s], kt);
+        const bool qvalid = pbase + q < P;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) kt[r] *= acol[q];  // K[4g+r][c]
+        if (SM == STASH_GAINS && qvalid) {
+          float* kp = kstash + ((pid[q] * T + t) * 16 + 4 * g) * 16 + c;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) kp[r * 16] = kt[r];
+        }
+        if (last) {
+          // u0[4g+r] = sum_c K[4g+r][c] h0[c]
+          const float hc = h0[pid[q] * 16 + c];
+          v4f u;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) u[r] = row16_sum(kt[r] * hc);
+          if (c == 0 && qvalid) {
+            if (WRITE_U) st4(u_out + pid[q] * 16 + 4 * g, u);
+            if (status != nullptr && !(isfinite(u[0]) && isfinite(u[1]) && isfinite(u[2]) && isfinite(u[3])))
+              atomicOr(status, TTC_LQR_STATUS_NONFINITE);
+          }
+          continue;
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) Nc[q] = mfma16x16x4(m4[s], m4[s], Nc[q]);  // N + M M', in place
+      const v4f arow = ld4(vA + q * 16 + 4 * g);
+      const v4f qrow = ld4(vQ + q * 16 + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Nc[q][r] = fmaf(arow[r] * acol[q], Nc[q][r], (qrow[r] * qcol[q]) * Qn[q][r]);
+    }
+    wave_sync();
+    return failed;
   };
 
-  int t_fb = -1;  // step at which the wave switched to the row-layout sweep
-  for (int t = T - 1; t >= 0; --t) {
-    const bool ok = (SM == STASH_GAINS || t == 0) ? step(std::true_type{}, t) : step(std::false_type{}, t);
-    if (!ok) {
-      t_fb = t;
-      break;
-    }
-  }
-
-  if (t_fb >= 0) {
-    // ---- row-layout fallback from step t_fb: V rows (V symmetric, so the lane's column
-    // fragment is a row fragment), then B of my problem, then rpl_sweep -------------------
-#pragma unroll
-    for (int q = 0; q < 4; ++q) st4(buf[q] + c * M16::LD + 4 * g, Vc[q]);
-    wave_sync();
+  // Row-layout sweep from step t_fb down to 0 after a breakdown at step t_fb: V rows (N in
+  // tile U, stored by the failed step; N is symmetric, so the lane's column fragment is a
+  // row fragment), then B of my problem, then rpl_sweep.
+  auto row_sweep_from = [&](const int t_fb) {
     float V[16];
-    ld_row<16>(own + c * M16::LD, V);
+    ld_row<16>(own + M16::OFF_U + c * M16::LD, V);  // N rows
+#pragma unroll
+    for (int m = 0; m < 16; ++m) V[m] = -V[m];
     wave_sync();
-    float* fb = sm + g * M16::FB_PER_PROB;
+    float* fb = own;
     const float* bn = Bg + (po / H) * 256;
 #pragma unroll
     for (int m = 0; m < 16; ++m) fb[m * Geo<16>::LDM + c] = bn[m * 16 + c];
     wave_sync();
     rpl_sweep<16, float, SM, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, fb, fb + Geo<16>::MAT, c, po,
-                                         own_valid, po / H, T, t_fb, V, u_out, kstash, q0stash, status);
+                                      own_valid, po / H, T, t_fb, V, u_out, kstash, q0stash, status);
+  };
+
+  if constexpr (SM == STASH_GAINS) {
+    for (int t = T - 1; t >= 0; --t) {
+      if (step(std::true_type{}, t)) {
+        row_sweep_from(t);
+        return;
+      }
+    }
+  } else {
+    // gains are formed only at t = 0: peel that step; the loop has a single exit
+    int t = T - 1;
+    bool failed = false;
+    while (!failed && t >= 1) {
+      failed = step(std::false_type{}, t);
+      t -= failed ? 0 : 1;
+    }
+    if (failed || step(std::true_type{}, 0)) row_sweep_from(t);
   }
 }
 
