@@ -121,6 +121,53 @@ def test_config4_layer_slice(precision):
     check_case("cfg4", layer_solver_inputs(4, x), c["T"], precision=precision)
 
 
+@pytest.mark.parametrize("cfg,n_tok,precision", [(3, 3, "fp32-row"), (4, 2, "fp32-row")])
+def test_wide_configs_row_kernel(cfg, n_tok, precision):
+    """d = 64 / 32 through the row-layout kernel: an independent cross-check of the
+    matrix-core kernel that the default precision selects."""
+    x = make_x(cfg, n_tokens=n_tok, seed=8)
+    check_case(f"cfg{cfg}-row", layer_solver_inputs(cfg, x), CONFIGS[cfg]["T"], precision=precision)
+
+
+@pytest.mark.parametrize("d,N,H,T", [(32, 3, 3, 40), (64, 2, 3, 33), (32, 1, 1, 1), (64, 1, 2, 2)])
+@pytest.mark.parametrize("stash", ["always", "never"])
+def test_wide_matrix_core_ragged(d, N, H, T, stash):
+    """d = 32 / 64 matrix-core kernels on the reference's bench distribution with an odd
+    problem count (an idle problem slot in the last d = 32 wave) and short horizons
+    (T = 1: step 0 only)."""
+    check_case(f"mc{d}", bench_solver_inputs(N, H, d, seed=d + T), T, stash=stash, precision="fp32")
+
+
+def _indefinite_wide_inputs(d, mode, seed=2):
+    """d = 32 / 64 inputs whose Cholesky pivot breaks down while the problem stays well
+    conditioned (B orthogonal, so B'B = I and Quu = R + beta^2 V in the step where it
+    happens).  mode "terminal": problem 1 has Q_f = -3 I, so Quu is negative definite
+    from the first step (t = T-1) on.  mode "mid": token 0 has Q = -10 I (barely
+    discounted) and Q_f = 0.1 I, so Quu is positive definite at t = T-1 and negative
+    definite from t = T-2 on.  The matrix-core kernel marks the affected waves and the
+    rescue pass recomputes those problems with the pivoted row-layout sweep.  (Condition
+    numbers of Quu stay below 3; the reference's own fp32 solvers are within 2e-5.)"""
+    ins = bench_solver_inputs(2, 2, d, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    B, _ = torch.linalg.qr(torch.randn(2, d, d, generator=g))
+    lgB = torch.full((2, 2, d), -0.01)
+    A_diag, _, Q, R_inv, Qf, lgA, _, lgQ, h0 = [t.clone() for t in ins]
+    if mode == "terminal":
+        Qf[0, 1] = -3.0 * torch.eye(d)
+    else:
+        Q[0] = -10.0 * torch.eye(d)
+        lgQ[0] = -0.01
+        Qf[0] = 0.1 * torch.eye(d)
+    return [A_diag, B.contiguous(), Q, R_inv, Qf, lgA, lgB, lgQ, h0]
+
+
+@pytest.mark.parametrize("d", [32, 64])
+@pytest.mark.parametrize("mode", ["terminal", "mid"])
+@pytest.mark.parametrize("stash", ["always", "never"])
+def test_wide_indefinite_Quu_rescued(d, mode, stash):
+    check_case(f"indef{d}-{mode}", _indefinite_wide_inputs(d, mode), 6, stash=stash, precision="fp32")
+
+
 @pytest.mark.parametrize("cfg,T", [(5, 64), (5, 1024), ("5b", 1024)])
 def test_config5_stress(cfg, T):
     x = make_x(cfg, n_tokens=4, seed=5)

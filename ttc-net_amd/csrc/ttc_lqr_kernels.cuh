@@ -915,6 +915,73 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
 
 
 // ---------------------------------------------------------------------------
+// Rescue pass after a matrix-core forward: every problem whose marker is NaN (u[p][0],
+// or Quu_0[p][0][0] in the stash when u is not written) is solved again from scratch
+// with the row-layout sweep (pivoted Gauss-Jordan at every step).  The matrix-core
+// kernels mark the problems whose Cholesky pivot broke down; a problem whose genuine
+// result is NaN is recomputed too and keeps its NaN.  Each block of one wave walks the
+// problems in strides of 64: one marker load per lane, a ballot, then PPW = 64 / D
+// marked problems at a time (lane li of group qo owns row li of problem qo).
+// ---------------------------------------------------------------------------
+template <int D>
+struct Rescue {
+  static constexpr int PPW = 64 / D;
+  static constexpr int PER = Geo<D>::MAT + Geo<D>::PER_PROB;  // B rows + rpl_sweep scratch
+  static constexpr size_t LDS_BYTES = sizeof(float) * (size_t)PPW * PER;
+};
+
+template <int D, int SM, bool WRITE_U>
+__global__ __launch_bounds__(64) void lqr_rescue_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
+    float* __restrict__ q0stash, int* __restrict__ status) {
+  constexpr int PPW = Rescue<D>::PPW;
+  extern __shared__ __align__(16) float smem[];
+  const int lane = threadIdx.x;
+  const int qo = lane / D;
+  const int li = lane % D;
+  float* Bs = smem + qo * Rescue<D>::PER;
+  float* S = Bs + Geo<D>::MAT;
+  const float* mark = WRITE_U ? u_out : q0stash;
+  const int64_t mstride = WRITE_U ? D : (int64_t)D * D;
+  for (int64_t base = (int64_t)blockIdx.x * 64; base < P; base += (int64_t)gridDim.x * 64) {
+    const int64_t pl = base + lane;
+    unsigned long long mask = __ballot(pl < P && isnan(mark[pl * mstride]));
+    while (mask != 0ull) {
+      // group qo takes the qo-th marked problem of the mask (if there is one)
+      unsigned long long m = mask;
+      for (int k = 0; k < qo && m != 0ull; ++k) m &= m - 1ull;
+      const bool valid = m != 0ull;
+      const int64_t p = base + (valid ? (__ffsll((long long)m) - 1) : (__ffsll((long long)mask) - 1));
+      for (int k = 0; k < PPW && mask != 0ull; ++k) mask &= mask - 1ull;
+      const int64_t n = p / H;
+      wave_sync();
+#pragma unroll
+      for (int c = 0; c < D; ++c) Bs[li * Geo<D>::LDM + c] = Bg[n * D * D + li * D + c];
+      float V[D];
+      const float* qf = Qf + p * D * D;
+#pragma unroll
+      for (int c = 0; c < D; ++c) V[c] = 0.5f * (qf[li * D + c] + qf[c * D + li]);
+      wave_sync();
+      rpl_sweep<D, float, SM, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, Bs, S, li, p, valid, n, T, T - 1, V,
+                                        u_out, kstash, q0stash, status);
+    }
+  }
+}
+
+template <int D, int SM, bool WU>
+inline void launch_rescue_k(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                            const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
+                            int T, float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
+  int64_t blocks = (P + 63) / 64;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL((lqr_rescue_kernel<D, SM, WU>), dim3((unsigned)blocks), dim3(64), Rescue<D>::LDS_BYTES, s, A, B,
+                     Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+}
+
+// ---------------------------------------------------------------------------
 // launch helpers (instantiated per D in ttc_lqr_d*.hip)
 // ---------------------------------------------------------------------------
 template <int D>
