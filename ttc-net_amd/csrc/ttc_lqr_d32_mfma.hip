@@ -2,15 +2,19 @@
 // rescue pass (row-layout recompute of the problems whose Cholesky broke down).
 #include "ttc_lqr_mfma_blk.cuh"
 
+#ifndef TTC_BLK32_PPW
+#define TTC_BLK32_PPW 2  // problems per wave (2 waves per SIMD; 4 problems fit only one)
+#endif
+
 namespace ttc {
 
 template <int SM, bool WU>
 static void launch_b32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
-  using G = MB<32>;
+  using G = MB<32, TTC_BLK32_PPW, 1>;
   const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
-  hipLaunchKernelGGL((lqr_fwd_blk_kernel<32, SM, WU>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB, lQ, h0,
+  hipLaunchKernelGGL((lqr_fwd_blk_kernel<32, TTC_BLK32_PPW, 1, SM, WU>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB, lQ, h0,
                      P, H, T, u, st_a, st_b, status);
   launch_rescue_k<32, SM, WU>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
 }

@@ -4,14 +4,26 @@
 
 namespace ttc {
 
+template <int SM, bool WU, int WPB>
+static void launch_b64_w(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
+                         float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
+  using G = MB<64, 1, WPB>;
+  const dim3 grid((unsigned)((P + WPB - 1) / WPB)), block(G::THREADS);
+  hipLaunchKernelGGL((lqr_fwd_blk_kernel<64, 1, WPB, SM, WU>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB,
+                     lQ, h0, P, H, T, u, st_a, st_b, status);
+}
+
+// Four-wave workgroups share one token's B and Q in LDS: every aligned group of four
+// problems belongs to one token when the head count is a multiple of 4.
 template <int SM, bool WU>
 static void launch_b64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
-  using G = MB<64>;
-  const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
-  hipLaunchKernelGGL((lqr_fwd_blk_kernel<64, SM, WU>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB, lQ, h0,
-                     P, H, T, u, st_a, st_b, status);
+  if (H % 4 == 0)
+    launch_b64_w<SM, WU, 4>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+  else
+    launch_b64_w<SM, WU, 1>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
   launch_rescue_k<64, SM, WU>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
 }
 

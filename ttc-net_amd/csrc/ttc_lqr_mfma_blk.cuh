@@ -1,13 +1,13 @@
 // ttc_lqr_mfma_blk.cuh -- d = du in {32, 64} forward kernel: the Riccati sweep as 16x16
 // tiles on the matrix cores (v_mfma_f32_16x16x4f32), with a blocked Cholesky.
 //
-// One wave holds PPW = 64 / D problems; every D x D matrix is NB x NB tiles (NB = D/16),
-// each tile in the MFMA C/D layout: lane 16g + c holds X[4g + r][c], r = 0..3.  For a
-// product C = X Y the A operand of lane (g, c) is X[c][4g + s] and the B operand
-// Y[4g + s][c] (instruction s of 4 covers k = 4g + s), so a C-layout tile serves directly
-// as a B operand, and as an A operand when X is the transpose of a tile we hold
-// (X_IK = T_KI').  Per Riccati step t >= 1 and problem:
-//   B_k = B diag(beta)                      NB*NB*4 VALU (the MFMA operand, scaled)
+// A wave holds PPW problems; every D x D matrix is NB x NB tiles (NB = D/16), each tile
+// in the MFMA C/D layout: lane 16g + c holds X[4g + r][c], r = 0..3.  For a product
+// C = X Y the A operand of lane (g, c) is X[c][4g + s] and the B operand Y[4g + s][c]
+// (instruction s of 4 covers k = 4g + s), so a C-layout tile serves directly as a B
+// operand, and as an A operand when X is the transpose of a tile we hold (X_IK = T_KI').
+// Per Riccati step t >= 1 and problem:
+//   B_k = B diag(beta)                      the MFMA operand, scaled per block-row
 //   -W = N B_k           (N = -V)           NB^3 * 4 MFMA
 //   -Quu = B_k'(-W) - R, upper tiles        NB(NB+1)/2 * NB * 4 MFMA
 //   -W' from -W through LDS (tile transpose)
@@ -22,6 +22,11 @@
 // partially pivoted Gauss-Jordan in the row layout (lane li owns row li); it also writes
 // the compact stash V_1 / Quu_0.
 //
+// d = 64: B and -sym(Q) live in LDS, shared by the WPB waves of a workgroup (one problem
+// per wave, WPB consecutive heads of one token -- the launcher guarantees it), so that
+// two 4-wave workgroups fit a CU and two waves share each SIMD.  d = 32: B and Q in
+// registers, one-wave workgroups.
+//
 // Breakdown guard: in exact arithmetic every Cholesky pivot of Quu = R + B'VB is at least
 // min_j 1/R_inv_j (Quu >= R); a pivot below half of that, or not finite, means rounding
 // made V indefinite.  The wave then stops and marks its problems with a NaN (u[p][0], or
@@ -32,30 +37,36 @@
 
 namespace ttc {
 
-template <int D>
+template <int D, int PPW_, int WPB_>
 struct MB {
   static constexpr int NB = D / 16;                 // tiles per dimension
-  static constexpr int PPW = 64 / D;                // problems per wave
+  static constexpr int PPW = PPW_;                  // problems per wave
+  static constexpr int WPB = WPB_;                  // waves per workgroup
+  static constexpr int GPP = 4 / PPW;               // 16-lane groups per problem in the 16x16 elimination
+  static constexpr int RPP = 64 / D;                // problems per row-layout pass (D lanes each)
+  static constexpr int NPASS = PPW / RPP;           // row-layout passes over the wave's problems
+  static_assert(PPW % RPP == 0 && PPW <= 4, "problems per wave");
   static constexpr int NT = NB * (NB + 1) / 2;      // upper tiles (I <= J)
   static constexpr int LDX = D + kPad;              // LDS row stride of D-wide rows
   static constexpr int LDG = 20;                    // LDS row stride of a 16 x 16 tile
-  // d = 64 keeps B and -sym(Q) in LDS (registers hold N and the step's products);
-  // d = 32 keeps them in registers.
-  static constexpr bool BQ_LDS = D == 64;
-  static constexpr int CH = BQ_LDS ? 2 : NB;        // block-rows per transpose round
-  // per-problem LDS region: [B' (column-major B) | -sym(Q) fragments | transpose buffer]
-  static constexpr int OFF_Q = BQ_LDS ? D * LDX : 0;
-  static constexpr int OFF_X = BQ_LDS ? OFF_Q + NT * 256 : 0;
+  static constexpr bool BQ_LDS = D == 64;           // B and -sym(Q) in (workgroup-shared) LDS
+  static_assert(BQ_LDS ? PPW == 1 : WPB == 1, "shared B / Q: one problem per wave");
+  // workgroup-shared region: [B' (column-major B) | -sym(Q) fragments]
+  static constexpr int OFF_Q = D * LDX;
+  static constexpr int SH = BQ_LDS ? OFF_Q + NT * 256 : 0;
+  // per-problem region: transpose buffer (CH block-rows per round), also the 16x16 tile
+  // buffer and the step-0 row buffer
+  static constexpr int CH = BQ_LDS ? 2 : NB;
   static constexpr int XROWS = CH * 16;
-  static constexpr int REG0 = OFF_X + XROWS * LDX;
-  static constexpr int QB_CAP = REG0 - OFF_Q;       // step 0: the full Quu_0 rows (from OFF_Q)
-  static_assert(QB_CAP >= D * LDX, "step 0 needs D rows of Quu_0");
-  static_assert(XROWS * LDX >= 16 * LDG, "the 16x16 tile buffer aliases the transpose buffer");
-  static constexpr int REG = (REG0 + 3) & ~3;       // 16-byte multiple
+  static constexpr int REG = XROWS * LDX;
+  static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4, "per-problem LDS region");
   static constexpr int VEC = 3 * D;                 // alpha, q (step 0: alpha*h0), beta
-  static constexpr int THREADS = 64;
-  static constexpr int WAVES = D == 64 ? 1 : 2;     // waves per SIMD the registers allow
-  static constexpr size_t LDS_BYTES = sizeof(float) * (size_t)PPW * (REG + VEC);
+  static constexpr int PER_WAVE = PPW * (REG + VEC);
+  static constexpr int THREADS = 64 * WPB;
+  // two waves per SIMD, except with four problems per wave (their registers fill one)
+  static constexpr int MINW = PPW == 4 ? 1 : 2;
+  static constexpr int MAXW = MINW;
+  static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)SH + (size_t)WPB * PER_WAVE);
 };
 
 // upper tile (I, J), I <= J, in row-major order of the upper triangle
@@ -64,114 +75,152 @@ __host__ __device__ constexpr int utile(int I, int J) {
   return I * NB - I * (I - 1) / 2 + (J - I);
 }
 
-template <int D, int SM, bool WRITE_U>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WAVES))) void lqr_fwd_blk_kernel(
-    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
-    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
-    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
-    int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
-    float* __restrict__ q0stash, int* __restrict__ status) {
-  using G = MB<D>;
+template <int D, int PPW_, int WPB_, int SM, bool WRITE_U>
+__global__ __launch_bounds__(64 * WPB_) __attribute__((amdgpu_waves_per_eu(MB<D, PPW_, WPB_>::MINW,
+                                                                           MB<D, PPW_, WPB_>::MAXW))) void
+lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+                   const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+                   const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+                   int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
+                   float* __restrict__ q0stash, int* __restrict__ status) {
+  using G = MB<D, PPW_, WPB_>;
   constexpr int NB = G::NB, PPW = G::PPW, NT = G::NT, LDX = G::LDX, LDG = G::LDG;
+  constexpr int RPP = G::RPP, NPASS = G::NPASS;
   constexpr bool BQL = G::BQ_LDS;
   extern __shared__ __align__(16) float sm[];
   constexpr float kLog2e = 1.4426950408889634f;
-  const int lane = threadIdx.x;
-  const int g = lane >> 4;   // lane group: MFMA row block
-  const int c = lane & 15;   // MFMA column; row of the 16x16 elimination
-  const int qo = lane / D;   // my problem in the row layout
-  const int li = lane % D;   // my row (of D) in the row layout
-  const int64_t pbase = (int64_t)blockIdx.x * PPW;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;  // wave of the workgroup
+  const int g = lane >> 4;          // lane group: MFMA row block
+  const int c = lane & 15;          // MFMA column; row of the 16x16 elimination
+  const int qe = g / G::GPP;        // my problem in the 16x16 elimination
+  const int li = lane % D;          // my row (of D) in the row layout
+  const int64_t pbase = ((int64_t)blockIdx.x * G::WPB + wv) * PPW;
 
   int64_t pid[PPW];
 #pragma unroll
   for (int q = 0; q < PPW; ++q) pid[q] = (pbase + q < P) ? (pbase + q) : (P - 1);  // idle: recompute, never store
-  const int64_t po = (pbase + qo < P) ? (pbase + qo) : (P - 1);
-  const bool own_valid = pbase + qo < P;
-  auto region = [&](int q) { return sm + q * G::REG; };
-  float* vecs = sm + PPW * G::REG;  // [q][alpha D | q D | beta D]
+  float* shb = sm;             // shared B' (d = 64)
+  float* shq = sm + G::OFF_Q;  // shared -sym(Q) fragments (d = 64)
+  float* wbase = sm + G::SH + wv * G::PER_WAVE;
+  auto region = [&](int q) { return wbase + q * G::REG; };
+  float* vecs = wbase + PPW * G::REG;  // [q][alpha D | q D | beta D]
 
-  // row-layout scalars of my problem (lane li of problem qo)
-  const float a_l = A_diag[po * D + li];
-  const float lb2_l = lgB[po * D + li] * kLog2e;
-  const float lq2_l = lgQ[po * D + li] * kLog2e;
-  const float la2_o = lgA[po] * kLog2e;
-  float piv_floor = 1.0f / Rinv[po * D + li];
-  piv_floor = row16_min(piv_floor);
-  if constexpr (D >= 32) piv_floor = fminf(piv_floor, __shfl_xor(piv_floor, 16, 64));
-  if constexpr (D >= 64) piv_floor = fminf(piv_floor, __shfl_xor(piv_floor, 32, 64));
-  piv_floor *= 0.5f;
+  // row layout, pass pa: lane li of problem qr = pa * RPP + lane / D
+  int qr[NPASS];
+  int64_t po[NPASS];
+  bool own_valid[NPASS];
+  float a_l[NPASS], lb2_l[NPASS], lq2_l[NPASS], la2_o[NPASS];
+#pragma unroll
+  for (int pa = 0; pa < NPASS; ++pa) {
+    qr[pa] = pa * RPP + lane / D;
+    po[pa] = (pbase + qr[pa] < P) ? (pbase + qr[pa]) : (P - 1);
+    own_valid[pa] = pbase + qr[pa] < P;
+    a_l[pa] = A_diag[po[pa] * D + li];
+    lb2_l[pa] = lgB[po[pa] * D + li] * kLog2e;
+    lq2_l[pa] = lgQ[po[pa] * D + li] * kLog2e;
+    la2_o[pa] = lgA[po[pa]] * kLog2e;
+  }
 
-  // C-layout state: N = -V (all tiles); B and -sym(Q) (registers, or LDS for d = 64)
+  // C-layout state: N = -V (all tiles); B and -sym(Q) (registers, or shared LDS for d = 64)
   v4f NV[PPW][NB][NB];
   float Bm[BQL ? 1 : PPW][NB][NB][4];
   v4f Qn[BQL ? 1 : PPW][NT];
   float rr[PPW][NB];  // 1 / R_inv[16I + c]
+  if constexpr (BQL) {
+    // the workgroup's token: B column-major, -sym(Q) as per-lane C-layout fragments
+    const int64_t n = pid[0] / H;
+    const float* bq = Bg + n * D * D;
+    const float* qq = Qg + n * D * D;
+    for (int e = threadIdx.x; e < D * D; e += G::THREADS) {
+      const int i = e / D, j = e % D;
+      shb[j * LDX + i] = bq[e];
+    }
+    for (int e = threadIdx.x; e < NT * 64; e += G::THREADS) {
+      const int tile = e >> 6, ln = e & 63;
+      int I = 0, rem = tile;
+      while (rem >= NB - I) {
+        rem -= NB - I;
+        ++I;
+      }
+      const int J = I + rem;
+      v4f qn;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * I + 4 * (ln >> 4) + r, j = 16 * J + (ln & 15);
+        qn[r] = -0.5f * (qq[i * D + j] + qq[j * D + i]);
+      }
+      st4(shq + e * 4, qn);
+    }
+  }
 #pragma unroll
   for (int q = 0; q < PPW; ++q) {
     const int64_t n = pid[q] / H;
     const float* bq = Bg + n * D * D;
     const float* qq = Qg + n * D * D;
     const float* fq = Qf + pid[q] * D * D;
-    float* rg = region(q);
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
       rr[q][I] = 1.0f / Rinv[pid[q] * D + 16 * I + c];
 #pragma unroll
       for (int J = 0; J < NB; ++J) {
-        v4f qn;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * I + 4 * g + r, j = 16 * J + c;
           NV[q][I][J][r] = -0.5f * (fq[i * D + j] + fq[j * D + i]);
-          const float b = bq[i * D + j];
-          if constexpr (BQL) rg[j * LDX + i] = b;  // column-major: a tile's operand is one float4
-          else Bm[q][I][J][r] = b;
-          qn[r] = -0.5f * (qq[i * D + j] + qq[j * D + i]);
-        }
-        if (I <= J) {
-          if constexpr (BQL) st4(rg + G::OFF_Q + (utile<NB>(I, J) * 64 + lane) * 4, qn);
-          else Qn[q][utile<NB>(I, J)] = qn;
+          if constexpr (!BQL) {
+            Bm[q][I][J][r] = bq[i * D + j];
+            if (I <= J) Qn[q][utile<NB>(I, J)][r] = -0.5f * (qq[i * D + j] + qq[j * D + i]);
+          }
         }
       }
     }
   }
-  wave_sync();
+  // pivot floor of my elimination problem: half of min_j 1 / R_inv_j
+  float piv_floor = 0.f;
+#pragma unroll
+  for (int q = 0; q < PPW; ++q) {
+    float m = rr[q][0];
+#pragma unroll
+    for (int I = 1; I < NB; ++I) m = fminf(m, rr[q][I]);
+    m = 0.5f * row16_min(m);
+    if (q == qe) piv_floor = m;
+  }
+  if constexpr (BQL) __syncthreads();  // shared B / Q written (the only workgroup barrier)
 
-  // B_k = B diag(beta) operand tiles of problem q (beta read from the vector buffer)
-  auto load_bk = [&](int q, float (&Bk)[NB][NB][4]) {
+  // B_k = B diag(beta), block-row K: Bk[J][s] = B[16K + 4g + s][16J + c] beta[16J + c]
+  auto load_bk_row = [&](int q, int K, float (&Bk)[NB][4]) {
     const float* v = vecs + q * G::VEC;
-    const float* rg = region(q);
 #pragma unroll
     for (int J = 0; J < NB; ++J) {
       const float bj = v[2 * D + 16 * J + c];
+      if constexpr (BQL) {
+        const v4f b4 = ld4(shb + (16 * J + c) * LDX + 16 * K + 4 * g);
 #pragma unroll
-      for (int K = 0; K < NB; ++K) {
-        if constexpr (BQL) {
-          const v4f b4 = ld4(rg + (16 * J + c) * LDX + 16 * K + 4 * g);
+        for (int s = 0; s < 4; ++s) Bk[J][s] = b4[s] * bj;
+      } else {
 #pragma unroll
-          for (int s = 0; s < 4; ++s) Bk[K][J][s] = b4[s] * bj;
-        } else {
-#pragma unroll
-          for (int s = 0; s < 4; ++s) Bk[K][J][s] = Bm[q][K][J][s] * bj;
-        }
+        for (int s = 0; s < 4; ++s) Bk[J][s] = Bm[q][K][J][s] * bj;
       }
     }
   };
   // -W = N B_k and the upper tiles of -Quu = B_k'(-W) - R
-  auto w_quu = [&](int q, const float (&Bk)[NB][NB][4], v4f (&nW)[NB][NB], v4f (&nQ)[NT]) {
+  auto w_quu = [&](int q, v4f (&nW)[NB][NB], v4f (&nQ)[NT]) {
 #pragma unroll
     for (int I = 0; I < NB; ++I)
 #pragma unroll
       for (int J = 0; J < NB; ++J) nW[I][J] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int K = 0; K < NB; ++K)
+    for (int K = 0; K < NB; ++K) {
+      float Bk[NB][4];
+      load_bk_row(q, K, Bk);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int I = 0; I < NB; ++I)
 #pragma unroll
-          for (int J = 0; J < NB; ++J) nW[I][J] = mfma16x16x4(NV[q][K][I][s], Bk[K][J][s], nW[I][J]);
+          for (int J = 0; J < NB; ++J) nW[I][J] = mfma16x16x4(NV[q][K][I][s], Bk[J][s], nW[I][J]);
+    }
 #pragma unroll
     for (int I = 0; I < NB; ++I)
 #pragma unroll
@@ -184,25 +233,29 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WA
         nQ[utile<NB>(I, J)] = acc;
       }
 #pragma unroll
-    for (int K = 0; K < NB; ++K)
+    for (int K = 0; K < NB; ++K) {
+      float Bk[NB][4];
+      load_bk_row(q, K, Bk);
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int I = 0; I < NB; ++I)
 #pragma unroll
           for (int J = I; J < NB; ++J)
-            nQ[utile<NB>(I, J)] = mfma16x16x4(Bk[K][I][s], nW[K][J][s], nQ[utile<NB>(I, J)]);
+            nQ[utile<NB>(I, J)] = mfma16x16x4(Bk[I][s], nW[K][J][s], nQ[utile<NB>(I, J)]);
+    }
   };
 
   // One matrix-core Riccati step t >= 1.  Returns true when the breakdown guard fired
   // (N is then unchanged: the guard is evaluated before N is touched).
   auto step = [&](const int t) -> bool {
     const float tp1 = (float)(t + 1);
-    {
-      float* v = vecs + qo * G::VEC;
-      v[li] = fmaf(a_l, __builtin_amdgcn_exp2f(la2_o * tp1), 1.0f);  // alpha
-      v[D + li] = __builtin_amdgcn_exp2f(lq2_l * (float)t);          // q
-      v[2 * D + li] = __builtin_amdgcn_exp2f(lb2_l * tp1);           // beta
+#pragma unroll
+    for (int pa = 0; pa < NPASS; ++pa) {
+      float* v = vecs + qr[pa] * G::VEC;
+      v[li] = fmaf(a_l[pa], __builtin_amdgcn_exp2f(la2_o[pa] * tp1), 1.0f);  // alpha
+      v[D + li] = __builtin_amdgcn_exp2f(lq2_l[pa] * (float)t);              // q
+      v[2 * D + li] = __builtin_amdgcn_exp2f(lb2_l[pa] * tp1);               // beta
     }
     wave_sync();
 
@@ -211,13 +264,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WA
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
       v4f nW[NB][NB];
-      {
-        float Bk[NB][NB][4];
-        load_bk(q, Bk);
-        w_quu(q, Bk, nW, nQ[q]);
-      }
+      w_quu(q, nW, nQ[q]);
       // -W -> LDS row-major, read back as -W' (CH block-rows per round)
-      float* xb = region(q) + G::OFF_X;
+      float* xb = region(q);
 #pragma unroll
       for (int h = 0; h < NB; h += G::CH) {
 #pragma unroll
@@ -241,33 +290,33 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WA
     for (int j = 0; j < NB; ++j) {
       // diagonal tile -Quu_jj (symmetric: the column fragment is a row fragment)
 #pragma unroll
-      for (int q = 0; q < PPW; ++q) st4(region(q) + G::OFF_X + c * LDG + 4 * g, nQ[q][utile<NB>(j, j)]);
+      for (int q = 0; q < PPW; ++q) st4(region(q) + c * LDG + 4 * g, nQ[q][utile<NB>(j, j)]);
       wave_sync();
-      float* tb = region(qo) + G::OFF_X;
-      float qr[16], ir[16];
-      ld_row<16>(tb + c * LDG, qr);
+      float* tb = region(qe);
+      float qrow[16], irow[16];
+      ld_row<16>(tb + c * LDG, qrow);
 #pragma unroll
-      for (int k = 0; k < 16; ++k) ir[k] = (k == c) ? -1.0f : 0.0f;
+      for (int k = 0; k < 16; ++k) irow[k] = (k == c) ? -1.0f : 0.0f;
       // elimination of the rows [-Quu_jj; -I]: the -I rows end as -L_jj^{-T}
       static_for<16>([&](auto kc) {
         constexpr int k = decltype(kc)::value;
-        const float npiv = bcast16<k>(qr[k]);  // -d_k
-        bad |= !(-npiv >= piv_floor);          // also catches NaN
+        const float npiv = bcast16<k>(qrow[k]);  // -d_k
+        bad |= !(-npiv >= piv_floor);            // also catches NaN
         const float rs = __builtin_amdgcn_rsqf(-npiv);
         const float ip = rs * rs;
-        const float ni = ir[k] * ip;
+        const float ni = irow[k] * ip;
         if constexpr (k < 15) {
-          const float nq = qr[k] * ip;
-          Elim16<k>::qw(qr, ir, nq, ni);
+          const float nq = qrow[k] * ip;
+          Elim16<k>::qw(qrow, irow, nq, ni);
         }
-        ir[k] *= rs;
+        irow[k] *= rs;
       });
       wave_sync();
-      st_row<16>(tb + c * LDG, ir);  // rows of -L_jj^{-T} (groups of one problem write equal values)
+      st_row<16>(tb + c * LDG, irow);  // rows of -L_jj^{-T} (groups of one problem write equal values)
       wave_sync();
 #pragma unroll
       for (int q = 0; q < PPW; ++q) {
-        const float* ub = region(q) + G::OFF_X;
+        const float* ub = region(q);
         float nU[4];  // A operand of -L_jj^{-1}: -L^{-T}[4g + s][c]
 #pragma unroll
         for (int s = 0; s < 4; ++s) nU[s] = ub[(4 * g + s) * LDG + c];
@@ -317,24 +366,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WA
 #pragma unroll
             for (int J = I; J < NB; ++J) NV[q][I][J] = mfma16x16x4(nWt[q][kb][I][s], nWt[q][kb][J][s], NV[q][I][J]);
       const float* v = vecs + q * G::VEC;
-      float* rg = region(q);
 #pragma unroll
       for (int I = 0; I < NB; ++I) {
         const v4f arow = ld4(v + 16 * I + 4 * g);
-        const v4f qrow = ld4(v + D + 16 * I + 4 * g);
+        const v4f qrw = ld4(v + D + 16 * I + 4 * g);
 #pragma unroll
         for (int J = I; J < NB; ++J) {
           const float acol = v[16 * J + c];
           const float qcol = v[D + 16 * J + c];
           v4f qn;
-          if constexpr (BQL) qn = ld4(rg + G::OFF_Q + (utile<NB>(I, J) * 64 + lane) * 4);
+          if constexpr (BQL) qn = ld4(shq + (utile<NB>(I, J) * 64 + lane) * 4);
           else qn = Qn[q][utile<NB>(I, J)];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) NV[q][I][J][r] = fmaf(arow[r] * acol, NV[q][I][J][r], (qrow[r] * qcol) * qn[r]);
+          for (int r = 0; r < 4; ++r) NV[q][I][J][r] = fmaf(arow[r] * acol, NV[q][I][J][r], (qrw[r] * qcol) * qn[r]);
         }
       }
       // lower tiles from the upper ones (CH block-rows per round)
-      float* xb = rg + G::OFF_X;
+      float* xb = region(q);
 #pragma unroll
       for (int h = 0; h < NB - 1; h += G::CH) {
 #pragma unroll
@@ -356,14 +404,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WA
 
   // Step 0: stash V_1, form W_0 and Quu_0, u0 = -Quu_0^{-1} W_0' (alpha_0 * h0).
   auto step0 = [&]() {
-    {
-      float* v = vecs + qo * G::VEC;
-      const float alpha = fmaf(a_l, __builtin_amdgcn_exp2f(la2_o), 1.0f);
+#pragma unroll
+    for (int pa = 0; pa < NPASS; ++pa) {
+      float* v = vecs + qr[pa] * G::VEC;
+      const float alpha = fmaf(a_l[pa], __builtin_amdgcn_exp2f(la2_o[pa]), 1.0f);
       v[li] = alpha;
-      v[D + li] = alpha * h0[po * D + li];          // (A_0 h0)_li
-      v[2 * D + li] = __builtin_amdgcn_exp2f(lb2_l);  // beta_0
+      v[D + li] = alpha * h0[po[pa] * D + li];            // (A_0 h0)_li
+      v[2 * D + li] = __builtin_amdgcn_exp2f(lb2_l[pa]);  // beta_0
     }
     wave_sync();
+    v4f nQ[PPW][NT];
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
       if (SM == STASH_V1 && pbase + q < P) {
@@ -376,12 +426,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WA
             for (int r = 0; r < 4; ++r) vp[(16 * I + 4 * g + r) * D + 16 * J + c] = -NV[q][I][J][r];
       }
       v4f nW[NB][NB];
-      v4f nQ[NT];
-      {
-        float Bk[NB][NB][4];
-        load_bk(q, Bk);
-        w_quu(q, Bk, nW, nQ);
-      }
+      w_quu(q, nW, nQ[q]);
       // -y = -W' A_0 h0: -y[16J + c] = sum_{I,r} (-W)[16I+4g+r][16J+c] ah[16I+4g+r]
       const float* v = vecs + q * G::VEC;
       float ny[NB];
@@ -400,39 +445,52 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, MB<D>::WA
         ny[J] += __shfl_xor(ny[J], 16, 64);
         ny[J] += __shfl_xor(ny[J], 32, 64);
       }
-      // Quu_0 rows (upper tiles and their mirror) into the LDS row buffer
-      float* qb = region(q) + G::OFF_Q;
-#pragma unroll
-      for (int I = 0; I < NB; ++I)
-#pragma unroll
-        for (int J = I; J < NB; ++J)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float x = -nQ[utile<NB>(I, J)][r];
-            qb[(16 * I + 4 * g + r) * LDX + 16 * J + c] = x;
-            if (J > I) qb[(16 * J + c) * LDX + 16 * I + 4 * g + r] = x;
-          }
-      wave_sync();  // every lane has read alpha*h0 before the rhs overwrites the beta slot
+      wave_sync();  // every lane has read alpha*h0 and beta before the rhs overwrites the beta slot
       if (g == 0) {
 #pragma unroll
         for (int J = 0; J < NB; ++J) vecs[q * G::VEC + 2 * D + 16 * J + c] = -ny[J];  // y
       }
     }
-    wave_sync();
-    float aug[D + 4];
-    float* qb = region(qo) + G::OFF_Q;
-    ld_row<D>(qb + li * LDX, *reinterpret_cast<float(*)[D]>(aug));
-    aug[D] = vecs[qo * G::VEC + 2 * D + li];
-    aug[D + 1] = aug[D + 2] = aug[D + 3] = 0.f;
-    if (SM == STASH_V1 && own_valid) st_global_row<D>(q0stash + (po * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
-    wave_sync();  // all rows read before the pivot-row buffer (aliasing them) is written
-    float piv;
-    int pos;
-    gauss_jordan<D, D + 4>(aug, li, qb, piv, pos);
-    const float u0 = -aug[D] / piv;
-    if (own_valid) {
-      if (WRITE_U) u_out[po * D + pos] = u0;
-      if (status != nullptr && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
+    // rows of Quu_0 to the row layout, XROWS rows per round through the transpose buffer
+#pragma unroll
+    for (int pa = 0; pa < NPASS; ++pa) {
+      float aug[D + 4];
+#pragma unroll
+      for (int k = 0; k < D + 4; ++k) aug[k] = 0.f;
+#pragma unroll
+      for (int h = 0; h < D; h += G::XROWS) {
+        wave_sync();
+#pragma unroll
+        for (int q = pa * RPP; q < pa * RPP + RPP; ++q) {
+          float* xb = region(q);
+#pragma unroll
+          for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int J = I; J < NB; ++J)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float x = -nQ[q][utile<NB>(I, J)][r];
+                if (16 * I >= h && 16 * I < h + G::XROWS) xb[(16 * I - h + 4 * g + r) * LDX + 16 * J + c] = x;
+                if (J > I && 16 * J >= h && 16 * J < h + G::XROWS)
+                  xb[(16 * J - h + c) * LDX + 16 * I + 4 * g + r] = x;
+              }
+        }
+        wave_sync();
+        if (li >= h && li < h + G::XROWS)
+          ld_row<D>(region(qr[pa]) + (li - h) * LDX, *reinterpret_cast<float(*)[D]>(aug));
+      }
+      aug[D] = vecs[qr[pa] * G::VEC + 2 * D + li];
+      if (SM == STASH_V1 && own_valid[pa])
+        st_global_row<D>(q0stash + (po[pa] * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
+      wave_sync();  // all rows read before the pivot-row buffer (aliasing them) is written
+      float piv;
+      int pos;
+      gauss_jordan<D, D + 4>(aug, li, region(qr[pa]), piv, pos);
+      const float u0 = -aug[D] / piv;
+      if (own_valid[pa]) {
+        if (WRITE_U) u_out[po[pa] * D + pos] = u0;
+        if (status != nullptr && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
+      }
     }
   };
 
