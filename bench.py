@@ -221,7 +221,7 @@ def main():
         "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
-                     "kernel": "lqr_fwd16_mfma_kernel" if d == 16 else f"lqr_fwd_blk_kernel<{d}>",
+                     "kernel": f"lqr_fwd_blk_kernel<{d}>" + (" (symplectic sweep)" if d == 16 else " (blocked Riccati)"),
                      "flops_per_problem": F_fwd,
                      "algorithmic_bytes_per_problem": fwd_bytes},
     }

@@ -53,14 +53,20 @@ extern "C" {
  * for long, barely-discounted horizons (e.g. T = 1024 with log-normal inputs),
  * where fp32 rounding of V ~ 1e17 corrupts the gains. */
 #define TTC_LQR_FLAG_FP64_RICCATI 1
-/* TTC_LQR_FLAG_ROW_KERNEL selects the row-layout (vector-ALU only) fp32 kernel where a
- * matrix-core kernel exists (d = 16).  Results agree to fp32 rounding; it serves as an
- * independent cross-check and as a fallback. */
+/* TTC_LQR_FLAG_ROW_KERNEL selects the row-layout (vector-ALU only) fp32 kernel instead of
+ * the matrix-core kernels.  Results agree to fp32 rounding; it serves as an independent
+ * cross-check and as a fallback. */
 #define TTC_LQR_FLAG_ROW_KERNEL 2
 /* TTC_LQR_FLAG_STABLE_BWD makes ttc_lqr_backward take the stable path for every problem
  * (feedback gains recomputed and stored per step, closed-loop costates) instead of the
  * certified Hamiltonian rollout.  Same results to fp32 rounding; slower. */
 #define TTC_LQR_FLAG_STABLE_BWD 4
+/* TTC_LQR_FLAG_RICCATI_STEPS makes the d = 16 fp32 forward take a Riccati step (with its
+ * Cholesky factorisation) at every horizon step on the matrix cores, instead of the
+ * default symplectic sweep (three matrix products per step, one pivoted solve at the
+ * end, a conditioning certificate per problem and a row-layout recompute of the
+ * problems that miss it).  Same results to fp32 rounding. */
+#define TTC_LQR_FLAG_RICCATI_STEPS 8
 
 /* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
  * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds

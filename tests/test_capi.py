@@ -57,7 +57,8 @@ def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(16, 16, 1) == 1 and L.ttc_lqr_supported_flags(32, 32, 1) == 1
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
-    assert L.ttc_lqr_supported_flags(16, 16, 8) == 0
+    assert L.ttc_lqr_supported_flags(16, 16, 8) == 1 and L.ttc_lqr_supported_flags(32, 32, 8 | 4) == 1
+    assert L.ttc_lqr_supported_flags(16, 16, 16) == 0
     assert _fwd(L, d=64, du=64, flags=1) == 2
 
 

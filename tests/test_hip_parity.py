@@ -75,7 +75,7 @@ def test_config1_layer_slice(stash):
     check_case("cfg1", layer_solver_inputs(1, x), c["T"], stash=stash)
 
 
-@pytest.mark.parametrize("precision", ["fp32", "fp32-row", "fp64"])
+@pytest.mark.parametrize("precision", ["fp32", "fp32-riccati", "fp32-row", "fp64"])
 def test_config2_layer_slice(precision):
     c = CONFIGS[2]
     x = make_x(2, n_tokens=64, seed=1)
@@ -129,16 +129,18 @@ def test_wide_configs_row_kernel(cfg, n_tok, precision):
     check_case(f"cfg{cfg}-row", layer_solver_inputs(cfg, x), CONFIGS[cfg]["T"], precision=precision)
 
 
-@pytest.mark.parametrize("d,N,H,T", [(32, 3, 3, 40), (64, 2, 3, 33), (32, 1, 1, 1), (64, 1, 2, 2)])
+@pytest.mark.parametrize("d,N,H,T", [(32, 3, 3, 40), (64, 2, 3, 33), (32, 1, 1, 1), (64, 1, 2, 2),
+                                     (32, 2, 16, 24), (64, 2, 4, 24), (32, 1, 16, 1), (64, 1, 4, 1)])
 @pytest.mark.parametrize("stash", ["always", "never"])
 def test_wide_matrix_core_ragged(d, N, H, T, stash):
-    """d = 32 / 64 matrix-core kernels on the reference's bench distribution with an odd
-    problem count (an idle problem slot in the last d = 32 wave) and short horizons
-    (T = 1: step 0 only)."""
+    """d = 32 / 64 matrix-core kernels on the reference's bench distribution: odd problem
+    counts (an idle problem slot in the last d = 32 wave), head counts that select the
+    one-wave (H = 1, 2, 3) or the 4-wave shared-B/Q workgroups (H = 16 at d = 32, H = 4 at
+    d = 64), and short horizons (T = 1: step 0 only)."""
     check_case(f"mc{d}", bench_solver_inputs(N, H, d, seed=d + T), T, stash=stash, precision="fp32")
 
 
-def _indefinite_wide_inputs(d, mode, seed=2):
+def _indefinite_wide_inputs(d, mode, H=2, seed=2):
     """d = 32 / 64 inputs whose Cholesky pivot breaks down while the problem stays well
     conditioned (B orthogonal, so B'B = I and Quu = R + beta^2 V in the step where it
     happens).  mode "terminal": problem 1 has Q_f = -3 I, so Quu is negative definite
@@ -147,10 +149,10 @@ def _indefinite_wide_inputs(d, mode, seed=2):
     definite from t = T-2 on.  The matrix-core kernel marks the affected waves and the
     rescue pass recomputes those problems with the pivoted row-layout sweep.  (Condition
     numbers of Quu stay below 3; the reference's own fp32 solvers are within 2e-5.)"""
-    ins = bench_solver_inputs(2, 2, d, seed=seed)
+    ins = bench_solver_inputs(2, H, d, seed=seed)
     g = torch.Generator().manual_seed(seed)
     B, _ = torch.linalg.qr(torch.randn(2, d, d, generator=g))
-    lgB = torch.full((2, 2, d), -0.01)
+    lgB = torch.full((2, H, d), -0.01)
     A_diag, _, Q, R_inv, Qf, lgA, _, lgQ, h0 = [t.clone() for t in ins]
     if mode == "terminal":
         Qf[0, 1] = -3.0 * torch.eye(d)
@@ -161,11 +163,13 @@ def _indefinite_wide_inputs(d, mode, seed=2):
     return [A_diag, B.contiguous(), Q, R_inv, Qf, lgA, lgB, lgQ, h0]
 
 
-@pytest.mark.parametrize("d", [32, 64])
+@pytest.mark.parametrize("d,H", [(32, 2), (64, 2), (32, 16), (64, 4)])
 @pytest.mark.parametrize("mode", ["terminal", "mid"])
 @pytest.mark.parametrize("stash", ["always", "never"])
-def test_wide_indefinite_Quu_rescued(d, mode, stash):
-    check_case(f"indef{d}-{mode}", _indefinite_wide_inputs(d, mode), 6, stash=stash, precision="fp32")
+def test_wide_indefinite_Quu_rescued(d, H, mode, stash):
+    """H = 2: one-wave workgroups; H = 16 (d = 32) / 4 (d = 64): workgroups of 4 waves that
+    share the token's B and Q in LDS."""
+    check_case(f"indef{d}-H{H}-{mode}", _indefinite_wide_inputs(d, mode, H), 6, stash=stash, precision="fp32")
 
 
 @pytest.mark.parametrize("cfg,T", [(5, 64), (5, 1024), ("5b", 1024)])
@@ -203,8 +207,27 @@ def _indefinite_terminal_inputs(s, seed=2):
 
 @pytest.mark.parametrize("s", [2.0, 0.2])
 @pytest.mark.parametrize("stash", ["always", "never"])
-def test_indefinite_Quu_switches_to_pivoted_sweep(s, stash):
-    check_case(f"indef{s}", _indefinite_terminal_inputs(s), 6, stash=stash, precision="fp32")
+@pytest.mark.parametrize("precision", ["fp32", "fp32-riccati"])
+def test_indefinite_Quu_switches_to_pivoted_sweep(s, stash, precision):
+    check_case(f"indef{s}", _indefinite_terminal_inputs(s), 6, stash=stash, precision=precision)
+
+
+@pytest.mark.parametrize("T", [64, 256])
+def test_symplectic_certificate_on_stress_inputs(T):
+    """Config-5 inputs: the d = 16 symplectic sweep's certificate (conditioning of Y1,
+    symmetry of V_1) rejects the ill-conditioned problems (about 8 % of them), which the
+    rescue pass recomputes with the pivoted row-layout sweep; u and every gradient match
+    the fp64 oracle and the per-step Riccati kernel."""
+    x = make_x(5, n_tokens=16, seed=13)
+    ins = layer_solver_inputs(5, x)
+    pb = LQRProblem(*ins, T)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(4)).double().numpy()
+    sym = run_hip(ins, T, dU, grad_limit=math.inf, precision="fp32")
+    ric = run_hip(ins, T, dU, grad_limit=math.inf, precision="fp32-riccati")
+    ref = solve_grads(pb, dU)
+    for k in ["u"] + NAMES:
+        assert _relerr(sym[k], ref[k]) <= TOL, k
+        assert _relerr(sym[k], ric[k]) <= TOL, k
 
 
 def test_T1_closed_form():

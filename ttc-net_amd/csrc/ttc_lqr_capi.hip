@@ -258,7 +258,8 @@ int ttc_lqr_supported(int32_t d, int32_t du) { return (d == du && (d == 16 || d 
 int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if (!ttc_lqr_supported(d, du)) return 0;
   if ((flags & TTC_LQR_FLAG_FP64_RICCATI) && d > 32) return 0;
-  const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD;
+  const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD |
+                        TTC_LQR_FLAG_RICCATI_STEPS;
   return (flags & ~known) ? 0 : 1;
 }
 

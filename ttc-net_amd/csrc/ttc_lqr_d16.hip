@@ -6,9 +6,14 @@ namespace ttc {
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
-  // fp32 sweeps run on the matrix-core kernel unless the row-layout kernel is asked for
-  if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL)))
+  // fp32 sweeps run on the matrix cores unless the row-layout kernel is asked for: the
+  // symplectic sweep by default, per-step Riccati when asked for or when every gain is
+  // stored (the stable backward)
+  if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL))) {
+    if (sm != STASH_GAINS && !(flags & TTC_LQR_FLAG_RICCATI_STEPS))
+      return launch_fwd_d16_sym(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
     return launch_fwd_d16_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
+  }
   return launch_fwd<16, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);
 }
 

@@ -1,0 +1,40 @@
+// ttc_lqr_d16_sym.hip -- launcher of the d = du = 16 symplectic matrix-core forward kernel
+// and its rescue pass (row-layout recompute of the problems the certificate rejects).
+#include "ttc_lqr_mfma_blk.cuh"
+
+namespace ttc {
+
+template <int SM, bool WU>
+static void launch_s16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                       const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
+                       float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
+  using G = MB<16, 4, 1, true>;
+  const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
+  hipLaunchKernelGGL((lqr_fwd_blk_kernel<16, 4, 1, SM, WU, true>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA,
+                     lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+  launch_rescue_k<16, SM, WU>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+}
+
+// Stash modes STASH_NONE and STASH_V1; the per-step gains (STASH_GAINS) come from the
+// Riccati kernels.
+int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                       const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
+                       int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s) {
+  if (P <= 0) return TTC_LQR_OK;
+  switch (sm) {
+    case STASH_NONE:
+      launch_s16<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      break;
+    case STASH_V1:
+      if (u != nullptr)
+        launch_s16<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      else
+        launch_s16<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      break;
+    default:
+      return TTC_LQR_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+}
+
+}  // namespace ttc

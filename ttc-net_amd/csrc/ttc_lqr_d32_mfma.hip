@@ -2,20 +2,30 @@
 // rescue pass (row-layout recompute of the problems whose Cholesky broke down).
 #include "ttc_lqr_mfma_blk.cuh"
 
-#ifndef TTC_BLK32_PPW
-#define TTC_BLK32_PPW 2  // problems per wave (2 waves per SIMD; 4 problems fit only one)
-#endif
-
 namespace ttc {
 
+template <int SM, bool WU, int PPW, int WPB>
+static void launch_b32_w(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
+                         float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
+  using G = MB<32, PPW, WPB>;
+  constexpr int PPB = PPW * WPB;
+  const dim3 grid((unsigned)((P + PPB - 1) / PPB)), block(G::THREADS);
+  hipLaunchKernelGGL((lqr_fwd_blk_kernel<32, PPW, WPB, SM, WU>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB,
+                     lQ, h0, P, H, T, u, st_a, st_b, status);
+}
+
+// With a head count that is a multiple of 16, 4-wave workgroups of 4 problems per wave
+// share one token's B and Q in LDS (every aligned group of 16 problems is one token);
+// otherwise one-wave workgroups of 2 problems keep B and Q in registers.
 template <int SM, bool WU>
 static void launch_b32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
-  using G = MB<32, TTC_BLK32_PPW, 1>;
-  const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
-  hipLaunchKernelGGL((lqr_fwd_blk_kernel<32, TTC_BLK32_PPW, 1, SM, WU>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB, lQ, h0,
-                     P, H, T, u, st_a, st_b, status);
+  if (H % 16 == 0)
+    launch_b32_w<SM, WU, 4, 4>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+  else
+    launch_b32_w<SM, WU, 2, 1>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
   launch_rescue_k<32, SM, WU>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
 }
 

@@ -22,10 +22,10 @@
 // partially pivoted Gauss-Jordan in the row layout (lane li owns row li); it also writes
 // the compact stash V_1 / Quu_0.
 //
-// d = 64: B and -sym(Q) live in LDS, shared by the WPB waves of a workgroup (one problem
-// per wave, WPB consecutive heads of one token -- the launcher guarantees it), so that
-// two 4-wave workgroups fit a CU and two waves share each SIMD.  d = 32: B and Q in
-// registers, one-wave workgroups.
+// Multi-wave workgroups (and every d = 64 launch) keep B and -sym(Q) in LDS, shared by the
+// WPB waves of the workgroup: its WPB * PPW problems are consecutive heads of one token
+// (the launcher guarantees it).  That leaves the registers to N and the step's products,
+// so two waves share each SIMD.  One-wave d = 32 workgroups keep B and Q in registers.
 //
 // Breakdown guard: in exact arithmetic every Cholesky pivot of Quu = R + B'VB is at least
 // min_j 1/R_inv_j (Quu >= R); a pivot below half of that, or not finite, means rounding
@@ -37,8 +37,9 @@
 
 namespace ttc {
 
-template <int D, int PPW_, int WPB_>
+template <int D, int PPW_, int WPB_, bool SYM_ = false>
 struct MB {
+  static constexpr bool SYM = SYM_;                 // symplectic sweep (d = 16) instead of Riccati steps
   static constexpr int NB = D / 16;                 // tiles per dimension
   static constexpr int PPW = PPW_;                  // problems per wave
   static constexpr int WPB = WPB_;                  // waves per workgroup
@@ -49,25 +50,48 @@ struct MB {
   static constexpr int NT = NB * (NB + 1) / 2;      // upper tiles (I <= J)
   static constexpr int LDX = D + kPad;              // LDS row stride of D-wide rows
   static constexpr int LDG = 20;                    // LDS row stride of a 16 x 16 tile
-  static constexpr bool BQ_LDS = D == 64;           // B and -sym(Q) in (workgroup-shared) LDS
-  static_assert(BQ_LDS ? PPW == 1 : WPB == 1, "shared B / Q: one problem per wave");
+  // B and -sym(Q) in LDS, shared by the workgroup (d = 64 always; d = 32 with several waves)
+  static constexpr bool BQ_LDS = D == 64 || WPB > 1;
   // workgroup-shared region: [B' (column-major B) | -sym(Q) fragments]
   static constexpr int OFF_Q = D * LDX;
   static constexpr int SH = BQ_LDS ? OFF_Q + NT * 256 : 0;
   // per-problem region: transpose buffer (CH block-rows per round), also the 16x16 tile
   // buffer and the step-0 row buffer
-  static constexpr int CH = BQ_LDS ? 2 : NB;
+  static constexpr int CH = BQ_LDS ? NB / 2 : NB;
   static constexpr int XROWS = CH * 16;
-  static constexpr int REG = XROWS * LDX;
+  static constexpr int LDS2 = 2 * D + 4;            // symplectic: rows of [Y1 | -Y2]
+  static constexpr int REG0 = XROWS * LDX;
+  static constexpr int REG = (SYM && D * LDS2 > REG0) ? D * LDS2 : REG0;
   static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4, "per-problem LDS region");
-  static constexpr int VEC = 3 * D;                 // alpha, q (step 0: alpha*h0), beta
+  static_assert(!SYM || (D == 16 && !BQ_LDS), "the symplectic sweep is built for d = 16");
+  // per-problem vectors: alpha, q (step 0: alpha*h0), beta (step 0: rhs), -beta^2 R^{-1}, 1/alpha
+  static constexpr int VEC = 5 * D;
   static constexpr int PER_WAVE = PPW * (REG + VEC);
   static constexpr int THREADS = 64 * WPB;
-  // two waves per SIMD, except with four problems per wave (their registers fill one)
-  static constexpr int MINW = PPW == 4 ? 1 : 2;
+  // two waves per SIMD, except with four problems per wave that keep B and Q in registers;
+  // the symplectic sweep's small state leaves room for four
+  static constexpr int MINW = SYM ? 4 : (PPW == 4 && !BQ_LDS) ? 1 : 2;
   static constexpr int MAXW = MINW;
   static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)SH + (size_t)WPB * PER_WAVE);
 };
+
+// Certificate of the symplectic sweep (d = 16): the final solve P = Y1^{-1} Y2 is accepted when
+// cond_inf(Y1) <= kSymCondMax and max|P - P'| <= kSymAsymMax max|P|; problems that miss it are
+// recomputed by the rescue pass.
+constexpr float kSymCondMax = 1.0e3f;
+constexpr float kSymAsymMax = 1.0e-5f;
+
+// max over the D lanes of a problem (D = 16, 32, 64)
+template <int D>
+__device__ __forceinline__ float dgroup_max(float v) {
+  v = fmaxf(v, ror16f<8>(v));
+  v = fmaxf(v, ror16f<4>(v));
+  v = fmaxf(v, ror16f<2>(v));
+  v = fmaxf(v, ror16f<1>(v));
+  if constexpr (D >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+  if constexpr (D >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
 
 // upper tile (I, J), I <= J, in row-major order of the upper triangle
 template <int NB>
@@ -75,15 +99,15 @@ __host__ __device__ constexpr int utile(int I, int J) {
   return I * NB - I * (I - 1) / 2 + (J - I);
 }
 
-template <int D, int PPW_, int WPB_, int SM, bool WRITE_U>
-__global__ __launch_bounds__(64 * WPB_) __attribute__((amdgpu_waves_per_eu(MB<D, PPW_, WPB_>::MINW,
-                                                                           MB<D, PPW_, WPB_>::MAXW))) void
+template <int D, int PPW_, int WPB_, int SM, bool WRITE_U, bool SYM_ = false>
+__global__ __launch_bounds__(64 * WPB_) __attribute__((amdgpu_waves_per_eu(MB<D, PPW_, WPB_, SYM_>::MINW,
+                                                                           MB<D, PPW_, WPB_, SYM_>::MAXW))) void
 lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
                    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
                    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
                    int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
                    float* __restrict__ q0stash, int* __restrict__ status) {
-  using G = MB<D, PPW_, WPB_>;
+  using G = MB<D, PPW_, WPB_, SYM_>;
   constexpr int NB = G::NB, PPW = G::PPW, NT = G::NT, LDX = G::LDX, LDG = G::LDG;
   constexpr int RPP = G::RPP, NPASS = G::NPASS;
   constexpr bool BQL = G::BQ_LDS;
@@ -104,13 +128,13 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   float* shq = sm + G::OFF_Q;  // shared -sym(Q) fragments (d = 64)
   float* wbase = sm + G::SH + wv * G::PER_WAVE;
   auto region = [&](int q) { return wbase + q * G::REG; };
-  float* vecs = wbase + PPW * G::REG;  // [q][alpha D | q D | beta D]
+  float* vecs = wbase + PPW * G::REG;  // [q][alpha D | q D | beta D | -beta^2/R D | 1/alpha D]
 
   // row layout, pass pa: lane li of problem qr = pa * RPP + lane / D
   int qr[NPASS];
   int64_t po[NPASS];
   bool own_valid[NPASS];
-  float a_l[NPASS], lb2_l[NPASS], lq2_l[NPASS], la2_o[NPASS];
+  float a_l[NPASS], lb2_l[NPASS], lq2_l[NPASS], la2_o[NPASS], rinv_l[NPASS];
 #pragma unroll
   for (int pa = 0; pa < NPASS; ++pa) {
     qr[pa] = pa * RPP + lane / D;
@@ -120,6 +144,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     lb2_l[pa] = lgB[po[pa] * D + li] * kLog2e;
     lq2_l[pa] = lgQ[po[pa] * D + li] * kLog2e;
     la2_o[pa] = lgA[po[pa]] * kLog2e;
+    rinv_l[pa] = Rinv[po[pa] * D + li];
   }
 
   // C-layout state: N = -V (all tiles); B and -sym(Q) (registers, or shared LDS for d = 64)
@@ -127,6 +152,10 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   float Bm[BQL ? 1 : PPW][NB][NB][4];
   v4f Qn[BQL ? 1 : PPW][NT];
   float rr[PPW][NB];  // 1 / R_inv[16I + c]
+  // symplectic sweep: B in the transposed operand layout, Bt[q][I][K][s] = B[16I + c][16K + 4g + s],
+  // and Y1' (the sweep keeps Y-hat = Y' in the C layout; Y2' is -N)
+  float Bt[G::SYM ? PPW : 1][NB][NB][4];
+  v4f Y1[G::SYM ? PPW : 1][NB][NB];
   if constexpr (BQL) {
     // the workgroup's token: B column-major, -sym(Q) as per-lane C-layout fragments
     const int64_t n = pid[0] / H;
@@ -171,6 +200,10 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
           if constexpr (!BQL) {
             Bm[q][I][J][r] = bq[i * D + j];
             if (I <= J) Qn[q][utile<NB>(I, J)][r] = -0.5f * (qq[i * D + j] + qq[j * D + i]);
+          }
+          if constexpr (G::SYM) {
+            Bt[q][I][J][r] = bq[(16 * I + c) * D + 16 * J + 4 * g + r];
+            Y1[q][I][J][r] = (i == j) ? 1.0f : 0.0f;
           }
         }
       }
@@ -402,6 +435,143 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     return false;
   };
 
+  // One step t >= 1 of the symplectic sweep (the reference's transposed row-block update,
+  // symplectic_iter.py:226-251, with V_t = Y1^{-1} Y2).  The registers hold Y-hat = Y' in the
+  // C layout: Y1' in Y1, Y2' as -N.  With B_k = B diag(beta) and R^{-1} = diag(R_inv):
+  //   M = R^{-1} B_k' Y2'      Y1' <- A_k^{-1} (Y1' + B_k M)      Y2' <- A_k Y2' + Qc_k Y1'
+  // (beta enters once, squared, in the row scaling of M).  Every 4 steps the columns of
+  // Y-hat (rows of Y, which leave Y1^{-1} Y2 unchanged) are rescaled by powers of 2.
+  auto sym_step = [&](const int t) {
+    if constexpr (G::SYM) {
+    static_assert(NB == 1, "symplectic sweep: one tile per matrix");
+    const float tp1 = (float)(t + 1);
+#pragma unroll
+    for (int pa = 0; pa < NPASS; ++pa) {
+      float* v = vecs + qr[pa] * G::VEC;
+      const float alpha = fmaf(a_l[pa], __builtin_amdgcn_exp2f(la2_o[pa] * tp1), 1.0f);
+      const float beta = __builtin_amdgcn_exp2f(lb2_l[pa] * tp1);
+      v[li] = alpha;
+      v[D + li] = __builtin_amdgcn_exp2f(lq2_l[pa] * (float)t);  // q
+      v[3 * D + li] = -(beta * beta) * rinv_l[pa];
+      v[4 * D + li] = __builtin_amdgcn_rcpf(alpha);
+    }
+    wave_sync();
+    const bool renorm = ((T - 1 - t) & 3) == 3;
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const float* v = vecs + q * G::VEC;
+      // M = (B' N) diag-row(-beta^2 R^{-1}) = R^{-1} B_k' Y2'
+      v4f M = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) M = mfma16x16x4(Bm[q][0][0][s], NV[q][0][0][s], M);
+      const v4f nf = ld4(v + 3 * D + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) M[r] *= nf[r];
+      // Y1' <- A^{-1} (Y1' + B M)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) Y1[q][0][0] = mfma16x16x4(Bt[q][0][0][s], M[s], Y1[q][0][0]);
+      const v4f ia = ld4(v + 4 * D + 4 * g);
+      const v4f al = ld4(v + 4 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        Y1[q][0][0][r] *= ia[r];
+        NV[q][0][0][r] *= al[r];
+      }
+      // -Y2' <- -A Y2' - Qc Y1'  (operand -Qc[c][4g+s] = q_c (-Q)[4g+s][c] q_{4g+s})
+      const float qc = v[D + c];
+      const v4f qrw = ld4(v + D + 4 * g);
+      float op[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) op[s] = Qn[q][0][s] * (qc * qrw[s]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) NV[q][0][0] = mfma16x16x4(op[s], Y1[q][0][0][s], NV[q][0][0]);
+      if (renorm) {
+        float m = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(fabsf(Y1[q][0][0][r]), fabsf(NV[q][0][0][r])));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        const int e = 1 - __builtin_amdgcn_frexp_expf(m);  // m * 2^e in [1, 2)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          Y1[q][0][0][r] = __builtin_amdgcn_ldexpf(Y1[q][0][0][r], e);
+          NV[q][0][0][r] = __builtin_amdgcn_ldexpf(NV[q][0][0][r], e);
+        }
+      }
+    }
+    wave_sync();
+    }
+  };
+
+  // End of the symplectic sweep: -V_1 = Y1^{-1} (-Y2) by pivoted Gauss-Jordan on the rows
+  // [Y1 | -Y2 | I] (lane li owns row li of problem qr), the certificate, and N = sym(-V_1) in
+  // the C layout.  Returns the accepted problems as bits.
+  auto sym_finish = [&]() -> unsigned {
+    if constexpr (!G::SYM) {
+      return ~0u;
+    } else {
+    constexpr int L2 = G::LDS2;
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      float* buf = region(q);
+      st4(buf + c * L2 + 4 * g, Y1[q][0][0]);      // row c of Y1 = column c of Y1'
+      st4(buf + c * L2 + D + 4 * g, NV[q][0][0]);  // row c of -Y2
+    }
+    wave_sync();
+    bool ok = true;
+#pragma unroll
+    for (int pa = 0; pa < NPASS; ++pa) {
+      float* buf = region(qr[pa]);
+      float aug[3 * D];
+      ld_row<2 * D>(buf + li * L2, *reinterpret_cast<float(*)[2 * D]>(aug));
+#pragma unroll
+      for (int k = 0; k < D; ++k) aug[2 * D + k] = (k == li) ? 1.0f : 0.0f;
+      float rs = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) rs += fabsf(aug[k]);
+      const float n1 = dgroup_max<D>(rs);  // ||Y1||_inf
+      wave_sync();  // every row read before the pivot-row buffer (aliasing them) is written
+      float piv;
+      int pos;
+      gauss_jordan<D, 3 * D>(aug, li, buf, piv, pos);
+      const float ip = 1.0f / piv;
+      float ri = 0.f, pn[D];
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        ri += fabsf(aug[2 * D + k]);
+        pn[k] = aug[D + k] * ip;
+      }
+      const float n2 = dgroup_max<D>(ri * fabsf(ip));  // ||Y1^{-1}||_inf
+      st_row<D>(buf + pos * L2, pn);
+      wave_sync();
+      float da = 0.f, mx = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        da = fmaxf(da, fabsf(pn[k] - buf[k * L2 + pos]));
+        mx = fmaxf(mx, fabsf(pn[k]));
+      }
+      da = dgroup_max<D>(da);
+      mx = dgroup_max<D>(mx);
+      ok = (n1 * n2 <= kSymCondMax) && (da <= kSymAsymMax * mx);  // false on NaN
+    }
+    const unsigned long long bal = __ballot(ok);
+    unsigned bits = 0u;
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) bits |= (unsigned)((bal >> (q * D)) & 1ull) << q;
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const float* buf = region(q);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        NV[q][0][0][r] = 0.5f * (buf[(4 * g + r) * L2 + c] + buf[c * L2 + 4 * g + r]);
+    }
+    wave_sync();
+    return bits;
+    }
+  };
+
+  unsigned okbits = ~0u;  // problems whose sweep is accepted (the symplectic certificate)
+
   // Step 0: stash V_1, form W_0 and Quu_0, u0 = -Quu_0^{-1} W_0' (alpha_0 * h0).
   auto step0 = [&]() {
 #pragma unroll
@@ -416,7 +586,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     v4f nQ[PPW][NT];
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
-      if (SM == STASH_V1 && pbase + q < P) {
+      if (SM == STASH_V1 && pbase + q < P && ((okbits >> q) & 1u)) {
         float* vp = kstash + pid[q] * D * D;
 #pragma unroll
         for (int I = 0; I < NB; ++I)
@@ -480,32 +650,37 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
           ld_row<D>(region(qr[pa]) + (li - h) * LDX, *reinterpret_cast<float(*)[D]>(aug));
       }
       aug[D] = vecs[qr[pa] * G::VEC + 2 * D + li];
-      if (SM == STASH_V1 && own_valid[pa])
+      const bool store = own_valid[pa] && ((okbits >> qr[pa]) & 1u);
+      if (SM == STASH_V1 && store)
         st_global_row<D>(q0stash + (po[pa] * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
       wave_sync();  // all rows read before the pivot-row buffer (aliasing them) is written
       float piv;
       int pos;
       gauss_jordan<D, D + 4>(aug, li, region(qr[pa]), piv, pos);
       const float u0 = -aug[D] / piv;
-      if (own_valid[pa]) {
+      if (store) {
         if (WRITE_U) u_out[po[pa] * D + pos] = u0;
         if (status != nullptr && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
       }
     }
   };
 
-  int t = T - 1;
-  bool failed = false;
-  while (!failed && t >= 1) {
-    failed = step(t);
-    --t;
-  }
-  if (!failed) {
+  if constexpr (G::SYM) {
+    for (int t = T - 1; t >= 1; --t) sym_step(t);
+    okbits = sym_finish();
     step0();
-    return;
+  } else {
+    int t = T - 1;
+    bool failed = false;
+    while (!failed && t >= 1) {
+      failed = step(t);
+      --t;
+    }
+    if (!failed) step0();
+    else okbits = 0u;
   }
-  // breakdown: mark the wave's problems for lqr_rescue_kernel
-  if (lane < PPW && pbase + lane < P) {
+  // problems whose sweep broke down or was not certified: mark them for lqr_rescue_kernel
+  if (lane < PPW && pbase + lane < P && !((okbits >> lane) & 1u)) {
     const float nan = __builtin_nanf("");
     if (WRITE_U) u_out[(pbase + lane) * D] = nan;
     else q0stash[(pbase + lane) * D * D] = nan;

@@ -11,11 +11,12 @@ import ctypes
 import os
 
 __all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI", "FLAG_ROW_KERNEL",
-           "FLAG_STABLE_BWD"]
+           "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS"]
 
 FLAG_FP64_RICCATI = 1  # TTC_LQR_FLAG_FP64_RICCATI
 FLAG_ROW_KERNEL = 2    # TTC_LQR_FLAG_ROW_KERNEL
 FLAG_STABLE_BWD = 4    # TTC_LQR_FLAG_STABLE_BWD
+FLAG_RICCATI_STEPS = 8  # TTC_LQR_FLAG_RICCATI_STEPS
 
 LIB_NAME = "libttc_lqr.so"
 _HERE = os.path.dirname(os.path.abspath(__file__))

@@ -28,8 +28,12 @@ Differences from the reference, by design:
   barely discounted horizons the value matrix reaches ~1e17 and fp32 rounding
   corrupts the gains (the reference's own fp32 solvers lose the gradients
   entirely there).  Everything else (rollouts, costates, gradients) is fp32.
-  For d = 16 the fp32 sweep runs on the matrix cores (MFMA); ``"fp32-row"`` selects
-  the vector-ALU row-layout kernel instead.
+  The fp32 sweep runs on the matrix cores (MFMA): for d = 16 as the symplectic
+  sweep (three matrix products per step, one certified solve at the end; the
+  problems the certificate rejects are recomputed by the row-layout kernel), for
+  d = 32 / 64 as blocked-Cholesky Riccati steps.  ``"fp32-riccati"`` selects per-step
+  Riccati on the matrix cores for d = 16 too, ``"fp32-row"`` the vector-ALU row-layout
+  kernel.
 
 Environment knobs:
 ``TTC_LQR_STASH`` = ``auto`` (default: keep the stash from the forward when it fits
@@ -47,7 +51,7 @@ import os
 
 import torch
 
-from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD
+from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "padded_dim", "SUPPORTED_DIMS", "last_backward_stats"]
 
@@ -94,14 +98,17 @@ def _pad_inputs(ins, d, du, Dp):
 def riccati_flags(precision: str, T: int, Dp: int) -> int:
     """Kernel flags for the requested Riccati arithmetic (fp64 kernels exist for d <= 32).
 
-    ``"fp32"``: the fastest fp32 kernel (matrix cores where one exists, d = 16);
-    ``"fp32-row"``: the row-layout fp32 kernel (vector ALU only) -- an independent
-    cross-check of the matrix-core kernel; ``"fp64"``: fp64 sweep; ``"auto"``: fp64
-    for T >= FP64_HORIZON where available, else fp32.
+    ``"fp32"``: the fastest fp32 kernel (matrix cores; symplectic sweep for d = 16);
+    ``"fp32-riccati"``: per-step Riccati on the matrix cores (d = 16; the same kernels
+    as ``"fp32"`` for d = 32 / 64); ``"fp32-row"``: the row-layout fp32 kernel (vector
+    ALU only) -- an independent cross-check of the matrix-core kernels; ``"fp64"``:
+    fp64 sweep; ``"auto"``: fp64 for T >= FP64_HORIZON where available, else fp32.
     """
-    assert precision in ("fp32", "fp32-row", "fp64", "auto"), f"unknown precision {precision}"
+    assert precision in ("fp32", "fp32-riccati", "fp32-row", "fp64", "auto"), f"unknown precision {precision}"
     if precision == "fp32-row":
         return FLAG_ROW_KERNEL
+    if precision == "fp32-riccati":
+        return FLAG_RICCATI_STEPS
     if precision == "fp64":
         assert lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_RICCATI), \
             f"fp64 Riccati kernels exist for state dims up to 32, got {Dp}"
@@ -228,8 +235,8 @@ def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_
     ``grad_limit``: the backward raises when a gradient reaches it (the reference's
     1e6 guard, ``fused_lqr.py:245``); ``math.inf`` disables the magnitude check.
     ``stash``: ``"auto" | "always" | "never"`` overrides ``TTC_LQR_STASH``.
-    ``precision``: ``"auto" | "fp32" | "fp32-row" | "fp64"`` arithmetic (and, for
-    ``"fp32-row"``, kernel) of the Riccati sweep; see ``riccati_flags``.
+    ``precision``: ``"auto" | "fp32" | "fp32-riccati" | "fp32-row" | "fp64"`` arithmetic
+    (and, for ``"fp32-riccati"`` / ``"fp32-row"``, kernel) of the sweep; see ``riccati_flags``.
     ``stable_backward``: skip the certified Hamiltonian rollout and compute every
     problem's gradients with the stable path.
     """
