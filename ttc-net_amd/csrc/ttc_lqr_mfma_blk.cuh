@@ -35,6 +35,13 @@
 #pragma once
 #include "ttc_lqr_mfma16.cuh"
 
+#ifndef TTC_SYM_WAVES
+#define TTC_SYM_WAVES 3   // waves per SIMD of the symplectic kernel (144 VGPRs, no spills)
+#endif
+#ifndef TTC_SYM_RENORM
+#define TTC_SYM_RENORM 8  // steps between power-of-2 renormalisations of the symplectic sweep
+#endif
+
 namespace ttc {
 
 template <int D, int PPW_, int WPB_, bool SYM_ = false>
@@ -70,7 +77,7 @@ struct MB {
   static constexpr int THREADS = 64 * WPB;
   // two waves per SIMD, except with four problems per wave that keep B and Q in registers;
   // the symplectic sweep's small state leaves room for four
-  static constexpr int MINW = SYM ? 4 : (PPW == 4 && !BQ_LDS) ? 1 : 2;
+  static constexpr int MINW = SYM ? TTC_SYM_WAVES : (PPW == 4 && !BQ_LDS) ? 1 : 2;
   static constexpr int MAXW = MINW;
   static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)SH + (size_t)WPB * PER_WAVE);
 };
@@ -439,7 +446,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   // symplectic_iter.py:226-251, with V_t = Y1^{-1} Y2).  The registers hold Y-hat = Y' in the
   // C layout: Y1' in Y1, Y2' as -N.  With B_k = B diag(beta) and R^{-1} = diag(R_inv):
   //   M = R^{-1} B_k' Y2'      Y1' <- A_k^{-1} (Y1' + B_k M)      Y2' <- A_k Y2' + Qc_k Y1'
-  // (beta enters once, squared, in the row scaling of M).  Every 4 steps the columns of
+  // (beta enters once, squared, in the row scaling of M).  Every TTC_SYM_RENORM steps the columns of
   // Y-hat (rows of Y, which leave Y1^{-1} Y2 unchanged) are rescaled by powers of 2.
   auto sym_step = [&](const int t) {
     if constexpr (G::SYM) {
@@ -456,7 +463,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       v[4 * D + li] = __builtin_amdgcn_rcpf(alpha);
     }
     wave_sync();
-    const bool renorm = ((T - 1 - t) & 3) == 3;
+    const bool renorm = (T - 1 - t) % TTC_SYM_RENORM == TTC_SYM_RENORM - 1;
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
       const float* v = vecs + q * G::VEC;
