@@ -689,9 +689,12 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
   const float a_i = A_diag[p * D + li];
   const float r_i = Rinv[p * D + li];
   const float rr_i = 1.0f / r_i;
+  constexpr float kLog2e = 1.4426950408889634f;
   const float lgB_i = lgB[p * D + li];
   const float lgQ_i = lgQ[p * D + li];
   const float lgA_p = lgA[p];
+  // discounts as exp2 of base-2 exponents, the arithmetic of the forward kernels
+  const float lb2_i = lgB_i * kLog2e, lq2_i = lgQ_i * kLog2e, la2_p = lgA_p * kLog2e;
   float Brow[D], Bcol[D], Qrow[D];
   {
     const float* qg = Qg + n * D * D;
@@ -724,9 +727,9 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
   float gBrow[D], gQrow[D];
   {
     const float u_i = u0g[p * D + li];
-    const float eA = expf(lgA_p);
+    const float eA = __builtin_amdgcn_exp2f(la2_p);
     const float alpha_i = fmaf(a_i, eA, 1.0f);
-    const float beta_i = expf(lgB_i);
+    const float beta_i = __builtin_amdgcn_exp2f(lb2_i);
     v2[li] = beta_i * u_i;
     v3[li] = beta_i * w_i;
     wave_sync();
@@ -782,9 +785,10 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
   for (int t = 1; t < T; ++t) {
     const float tf = (float)t;
     // state cost on h_t:  Qc_t = D_t Q D_t,  D_t = diag(exp(lgQ t))   (torch_lqr.py:55 + chain rule)
-    const float q_i = expf(lgQ_i * tf);
-    v0[li] = q_i * h_i;
-    v1[li] = q_i * hb_i;
+    const float q_i = __builtin_amdgcn_exp2f(lq2_i * tf);
+    const float qh_i = q_i * h_i, qhb_i = q_i * hb_i;
+    v0[li] = qh_i;
+    v1[li] = qhb_i;
     wave_sync();
     float qh[D], qhb[D];
     ld_row<D>(v0, qh);
@@ -794,17 +798,18 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
     for (int c = 0; c < D; ++c) {
       Qh = fmaf(Qrow[c], qh[c], Qh);
       Qhb = fmaf(Qrow[c], qhb[c], Qhb);
-      gQrow[c] = fmaf(0.5f * q_i, fmaf(h_i, qhb[c], hb_i * qh[c]), gQrow[c]);
+      // twice the symmetric gradient of Qc_t (halved after the loop)
+      gQrow[c] = fmaf(qh_i, qhb[c], fmaf(qhb_i, qh[c], gQrow[c]));
     }
     Qh *= q_i;
     Qhb *= q_i;
     glgQ_i = fmaf(tf, fmaf(h_i, Qhb, hb_i * Qh), glgQ_i);
     // step t dynamics
     const float tp1 = tf + 1.0f;
-    const float eA = expf(lgA_p * tp1);
+    const float eA = __builtin_amdgcn_exp2f(la2_p * tp1);
     const float alpha_i = fmaf(a_i, eA, 1.0f);
-    const float beta_i = expf(lgB_i * tp1);
-    const float ia = 1.0f / alpha_i;
+    const float beta_i = __builtin_amdgcn_exp2f(lb2_i * tp1);
+    const float ia = __builtin_amdgcn_rcpf(alpha_i);
     const float lam_n = (lam_i - Qh) * ia;
     const float lamb_n = (lamb_i - Qhb) * ia;
     v2[li] = lam_n;
@@ -845,6 +850,9 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
     lamb_i = lamb_n;
     wave_sync();
   }
+
+#pragma unroll
+  for (int c = 0; c < D; ++c) gQrow[c] *= 0.5f;
 
   // terminal cost: grad Q_f = sym(h_T h~_T'); certificate lambda_T = Q_f h_T
   float gq[D];
