@@ -12,7 +12,9 @@ Prints one JSON line: value = forward+backward LQR solves/s; the forward-only
 rate, tokens/s, the fp32 roofline of the forward kernel (algorithmic flops per
 problem F_fwd = T(4 d^2 du + 2 d^3), timed with HIP events on the launch stream)
 and a CPU baseline (an op-for-op restatement of the reference `riccati` solver,
-fwd and autograd fwd+bwd, on a bounded token sample, all host cores) ride along.
+fwd and autograd fwd+bwd, on a bounded token sample, all host cores) ride along,
+as do configs 3 and 4 on 8,192-token samples (`extra_configs`).
+`--sweep horizon|batch` runs the reference bench's sweeps instead (one line per point).
 """
 from __future__ import annotations
 
@@ -55,6 +57,15 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--fwd-only", action="store_true",
                     help="profiling aid: time only the forward solve (the JSON value is then fwd solves/s)")
+    ap.add_argument("--extra-configs", default="3,4",
+                    help="comma list of further configs measured on a token sample after the main one "
+                         "(forward and fwd+bwd, reported under 'extra_configs'); '' for none")
+    ap.add_argument("--extra-tokens", type=int, default=8192, help="token sample of the extra configs")
+    ap.add_argument("--sweep", default=None, choices=["horizon", "batch"],
+                    help="the reference bench's sweeps (bench_lqr_solvers.py:259-425) on its solver-level "
+                         "distribution (batch 1024, 1 head, d 64, T 64): one JSON line per point with fwd+bwd "
+                         "time, solves/s, FLOP/s and peak memory; skips the main measurement")
+    ap.add_argument("--sweep-dim", type=int, default=64)
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
                     help="profiling aid: run one plain device copy of this many GiB and exit "
                          "(scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
@@ -109,6 +120,120 @@ def cpu_baseline(ins_cpu, T, H, sample_tokens):
                       f"os.cpu_count()={cores}"}
 
 
+def layer_workload(cfg, tokens, dev):
+    """Nine solver inputs of a config (seeded layer front-end on synthetic x) and the d_u
+    that dy ~ N(0,1) induces through the layer back-end (l2norm rescale + out_proj)."""
+    import torch
+    from ttc import TTCLayer
+    from ttc.layers.ttc_layer import l2norm
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+    c = CONFIGS[cfg]
+    torch.manual_seed(0)
+    layer = TTCLayer(c["in_dim"], c["out_dim"], c["h_dim"], c["num_heads"], c["b_rank"], c["q_rank"],
+                     solver_impl="hip").to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    xshape = c["x_shape"] if tokens == 0 else (tokens, c["in_dim"])
+    x = torch.randn(xshape, generator=g, device=dev) * c.get("x_scale", 1.0)
+    if c.get("x_bf16"):
+        x = x.to(torch.bfloat16).float()
+    T = c["T"]
+    with torch.no_grad():
+        ins = [t.float().contiguous() for t in layer.solver_inputs(x)]
+    with torch.no_grad():
+        u0 = hip_lqr_solve(*ins, T)
+    u_req = u0.clone().requires_grad_(True)
+    y = layer.out_proj(l2norm(u_req).reshape(*x.shape[:-1], -1))
+    dy = torch.randn(y.shape, generator=g, device=dev)
+    (d_u,) = torch.autograd.grad(y, u_req, dy)
+    return ins, d_u.contiguous(), list(xshape)
+
+
+def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False):
+    """Forward: mean per-call GPU time from HIP events on the launch stream.  fwd+bwd: wall
+    time of `steps` steps between two device synchronisations."""
+    import torch
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        with torch.no_grad():
+            hip_lqr_solve(*ins, T)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for e0, e1 in evs:
+        e0.record(stream)
+        with torch.no_grad():
+            hip_lqr_solve(*ins, T)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    res = {"fwd_wall_ms": (time.perf_counter() - t0) / steps * 1e3,
+           "fwd_ms": statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)}
+    if fwd_only:
+        return res
+    xs = [t.clone().requires_grad_(True) for t in ins]
+
+    def step():
+        u = hip_lqr_solve(*xs, T, stash=stash)
+        return torch.autograd.grad(u, xs, d_u)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    res["step_ms"] = (time.perf_counter() - t0) / steps * 1e3
+    return res
+
+
+def flops_fwd(d, T):
+    return T * (4 * d * d * d + 2 * d ** 3)
+
+
+def flops_bwd(d, T):
+    return T * (7 * d * d + 11 * d * d)
+
+
+def sweep(args):
+    """Horizon / batch sweeps of the reference bench (bench_lqr_solvers.py:259-425): its
+    solver-level distribution, fwd+bwd median of 5, peak memory above the inputs.  The
+    reference labels 4 * batch * d^3 * T / t as "GB/s"; it is reported here as
+    `ref_metric` next to solves/s and the algorithmic FLOP/s."""
+    import torch
+    from oracle.inputs import bench_solver_inputs
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+    dev = torch.device("cuda:0")
+    d = args.sweep_dim
+    points = [(2 ** i, 1024) for i in range(4, 12)] if args.sweep == "horizon" else [(64, 2 ** i) for i in range(4, 14)]
+    for T, batch in points:
+        ins = [t.to(dev) for t in bench_solver_inputs(batch, 1, d, seed=0)]
+        xs = [t.clone().requires_grad_(True) for t in ins]
+        gr = torch.randn(batch, 1, d, device=dev, generator=torch.Generator(device=dev).manual_seed(1))
+
+        def step():
+            u = hip_lqr_solve(*xs, T)
+            return torch.autograd.grad(u, xs, gr)
+
+        step()
+        torch.cuda.synchronize()
+        ts, peaks = [], []
+        for _ in range(5):
+            torch.cuda.reset_peak_memory_stats()
+            before = torch.cuda.memory_allocated()
+            t0 = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+            peaks.append(torch.cuda.max_memory_allocated() - before)
+        t = statistics.median(ts)
+        print(json.dumps({"sweep": args.sweep, "T": T, "batch": batch, "heads": 1, "d": d,
+                          "fwd_bwd_ms": t * 1e3, "solves_per_s": batch / t,
+                          "tflops": batch * (flops_fwd(d, T) + flops_bwd(d, T)) / t / 1e12,
+                          "ref_metric": 4 * batch * d ** 3 * T * 1e-9 / t,
+                          "peak_mem_gb": statistics.median(peaks) / 1e9}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -126,77 +251,29 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": 4 * n}))
         return
-    from ttc import TTCLayer
-    from ttc.layers.ttc_layer import l2norm
-    from ttc.solvers.hip_lqr import hip_lqr_solve
+    if args.sweep:
+        sweep(args)
+        return
 
     c = CONFIGS[args.config]
     dev = torch.device("cuda:0")
-    torch.manual_seed(0)
-    layer = TTCLayer(c["in_dim"], c["out_dim"], c["h_dim"], c["num_heads"], c["b_rank"], c["q_rank"],
-                     solver_impl="hip").to(dev)
-    g = torch.Generator(device=dev).manual_seed(0)
-    xshape = c["x_shape"] if args.tokens == 0 else (args.tokens, c["in_dim"])
-    x = torch.randn(xshape, generator=g, device=dev) * c.get("x_scale", 1.0)
-    if c.get("x_bf16"):
-        x = x.to(torch.bfloat16).float()
     T, H, d = c["T"], c["num_heads"], c["h_dim"]
-    with torch.no_grad():
-        ins = [t.float().contiguous() for t in layer.solver_inputs(x)]
+    ins, d_u, xshape = layer_workload(args.config, args.tokens, dev)
     N = ins[0].shape[0]
     P = N * H
-    # d_u from dy ~ N(0,1) through the layer back-end (l2norm rescale + out_proj)
-    with torch.no_grad():
-        u0 = hip_lqr_solve(*ins, T)
-    u_req = u0.clone().requires_grad_(True)
-    y = layer.out_proj(l2norm(u_req).reshape(*x.shape[:-1], -1))
-    dy = torch.randn(y.shape, generator=g, device=dev)
-    (d_u,) = torch.autograd.grad(y, u_req, dy)
-    d_u = d_u.contiguous()
-    del y, u_req, u0
-    stream = torch.cuda.current_stream(dev)
-
-    # forward only: per-call GPU time with events on the launch stream
-    for _ in range(args.warmup):
-        with torch.no_grad():
-            hip_lqr_solve(*ins, T)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for e0, e1 in evs:
-        e0.record(stream)
-        with torch.no_grad():
-            hip_lqr_solve(*ins, T)
-        e1.record(stream)
-    torch.cuda.synchronize()
-    fwd_wall = (time.perf_counter() - t0) / args.steps
-    fwd_gpu_ms = statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)
-
+    r = time_solver(ins, d_u, T, args.steps, args.warmup, stash=args.stash, fwd_only=args.fwd_only)
+    fwd_gpu_ms = r["fwd_ms"]
     if args.fwd_only:
         print(json.dumps({"mode": "fwd-only", "fwd_ms": fwd_gpu_ms, "fwd_solves_per_s": P / (fwd_gpu_ms * 1e-3),
                           "problems": P}), flush=True)
         return
+    step_s = r["step_ms"] * 1e-3
 
-    # forward + backward (the timed steps)
-    xs = [t.clone().requires_grad_(True) for t in ins]
-
-    def step():
-        u = hip_lqr_solve(*xs, T, stash=args.stash)
-        return torch.autograd.grad(u, xs, d_u)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / args.steps
-
-    F_fwd = T * (4 * d * d * d + 2 * d ** 3)
+    F_fwd = flops_fwd(d, T)
     achieved = F_fwd * P / (fwd_gpu_ms * 1e-3)
     fwd_bytes = 4 * (3 * d + 2 * d + d * d + 1 + d) + 4 * (d * d + d * d) / H
     traffic = traffic_from_profiles(f"lqr_fwd_cfg{args.config}")
+    kern = f"lqr_fwd_blk_kernel<{d}>" + (" (symplectic sweep)" if d == 16 else " (blocked Riccati)")
     out = {
         "metric": METRIC,
         "value": P / step_s,
@@ -211,20 +288,37 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded N(0,1) x, random-init layer weights)",
         "config": {"workload": f"cfg{args.config}: TTCLayer(in={c['in_dim']},out={c['out_dim']},h={d},heads={H},"
-                               f"b_rank={c['b_rank']},q_rank={c['q_rank']}) T={T}, x{list(xshape)} -> "
+                               f"b_rank={c['b_rank']},q_rank={c['q_rank']}) T={T}, x{xshape} -> "
                                f"{N} tokens, {P} LQR problems, solver fwd+bwd",
                    "tokens": N, "heads": H, "d": d, "du": d, "T": T, "problems": P},
         "fwd_solves_per_s": P / (fwd_gpu_ms * 1e-3),
         "fwd_ms": fwd_gpu_ms,
-        "fwd_wall_ms": fwd_wall * 1e3,
+        "fwd_wall_ms": r["fwd_wall_ms"],
         "tokens_per_s_fwd_bwd": N / step_s,
         "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
-                     "kernel": f"lqr_fwd_blk_kernel<{d}>" + (" (symplectic sweep)" if d == 16 else " (blocked Riccati)"),
-                     "flops_per_problem": F_fwd,
+                     "kernel": kern, "flops_per_problem": F_fwd,
                      "algorithmic_bytes_per_problem": fwd_bytes},
     }
+    extras = []
+    for cfg in [int(x) for x in args.extra_configs.split(",") if x.strip()]:
+        if cfg == args.config:
+            continue
+        ce = CONFIGS[cfg]
+        Te, He, de = ce["T"], ce["num_heads"], ce["h_dim"]
+        ins_e, du_e, xs_e = layer_workload(cfg, args.extra_tokens, dev)
+        Pe = ins_e[0].shape[0] * He
+        re_ = time_solver(ins_e, du_e, Te, 3, 1)
+        ach = flops_fwd(de, Te) * Pe / (re_["fwd_ms"] * 1e-3)
+        extras.append({"config": f"cfg{cfg}", "x": xs_e, "d": de, "T": Te, "heads": He, "problems": Pe,
+                       "fwd_ms": re_["fwd_ms"], "fwd_solves_per_s": Pe / (re_["fwd_ms"] * 1e-3),
+                       "fwd_bwd_ms": re_["step_ms"], "fwd_bwd_solves_per_s": Pe / (re_["step_ms"] * 1e-3),
+                       "roofline_frac": ach / PEAK_FP32_MFMA, "achieved_tflops": ach / 1e12,
+                       "traffic": traffic_from_profiles(f"lqr_fwd_cfg{cfg}")})
+        del ins_e, du_e
+        torch.cuda.empty_cache()
+    out["extra_configs"] = extras
     if not args.no_cpu_baseline:
         ins_cpu = [t.detach().cpu() for t in ins]
         out["cpu_baseline"] = cpu_baseline(ins_cpu, T, H, min(args.cpu_sample_tokens, N))
