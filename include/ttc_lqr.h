@@ -24,7 +24,8 @@
  *   - `status` (device int32, caller-zeroed, may be NULL) receives bit flags:
  *     TTC_LQR_STATUS_NONFINITE if any output is NaN/Inf, TTC_LQR_STATUS_LARGE if
  *     a gradient has |g| >= grad_limit.  The caller reads it after the stream
- *     completes and raises (the reference raises RuntimeError, fused_lqr.py:101,246).
+ *     completes and raises on those two bits (the reference raises RuntimeError,
+ *     fused_lqr.py:101,246); TTC_LQR_STATUS_RESCUED is informational.
  *   - Q and Q_f enter through their symmetric parts; the Q / Q_f gradients are
  *     the symmetric gradients (as the reference's fused/kkt solvers return).
  *   - Thread-safe and re-entrant; calls that share a workspace or stash must be
@@ -47,6 +48,10 @@ extern "C" {
 
 #define TTC_LQR_STATUS_NONFINITE 1
 #define TTC_LQR_STATUS_LARGE 2
+/* Informational, not an error: the forward's matrix-core kernel handed some problems to
+ * its rescue pass (pivoted row-layout recompute).  The rescue pass skips its scan when
+ * `status` is given and this bit is clear. */
+#define TTC_LQR_STATUS_RESCUED 4
 
 /* `flags` bits.  TTC_LQR_FLAG_FP64_RICCATI runs the backward-in-time Riccati sweep
  * (the gains) in fp64 arithmetic; inputs, outputs and the stash stay fp32.  Needed

@@ -1,5 +1,5 @@
 // ttc_lqr_d16_sym.hip -- launcher of the d = du = 16 symplectic matrix-core forward kernel
-// and its rescue pass (row-layout recompute of the problems the certificate rejects).
+// and its rescue pass (the per-step Riccati kernel on the problems the certificate rejects).
 #include "ttc_lqr_mfma_blk.cuh"
 
 namespace ttc {
@@ -12,7 +12,12 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
   const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
   hipLaunchKernelGGL((lqr_fwd_blk_kernel<16, 4, 1, SM, WU, true>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA,
                      lB, lQ, h0, P, H, T, u, st_a, st_b, status);
-  launch_rescue_k<16, SM, WU>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+  // rescue: the per-step Riccati kernel on the marked problems (its own breakdown guard
+  // finishes on the pivoted row-layout sweep)
+  const int64_t groups = (P + 3) / 4;
+  hipLaunchKernelGGL((lqr_rescue16_mfma_kernel<SM, WU>), dim3((unsigned)(groups < 2048 ? groups : 2048)),
+                     dim3(M16::THREADS), M16::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b,
+                     status);
 }
 
 // Stash modes STASH_NONE and STASH_V1; the per-step gains (STASH_GAINS) come from the

@@ -929,7 +929,8 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
 // kernels mark the problems whose Cholesky pivot broke down; a problem whose genuine
 // result is NaN is recomputed too and keeps its NaN.  Each block of one wave walks the
 // problems in strides of 64: one marker load per lane, a ballot, then PPW = 64 / D
-// marked problems at a time (lane li of group qo owns row li of problem qo).
+// marked problems at a time (lane li of group qo owns row li of problem qo).  With a status
+// word, the scan runs only when the forward set TTC_LQR_STATUS_RESCUED in it.
 // ---------------------------------------------------------------------------
 template <int D>
 struct Rescue {
@@ -952,6 +953,8 @@ __global__ __launch_bounds__(64) void lqr_rescue_kernel(
   const int li = lane % D;
   float* Bs = smem + qo * Rescue<D>::PER;
   float* S = Bs + Geo<D>::MAT;
+  // nothing was marked (the forward sets the bit when it marks a problem)
+  if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
   const float* mark = WRITE_U ? u_out : q0stash;
   const int64_t mstride = WRITE_U ? D : (int64_t)D * D;
   for (int64_t base = (int64_t)blockIdx.x * 64; base < P; base += (int64_t)gridDim.x * 64) {

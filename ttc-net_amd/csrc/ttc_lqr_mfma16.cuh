@@ -109,28 +109,36 @@ __device__ __forceinline__ void st4(float* p, v4f v) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-template <int SM, bool WRITE_U>
-__global__ __launch_bounds__(M16::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void lqr_fwd16_mfma_kernel(
+// The sweep of the 4 problems pbase .. pbase+3 (one wave).  RESCUE: only the problems a
+// matrix-core forward marked with a NaN (u[p][0], or Quu_0[p][0][0] without u) are stored,
+// and the wave returns at once when none of its 4 problems is marked.
+template <int SM, bool WRITE_U, bool RESCUE>
+__device__ __forceinline__ void fwd16_group(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
     int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
-    float* __restrict__ q0stash, int* __restrict__ status) {
+    float* __restrict__ q0stash, int* __restrict__ status, const int64_t pbase) {
   extern __shared__ __align__(16) float sm[];
   constexpr float kLog2e = 1.4426950408889634f;
   const int lane = threadIdx.x;
   const int g = lane >> 4;  // lane group: MFMA row block, and "my problem" in the row layout
   const int c = lane & 15;  // MFMA column, and "my row" in the row layout
-  const int64_t pbase = (int64_t)blockIdx.x * 4;
 
   int64_t pid[4];
   float* buf[4];
+  bool pv[4];  // problem q exists (and, when rescuing, is marked): its results are stored
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     pid[q] = (pbase + q < P) ? (pbase + q) : (P - 1);  // idle problems recompute a real one, never store
     buf[q] = sm + q * M16::PER_PROB;
+    pv[q] = pbase + q < P;
+    if constexpr (RESCUE) pv[q] = pv[q] && isnan(WRITE_U ? u_out[pid[q] * 16] : q0stash[pid[q] * 256]);
   }
-  const bool own_valid = pbase + g < P;
+  if constexpr (RESCUE) {
+    if (!(pv[0] || pv[1] || pv[2] || pv[3])) return;
+  }
+  const bool own_valid = pv[g];
   const int64_t po = pid[g];
   float* own = sm + g * M16::PER_PROB;  // (not buf[g]: a dynamically indexed pointer loses its LDS address space)
   float* vA = sm + M16::OFF_VEC;  // alpha [q][i]
@@ -189,7 +197,7 @@ __global__ __launch_bounds__(M16::THREADS) __attribute__((amdgpu_waves_per_eu(2,
       // compact stash: V_1 (the value entering step 0), rows 4g..4g+3 of column c
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        if (pbase + q < P) {
+        if (pv[q]) {
           float* vp = kstash + (pid[q] * 16 + 4 * g) * 16 + c;
 #pragma unroll
           for (int r = 0; r < 4; ++r) vp[r * 16] = -Nc[q][r];
@@ -286,7 +294,7 @@ __global__ __launch_bounds__(M16::THREADS) __attribute__((amdgpu_waves_per_eu(2,
         v4f kt = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) kt = mfma16x16x4(u4[s], m4[s], kt);
-        const bool qvalid = pbase + q < P;
+        const bool qvalid = pv[q];
 #pragma unroll
         for (int r = 0; r < 4; ++r) kt[r] *= acol[q];  // K[4g+r][c]
         if (SM == STASH_GAINS && qvalid) {
@@ -353,6 +361,36 @@ __global__ __launch_bounds__(M16::THREADS) __attribute__((amdgpu_waves_per_eu(2,
       t -= failed ? 0 : 1;
     }
     if (failed || step(std::true_type{}, 0)) row_sweep_from(t);
+  }
+}
+
+template <int SM, bool WRITE_U>
+__global__ __launch_bounds__(M16::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void lqr_fwd16_mfma_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
+    float* __restrict__ q0stash, int* __restrict__ status) {
+  fwd16_group<SM, WRITE_U, false>(A_diag, Bg, Qg, Rinv, Qf, lgA, lgB, lgQ, h0, P, H, T, u_out, kstash, q0stash,
+                                  status, (int64_t)blockIdx.x * 4);
+}
+
+// Rescue pass after the d = 16 symplectic forward: the per-step Riccati sweep (with its own
+// breakdown guard and row-layout finish) of every marked problem.  A small grid walks the
+// 4-problem groups; it returns at once when `status` is given without
+// TTC_LQR_STATUS_RESCUED (nothing was marked).
+template <int SM, bool WRITE_U>
+__global__ __launch_bounds__(M16::THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void lqr_rescue16_mfma_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
+    float* __restrict__ q0stash, int* __restrict__ status) {
+  if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
+  for (int64_t pb = (int64_t)blockIdx.x * 4; pb < P; pb += (int64_t)gridDim.x * 4) {
+    fwd16_group<SM, WRITE_U, true>(A_diag, Bg, Qg, Rinv, Qf, lgA, lgB, lgQ, h0, P, H, T, u_out, kstash, q0stash,
+                                   status, pb);
+    wave_sync();  // the group's LDS is reused by the next one
   }
 }
 

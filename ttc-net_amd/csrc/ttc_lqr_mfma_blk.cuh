@@ -85,8 +85,8 @@ struct MB {
 // Certificate of the symplectic sweep (d = 16): the final solve P = Y1^{-1} Y2 is accepted when
 // cond_inf(Y1) <= kSymCondMax and max|P - P'| <= kSymAsymMax max|P|; problems that miss it are
 // recomputed by the rescue pass.
-constexpr float kSymCondMax = 1.0e3f;
-constexpr float kSymAsymMax = 1.0e-5f;
+constexpr float kSymCondMax = 1.0e7f;
+constexpr float kSymAsymMax = 1.0e-6f;
 
 // max over the D lanes of a problem (D = 16, 32, 64)
 template <int D>
@@ -691,6 +691,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     const float nan = __builtin_nanf("");
     if (WRITE_U) u_out[(pbase + lane) * D] = nan;
     else q0stash[(pbase + lane) * D * D] = nan;
+    if (status != nullptr) atomicOr(status, TTC_LQR_STATUS_RESCUED);
   }
 }
 

@@ -41,7 +41,9 @@ in half of the device memory available at forward time (free on the device plus
 held unallocated by torch's caching allocator), capped by
 ``TTC_LQR_STASH_MAX_BYTES`` if set) | ``always`` | ``never`` (the backward then
 recomputes it with one forward sweep).
-``TTC_LQR_WORKSPACE_BYTES``: backward workspace per call (default 4 GiB).
+``TTC_LQR_WORKSPACE_BYTES``: backward workspace per call (default: 16 GiB or half of the
+memory available at backward time, whichever is smaller; the library splits the tokens
+into passes that fit, and one pass is fastest).
 """
 from __future__ import annotations
 
@@ -59,6 +61,7 @@ SUPPORTED_DIMS = (16, 32, 64)
 FP64_HORIZON = 512
 _FWD_MSG = "Numerical instability detected during fused LQR forward recurrence."
 _BWD_MSG = "Numerical instability detected during fused LQR backward pass."
+_ERROR_BITS = 1 | 2  # TTC_LQR_STATUS_NONFINITE | TTC_LQR_STATUS_LARGE (4 = RESCUED is informational)
 
 # problems / fallback problems of the most recent backward call (observability)
 last_backward_stats = {"problems": 0, "fallback": 0}
@@ -173,7 +176,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
             rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, flags, u.data_ptr(),
                                      None if st is None else st.data_ptr(), status.data_ptr(), _stream_handle(dev))
         check(rc, "ttc_lqr_forward")
-        if int(status.item()) != 0:
+        if int(status.item()) & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
             ctx.save_for_backward(*f32, u, *([st] if st is not None else []))
@@ -189,8 +192,11 @@ class HipLQRSolveFunc(torch.autograd.Function):
         u = saved[9]
         st = saved[10] if has_stash else None
         dev = f32[0].device
-        dU = torch.zeros(bs, nh, Dp, device=dev, dtype=torch.float32)
-        dU[..., :du] = d_u.to(torch.float32)
+        if du == Dp:
+            dU = d_u.to(torch.float32).contiguous()
+        else:
+            dU = torch.zeros(bs, nh, Dp, device=dev, dtype=torch.float32)
+            dU[..., :du] = d_u.to(torch.float32)
         g = {
             "A": torch.empty(bs, nh, Dp, device=dev), "B": torch.empty(bs, Dp, Dp, device=dev),
             "Q": torch.empty(bs, Dp, Dp, device=dev), "R": torch.empty(bs, nh, Dp, device=dev),
@@ -199,7 +205,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
             "h0": torch.empty(bs, nh, Dp, device=dev),
         }
         status = torch.zeros(1, device=dev, dtype=torch.int32)
-        budget = _env_bytes("TTC_LQR_WORKSPACE_BYTES", 4 << 30)
+        budget = _env_bytes("TTC_LQR_WORKSPACE_BYTES", min(16 << 30, max(1 << 30, _stash_budget(dev))))
         with_st = 1 if st is not None else 0
         # one pass over all tokens when it fits the budget; the library picks the largest
         # token chunk that fits whatever it is given (at least one token's worth)
@@ -217,7 +223,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
                 ws.data_ptr(), ws.numel(), limit, status.data_ptr(), ctypes.byref(n_fb), _stream_handle(dev))
         check(rc, "ttc_lqr_backward")
         last_backward_stats.update(problems=bs * nh, fallback=int(n_fb.value))
-        if int(status.item()) != 0:
+        if int(status.item()) & _ERROR_BITS:
             raise RuntimeError(_BWD_MSG)
         out = (g["A"][..., :d], g["B"][:, :d, :du], g["Q"][:, :d, :d], g["R"][..., :du], g["Qf"][:, :, :d, :d],
                g["lA"], g["lB"][..., :du], g["lQ"][..., :d], g["h0"][..., :d])
