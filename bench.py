@@ -61,11 +61,16 @@ def parse():
                     help="comma list of further configs measured on a token sample after the main one "
                          "(forward and fwd+bwd, reported under 'extra_configs'); '' for none")
     ap.add_argument("--extra-tokens", type=int, default=8192, help="token sample of the extra configs")
+    ap.add_argument("--factored", action="store_true",
+                    help="measure the solver on the layer's low-rank factors (coeff_B, coeff_Q, coeff_Qf + bases, "
+                         "expanded per token chunk on the device) instead of materialised B, Q, Q_f: the only "
+                         "form in which configs 3 and 4 fit one GPU at full size")
     ap.add_argument("--sweep", default=None, choices=["horizon", "batch"],
                     help="the reference bench's sweeps (bench_lqr_solvers.py:259-425) on its solver-level "
                          "distribution (batch 1024, 1 head, d 64, T 64): one JSON line per point with fwd+bwd "
                          "time, solves/s, FLOP/s and peak memory; skips the main measurement")
     ap.add_argument("--sweep-dim", type=int, default=64)
+    ap.add_argument("--progress", action="store_true", help="print a line to stderr after every solver call")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
                     help="profiling aid: run one plain device copy of this many GiB and exit "
                          "(scales rocprofv3 FETCH_SIZE/WRITE_SIZE to bytes)")
@@ -120,13 +125,18 @@ def cpu_baseline(ins_cpu, T, H, sample_tokens):
                       f"os.cpu_count()={cores}"}
 
 
-def layer_workload(cfg, tokens, dev):
-    """Nine solver inputs of a config (seeded layer front-end on synthetic x) and the d_u
-    that dy ~ N(0,1) induces through the layer back-end (l2norm rescale + out_proj)."""
+def _solver_for(ins):
+    from ttc.solvers.hip_lqr import hip_lqr_solve, hip_lqr_solve_factored
+    return hip_lqr_solve_factored if len(ins) == 11 else hip_lqr_solve
+
+
+def layer_workload(cfg, tokens, dev, factored=False):
+    """Solver inputs of a config (seeded layer front-end on synthetic x: the nine materialised
+    inputs, or with `factored` the eleven low-rank ones) and the d_u that dy ~ N(0,1) induces
+    through the layer back-end (l2norm rescale + out_proj)."""
     import torch
     from ttc import TTCLayer
     from ttc.layers.ttc_layer import l2norm
-    from ttc.solvers.hip_lqr import hip_lqr_solve
     c = CONFIGS[cfg]
     torch.manual_seed(0)
     layer = TTCLayer(c["in_dim"], c["out_dim"], c["h_dim"], c["num_heads"], c["b_rank"], c["q_rank"],
@@ -138,9 +148,11 @@ def layer_workload(cfg, tokens, dev):
         x = x.to(torch.bfloat16).float()
     T = c["T"]
     with torch.no_grad():
-        ins = [t.float().contiguous() for t in layer.solver_inputs(x)]
-    with torch.no_grad():
-        u0 = hip_lqr_solve(*ins, T)
+        front = layer.factored_inputs(x) if factored else layer.solver_inputs(x)
+        ins = [t.detach().float().contiguous() for t in front]
+        del front
+        u0 = _solver_for(ins)(*ins, T)
+    _note(f"workload cfg{cfg}: {ins[0].shape[0]} tokens, factored={factored}")
     u_req = u0.clone().requires_grad_(True)
     y = layer.out_proj(l2norm(u_req).reshape(*x.shape[:-1], -1))
     dy = torch.randn(y.shape, generator=g, device=dev)
@@ -148,15 +160,24 @@ def layer_workload(cfg, tokens, dev):
     return ins, d_u.contiguous(), list(xshape)
 
 
+PROGRESS = False
+
+
+def _note(msg):
+    if PROGRESS:
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False):
     """Forward: mean per-call GPU time from HIP events on the launch stream.  fwd+bwd: wall
     time of `steps` steps between two device synchronisations."""
     import torch
-    from ttc.solvers.hip_lqr import hip_lqr_solve
+    hip_lqr_solve = _solver_for(ins)
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
+    for i in range(warmup):
         with torch.no_grad():
             hip_lqr_solve(*ins, T)
+        _note(f"warm-up forward {i + 1}/{warmup}")
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     t0 = time.perf_counter()
@@ -165,6 +186,7 @@ def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False):
         with torch.no_grad():
             hip_lqr_solve(*ins, T)
         e1.record(stream)
+        _note("timed forward")
     torch.cuda.synchronize()
     res = {"fwd_wall_ms": (time.perf_counter() - t0) / steps * 1e3,
            "fwd_ms": statistics.mean(e0.elapsed_time(e1) for e0, e1 in evs)}
@@ -176,14 +198,18 @@ def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False):
         u = hip_lqr_solve(*xs, T, stash=stash)
         return torch.autograd.grad(u, xs, d_u)
 
-    for _ in range(warmup):
+    for i in range(warmup):
         step()
+        _note(f"warm-up fwd+bwd {i + 1}/{warmup}")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for i in range(steps):
         step()
+        _note(f"timed fwd+bwd {i + 1}/{steps}")
     torch.cuda.synchronize()
     res["step_ms"] = (time.perf_counter() - t0) / steps * 1e3
+    from ttc.solvers.hip_lqr import last_backward_stats
+    res["bwd_fallback_problems"] = last_backward_stats["fallback"]
     return res
 
 
@@ -235,7 +261,9 @@ def sweep(args):
 
 
 def main():
+    global PROGRESS
     args = parse()
+    PROGRESS = args.progress
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the LQR problems shard over tokens with no "
                                    "exchange, so a multi-GPU figure is not produced here (see DESIGN.md)",
@@ -258,7 +286,7 @@ def main():
     c = CONFIGS[args.config]
     dev = torch.device("cuda:0")
     T, H, d = c["T"], c["num_heads"], c["h_dim"]
-    ins, d_u, xshape = layer_workload(args.config, args.tokens, dev)
+    ins, d_u, xshape = layer_workload(args.config, args.tokens, dev, factored=args.factored)
     N = ins[0].shape[0]
     P = N * H
     r = time_solver(ins, d_u, T, args.steps, args.warmup, stash=args.stash, fwd_only=args.fwd_only)
@@ -289,11 +317,14 @@ def main():
         "data": "synthetic (seeded N(0,1) x, random-init layer weights)",
         "config": {"workload": f"cfg{args.config}: TTCLayer(in={c['in_dim']},out={c['out_dim']},h={d},heads={H},"
                                f"b_rank={c['b_rank']},q_rank={c['q_rank']}) T={T}, x{xshape} -> "
-                               f"{N} tokens, {P} LQR problems, solver fwd+bwd",
+                               f"{N} tokens, {P} LQR problems, solver fwd+bwd"
+                               + (" on the layer's low-rank factors (B, Q, Q_f expanded on the device)"
+                                  if args.factored else ""),
                    "tokens": N, "heads": H, "d": d, "du": d, "T": T, "problems": P},
         "fwd_solves_per_s": P / (fwd_gpu_ms * 1e-3),
         "fwd_ms": fwd_gpu_ms,
         "fwd_wall_ms": r["fwd_wall_ms"],
+        "bwd_fallback_problems": r["bwd_fallback_problems"],
         "tokens_per_s_fwd_bwd": N / step_s,
         "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
@@ -319,8 +350,23 @@ def main():
         del ins_e, du_e
         torch.cuda.empty_cache()
     out["extra_configs"] = extras
+    if not args.factored:
+        # the layer's default path: the same solve on the low-rank factors, B / Q / Q_f expanded per
+        # token chunk on the device (no [N,H,d,d] Q_f in HBM)
+        ins_f, du_f, _ = layer_workload(args.config, args.tokens, dev, factored=True)
+        rf = time_solver(ins_f, du_f, T, 3, 1, stash=args.stash)
+        out["factored"] = {"fwd_ms": rf["fwd_ms"], "fwd_bwd_ms": rf["step_ms"],
+                           "fwd_bwd_solves_per_s": P / (rf["step_ms"] * 1e-3),
+                           "input_bytes_per_problem": 4 * (5 * d + 1 + (c["b_rank"] + c["q_rank"]) / H + c["q_rank"])}
+        del ins_f, du_f
+        torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
-        ins_cpu = [t.detach().cpu() for t in ins]
+        n_s = min(args.cpu_sample_tokens, N)
+        ins_cpu = [t.detach()[:n_s].cpu() if i < 9 else t.detach().cpu() for i, t in enumerate(ins)]
+        if len(ins_cpu) == 11:  # the reference solver takes materialised B, Q, Q_f
+            A, cB, cQ, R, cQf, lA, lB, lQ, h0, Bs, Gs = ins_cpu
+            ins_cpu = [A, torch.einsum("nr,rij->nij", cB, Bs), torch.einsum("nr,rij->nij", cQ, Gs), R,
+                       torch.einsum("nhr,rij->nhij", cQf, Gs), lA, lB, lQ, h0]
         out["cpu_baseline"] = cpu_baseline(ins_cpu, T, H, min(args.cpu_sample_tokens, N))
     else:
         out["cpu_baseline"] = None

@@ -140,6 +140,59 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
                      size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
                      void* stream);
 
+/* ---- Factored inputs: the low-rank front-end of TTCLayer (ttc/layers/ttc_layer.py:117-123) ----
+ * Instead of B, Q, Q_f the solver takes the layer's mixture coefficients and bases:
+ *   coeff_B [N,rb]  coeff_Q [N,rq]  coeff_Qf [N,H,rq]  B_basis [rb,d,du]  Q_basis [rq,d,d]
+ *   B_n = sum_r coeff_B[n,r] B_basis[r],  Q_n = sum_r coeff_Q[n,r] Q_basis[r],
+ *   Q_f[n,h] = sum_r coeff_Qf[n,h,r] Q_basis[r]
+ * (the reference's einsums "...r,rmn->...mn"; for q_reparam="cholesky" the caller passes
+ * Q_basis[r] = Qs[r] Qs[r]' / sqrt(h_dim)).  The library expands them token chunk by
+ * token chunk inside `workspace` just before the solver kernels read them, so the
+ * [N,H,d,d] Q_f (137 GB at d = 64, 8.4 M problems) and its gradient never exist in full.
+ * Ranks 1..64; basis pointers 16-byte aligned.  Results equal ttc_lqr_forward /
+ * ttc_lqr_backward on the expanded tensors (same kernels), up to the fp32 rounding of
+ * the expansion.  No counterpart in the reference (whose layer materialises B, Q, Q_f),
+ * proposed as its next component; the entry points keep the conventions above. */
+
+/* Workspace bytes of the factored entry points for `chunk_tokens` tokens per pass:
+ * backward = 0 for ttc_lqr_forward_factored (the expanded B, Q, Q_f of a chunk),
+ * backward != 0 for ttc_lqr_backward_factored (plus the chunk's B / Q / Q_f gradients,
+ * the reduction partials and ttc_lqr_backward's own workspace). */
+size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du,
+                                        int32_t b_rank, int32_t q_rank, int32_t T, int32_t with_stash,
+                                        int32_t backward);
+
+/* Forward on factored inputs; u, stash, status and flags as ttc_lqr_forward.
+ * workspace_bytes >= ttc_lqr_factored_workspace_bytes(1, ..., backward = 0). */
+int ttc_lqr_forward_factored(const float* A_diag, const float* coeff_B, const float* coeff_Q,
+                             const float* R_inv, const float* coeff_Qf, const float* log_gamma_A,
+                             const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
+                             const float* B_basis, const float* Q_basis, int64_t n_tokens, int32_t heads,
+                             int32_t d, int32_t du, int32_t b_rank, int32_t q_rank, int32_t T,
+                             int32_t flags, float* u, float* stash, void* workspace, size_t workspace_bytes,
+                             int32_t* status, void* stream);
+
+/* Backward on factored inputs: the gradients of sum(d_u * u) w.r.t. the eleven inputs.
+ * grad_coeff_B [N,rb] = <grad_B_n, B_basis[r]>, grad_coeff_Q [N,rq], grad_coeff_Qf [N,H,rq]
+ * likewise with Q_basis, grad_B_basis [rb,d,du] = sum_n coeff_B[n,r] grad_B_n and
+ * grad_Q_basis [rq,d,d] = sum_n coeff_Q[n,r] grad_Q_n + sum_(n,h) coeff_Qf[n,h,r] grad_Q_f[n,h],
+ * where grad_B / grad_Q / grad_Q_f are ttc_lqr_backward's (head-summed, symmetric).  The
+ * basis gradients are summed in a fixed order (deterministic).  grad_limit and the status
+ * bits apply to grad_B / grad_Q / grad_Q_f as in ttc_lqr_backward.
+ * workspace_bytes >= ttc_lqr_factored_workspace_bytes(1, ..., backward = 1). */
+int ttc_lqr_backward_factored(const float* A_diag, const float* coeff_B, const float* coeff_Q,
+                              const float* R_inv, const float* coeff_Qf, const float* log_gamma_A,
+                              const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
+                              const float* B_basis, const float* Q_basis, const float* u, const float* d_u,
+                              int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t b_rank,
+                              int32_t q_rank, int32_t T, int32_t flags, const float* stash,
+                              float* grad_A_diag, float* grad_coeff_B, float* grad_coeff_Q,
+                              float* grad_R_inv, float* grad_coeff_Qf, float* grad_log_gamma_A,
+                              float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0,
+                              float* grad_B_basis, float* grad_Q_basis, void* workspace,
+                              size_t workspace_bytes, float grad_limit, int32_t* status,
+                              int64_t* n_fallback, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

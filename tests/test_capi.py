@@ -29,7 +29,8 @@ def L():
 def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
-        "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes"])
+        "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes",
+        "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -113,3 +114,40 @@ def test_backward_argument_validation(L):
     empty = head + [0, 1, 16, 16, 4, 0, None] + [p] * 9
     assert L.ttc_lqr_backward(*empty, p, 0, float("inf"), None, ctypes.byref(n_fb), None) == 0
     assert n_fb.value == 0
+
+
+def test_factored_workspace_bytes(L):
+    # forward: the expanded B, Q (per token) and Q_f (per problem) of one chunk
+    N, H, d, T = 1000, 8, 16, 64
+    f = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0)
+    assert 4 * N * (2 * d * d + H * d * d) <= f < 4 * N * (2 * d * d + H * d * d) + 1024
+    # backward: also the chunk's gradients of B, Q, Q_f and ttc_lqr_backward's own workspace
+    b = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1)
+    assert b >= 2 * f + L.ttc_lqr_workspace_bytes(N, H, d, d, T, 1)
+    assert L.ttc_lqr_factored_workspace_bytes(2 * N, H, d, d, 16, 16, T, 1, 1) > b
+    for bad in [(N, H, d, d, 0, 16), (N, H, d, d, 16, 65), (0, H, d, d, 16, 16), (N, H, 16, 32, 16, 16)]:
+        assert L.ttc_lqr_factored_workspace_bytes(*bad, T, 0, 0) == 0
+
+
+def test_factored_argument_validation(L):
+    p = ctypes.c_void_p(16)
+    odd = ctypes.c_void_p(20)   # not 16-byte aligned
+    ws = 1 << 30
+
+    def fwd(n=1, rb=16, rq=16, basis=p, work=ws, d=16):
+        return L.ttc_lqr_forward_factored(*([p] * 9), basis, basis, n, 1, d, d, rb, rq, 4, 0, p, None, p, work,
+                                          None, None)
+    assert fwd(rb=0) == 1 and fwd(rq=65) == 1 and fwd(n=-1) == 1
+    assert fwd(d=24) == 2
+    assert fwd(basis=odd) == 1
+    assert fwd(work=16) == 1                  # workspace below one token's expansion
+    assert fwd(n=0) == 0
+
+    def bwd(rb=16, basis=p, work=ws):
+        n_fb = ctypes.c_int64(-3)
+        rc = L.ttc_lqr_backward_factored(*([p] * 9), basis, basis, p, p, 1, 1, 16, 16, rb, 16, 4, 0, None,
+                                         *([p] * 11), p, work, float("inf"), None, ctypes.byref(n_fb), None)
+        return rc, n_fb.value
+    assert bwd(rb=70) == (1, 0)
+    assert bwd(basis=odd) == (1, 0)
+    assert bwd(work=64) == (1, 0)

@@ -235,6 +235,169 @@ static Compact compact_at(char* base, int64_t F64, int d, int du) {
   return c;
 }
 
+// Gradients of n_tokens tokens (inputs already validated), token chunk by token chunk
+// inside ws: the certified Hamiltonian rollout with its per-problem fallback, or the
+// stable path for every problem under TTC_LQR_FLAG_STABLE_BWD.  v1s / q0s: the forward's
+// stash halves (V_1 [P,d,d], Quu_0 [P,du,du]) or null to recompute them per chunk.
+static int backward_core(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
+                         const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q,
+                         const float* h0, const float* u, const float* d_u, int64_t n_tokens, int H, int d, int du,
+                         int T, int flags, const float* v1s, const float* q0s, float* grad_A_diag, float* grad_B,
+                         float* grad_Q, float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A,
+                         float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0, char* ws,
+                         size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
+                         hipStream_t s) {
+  if (flags & TTC_LQR_FLAG_STABLE_BWD) {
+    if (n_fallback) *n_fallback = n_tokens * H;
+    return stable_backward(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, d_u, n_tokens, H, d,
+                           T, flags, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f, grad_log_gamma_A,
+                           grad_log_gamma_B, grad_log_gamma_Q, grad_h0, ws, workspace_bytes, grad_limit, status, s);
+  }
+  const bool with_stash = v1s != nullptr;
+  // largest token chunk whose layout fits the workspace (the layout grows with the chunk)
+  if (workspace_bytes < fast_layout(1, H, d, du, T, with_stash).total) return TTC_LQR_EINVAL;
+  int64_t chunk = 1, hi = n_tokens;
+  while (chunk < hi) {
+    const int64_t mid = chunk + (hi - chunk + 1) / 2;
+    if (fast_layout(mid, H, d, du, T, with_stash).total <= workspace_bytes) chunk = mid;
+    else hi = mid - 1;
+  }
+  const int64_t dd = (int64_t)d * d;
+  const float tau = TTC_LQR_CERT_TOL;
+  int64_t total_fb = 0;
+  for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
+    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
+    const int64_t p0 = n0 * H, Pc = nc * H;
+    const FastLayout L = fast_layout(nc, H, d, du, T, with_stash);
+    const float *a = A_diag + p0 * d, *b = B + n0 * dd, *q = Q + n0 * dd, *r = R_inv + p0 * du;
+    const float *qf = Q_f + p0 * dd, *la = log_gamma_A + p0, *lb = log_gamma_B + p0 * du;
+    const float *lq = log_gamma_Q + p0 * d, *hz = h0 + p0 * d, *dz = d_u + p0 * du, *uz = u + p0 * du;
+    float *gA = grad_A_diag + p0 * d, *gR = grad_R_inv + p0 * du, *gQf = grad_Q_f + p0 * dd;
+    float *glA = grad_log_gamma_A + p0, *glB = grad_log_gamma_B + p0 * du, *glQ = grad_log_gamma_Q + p0 * d;
+    float* gh = grad_h0 + p0 * d;
+    const float *v1, *q0;
+    int rc = TTC_LQR_OK;
+    if (with_stash) {
+      v1 = v1s + p0 * dd;
+      q0 = q0s + p0 * (int64_t)du * du;
+    } else {
+      float* v1w = reinterpret_cast<float*>(ws + L.v1);
+      float* q0w = reinterpret_cast<float*>(ws + L.q0);
+      rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, Pc, H, T, nullptr, v1w, q0w, kStashV1, nullptr, s, flags);
+      if (rc != TTC_LQR_OK) return rc;
+      v1 = v1w;
+      q0 = q0w;
+    }
+    float* gBp = reinterpret_cast<float*>(ws + L.gBp);
+    float* gQp = reinterpret_cast<float*>(ws + L.gQp);
+    int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
+    int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
+    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
+    switch (d) {
+      case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
+      case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
+      case 64: rc = launch_ham_d64(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
+      default: return TTC_LQR_EUNSUPPORTED;
+    }
+    if (rc != TTC_LQR_OK) return rc;
+    // how many problems the certificate rejected (one stream synchronisation per chunk)
+    int32_t nfail = 0;
+    if (hipMemcpyAsync(&nfail, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;
+    if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
+    if (nfail < 0 || nfail > Pc) return TTC_LQR_ELAUNCH;
+    total_fb += nfail;
+    const Compact c = compact_at(ws + L.fb, L.F, d, du);
+    for (int64_t f0 = 0; f0 < nfail; f0 += L.F) {
+      const int64_t fc = (f0 + L.F <= nfail) ? L.F : (nfail - f0);
+      hipLaunchKernelGGL(gather_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q, r, qf, la,
+                         lb, lq, hz, dz, c);
+      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+      rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags, c.gA, c.gB,
+                           c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable,
+                           L.total - L.fb_stable, grad_limit, status, s);
+      if (rc != TTC_LQR_OK) return rc;
+      hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
+                         glB, glQ, gh, gBp, gQp);
+      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+    }
+    rc = launch_headsum(gBp, nc, H, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
+    if (rc != TTC_LQR_OK) return rc;
+    rc = launch_headsum(gQp, nc, H, (int)dd, grad_Q + n0 * dd, grad_limit, status, s);
+    if (rc != TTC_LQR_OK) return rc;
+  }
+  if (n_fallback) *n_fallback = total_fb;
+  return TTC_LQR_OK;
+}
+
+
+
+// ---- factored inputs: expanded B / Q / Q_f per token chunk ---------------------------
+struct FactLayout {
+  size_t Bx, Qx, Qfx, gB, gQ, gQf, part, inner, total;
+};
+
+static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, int T, bool with_stash,
+                              bool backward) {
+  const size_t N = (size_t)nc, P = (size_t)nc * (size_t)H, Eb = (size_t)d * du, Eq = (size_t)d * d;
+  FactLayout L{};
+  size_t off = 0;
+  L.Bx = off;
+  off += align256(N * Eb * sizeof(float));
+  L.Qx = off;
+  off += align256(N * Eq * sizeof(float));
+  L.Qfx = off;
+  off += align256(P * Eq * sizeof(float));
+  if (backward) {
+    L.gB = off;
+    off += align256(N * Eb * sizeof(float));
+    L.gQ = off;
+    off += align256(N * Eq * sizeof(float));
+    L.gQf = off;
+    off += align256(P * Eq * sizeof(float));
+    size_t part = factor_partial_floats(nc, rb, (int)Eb);
+    const size_t pq = factor_partial_floats(nc, rq, (int)Eq), pf = factor_partial_floats((int64_t)P, rq, (int)Eq);
+    part = part > pq ? part : pq;
+    part = part > pf ? part : pf;
+    L.part = off;
+    off += align256(part * sizeof(float));
+    L.inner = off;
+    // ttc_lqr_backward's workspace for this chunk in one pass; the stable path (flag
+    // TTC_LQR_FLAG_STABLE_BWD) splits the chunk further inside it (one token at least)
+    const size_t fast = fast_layout(nc, H, d, du, T, with_stash).total, stab = stable_layout(1, H, d, T).total;
+    off += fast > stab ? fast : stab;
+  }
+  L.total = off;
+  return L;
+}
+
+static bool fact_args_ok(int64_t n_tokens, int H, int d, int du, int rb, int rq, int T) {
+  return n_tokens >= 0 && H > 0 && d > 0 && du > 0 && T > 0 && rb >= 1 && rb <= 64 && rq >= 1 && rq <= 64;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Largest token chunk whose factored layout fits ws_bytes (0 when not even one token fits).
+static int64_t fact_chunk(int64_t n_tokens, int H, int d, int du, int rb, int rq, int T, bool with_stash,
+                          bool backward, size_t ws_bytes) {
+  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward).total > ws_bytes) return 0;
+  int64_t chunk = 1, hi = n_tokens;
+  while (chunk < hi) {
+    const int64_t mid = chunk + (hi - chunk + 1) / 2;
+    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward).total <= ws_bytes) chunk = mid;
+    else hi = mid - 1;
+  }
+  return chunk;
+}
+
+static int expand_chunk(const float* cB, const float* cQ, const float* cQf, const float* Bs, const float* Gs,
+                        int64_t nc, int H, int d, int du, int rb, int rq, float* Bx, float* Qx, float* Qfx,
+                        hipStream_t s) {
+  int rc = launch_expand(cB, nc, rb, Bs, d * du, Bx, s);
+  if (rc == TTC_LQR_OK) rc = launch_expand(cQ, nc, rq, Gs, d * d, Qx, s);
+  if (rc == TTC_LQR_OK) rc = launch_expand(cQf, nc * H, rq, Gs, d * d, Qfx, s);
+  return rc;
+}
+
 }  // namespace ttc
 
 using namespace ttc;
@@ -308,85 +471,125 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
       !grad_A_diag || !grad_B || !grad_Q || !grad_R_inv || !grad_Q_f || !grad_log_gamma_A || !grad_log_gamma_B ||
       !grad_log_gamma_Q || !grad_h0 || !workspace || (!stable && !u))
     return TTC_LQR_EINVAL;
+  const float* v1s = stash;
+  const float* q0s = stash ? stash + n_tokens * heads * (int64_t)d * d : nullptr;
+  return backward_core(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, u, d_u, n_tokens, heads,
+                       d, du, T, flags, v1s, q0s, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f,
+                       grad_log_gamma_A, grad_log_gamma_B, grad_log_gamma_Q, grad_h0,
+                       static_cast<char*>(workspace), workspace_bytes, grad_limit, status, n_fallback,
+                       reinterpret_cast<hipStream_t>(stream));
+}
+
+
+size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t b_rank,
+                                        int32_t q_rank, int32_t T, int32_t with_stash, int32_t backward) {
+  if (chunk_tokens <= 0 || !fact_args_ok(chunk_tokens, heads, d, du, b_rank, q_rank, T) || du != d) return 0;
+  return fact_layout(chunk_tokens, heads, d, du, b_rank, q_rank, T, with_stash != 0, backward != 0).total;
+}
+
+int ttc_lqr_forward_factored(const float* A_diag, const float* coeff_B, const float* coeff_Q, const float* R_inv,
+                             const float* coeff_Qf, const float* log_gamma_A, const float* log_gamma_B,
+                             const float* log_gamma_Q, const float* h0, const float* B_basis, const float* Q_basis,
+                             int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t b_rank, int32_t q_rank,
+                             int32_t T, int32_t flags, float* u, float* stash, void* workspace,
+                             size_t workspace_bytes, int32_t* status, void* stream) {
+  if (!fact_args_ok(n_tokens, heads, d, du, b_rank, q_rank, T)) return TTC_LQR_EINVAL;
+  if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  if (n_tokens == 0) return TTC_LQR_OK;
+  if (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !log_gamma_A || !log_gamma_B || !log_gamma_Q ||
+      !h0 || !B_basis || !Q_basis || !u || !workspace || !aligned16(B_basis) || !aligned16(Q_basis))
+    return TTC_LQR_EINVAL;
+  const int H = heads;
+  const int64_t chunk = fact_chunk(n_tokens, H, d, du, b_rank, q_rank, T, false, false, workspace_bytes);
+  if (chunk == 0) return TTC_LQR_EINVAL;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  const int64_t P = n_tokens * H, dd = (int64_t)d * d;
+  for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
+    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
+    const int64_t p0 = n0 * H;
+    const FactLayout L = fact_layout(nc, H, d, du, b_rank, q_rank, T, false, false);
+    float* Bx = reinterpret_cast<float*>(ws + L.Bx);
+    float* Qx = reinterpret_cast<float*>(ws + L.Qx);
+    float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
+    int rc = expand_chunk(coeff_B + n0 * b_rank, coeff_Q + n0 * q_rank, coeff_Qf + p0 * q_rank, B_basis, Q_basis,
+                          nc, H, d, du, b_rank, q_rank, Bx, Qx, Qfx, s);
+    if (rc != TTC_LQR_OK) return rc;
+    float* v1 = stash ? stash + p0 * dd : nullptr;
+    float* q0 = stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
+    rc = fwd_d(d, A_diag + p0 * d, Bx, Qx, R_inv + p0 * du, Qfx, log_gamma_A + p0, log_gamma_B + p0 * du,
+               log_gamma_Q + p0 * d, h0 + p0 * d, nc * H, H, T, u + p0 * du, v1, q0, stash ? kStashV1 : 0, status, s,
+               flags);
+    if (rc != TTC_LQR_OK) return rc;
+  }
+  return TTC_LQR_OK;
+}
+
+int ttc_lqr_backward_factored(const float* A_diag, const float* coeff_B, const float* coeff_Q, const float* R_inv,
+                              const float* coeff_Qf, const float* log_gamma_A, const float* log_gamma_B,
+                              const float* log_gamma_Q, const float* h0, const float* B_basis, const float* Q_basis,
+                              const float* u, const float* d_u, int64_t n_tokens, int32_t heads, int32_t d,
+                              int32_t du, int32_t b_rank, int32_t q_rank, int32_t T, int32_t flags,
+                              const float* stash, float* grad_A_diag, float* grad_coeff_B, float* grad_coeff_Q,
+                              float* grad_R_inv, float* grad_coeff_Qf, float* grad_log_gamma_A,
+                              float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0,
+                              float* grad_B_basis, float* grad_Q_basis, void* workspace, size_t workspace_bytes,
+                              float grad_limit, int32_t* status, int64_t* n_fallback, void* stream) {
+  if (n_fallback) *n_fallback = 0;
+  if (!fact_args_ok(n_tokens, heads, d, du, b_rank, q_rank, T)) return TTC_LQR_EINVAL;
+  if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
+  if (!grad_B_basis || !grad_Q_basis || !workspace) return TTC_LQR_EINVAL;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int Eb = d * du, Eq = d * d;
+  if (n_tokens == 0) {  // the basis gradients are sums over no tokens
+    int rc = launch_reduce(nullptr, 0, b_rank, nullptr, Eb, nullptr, grad_B_basis, 0, s);
+    return rc == TTC_LQR_OK ? launch_reduce(nullptr, 0, q_rank, nullptr, Eq, nullptr, grad_Q_basis, 0, s) : rc;
+  }
+  if (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !log_gamma_A || !log_gamma_B || !log_gamma_Q ||
+      !h0 || !B_basis || !Q_basis || !d_u || !grad_A_diag || !grad_coeff_B || !grad_coeff_Q || !grad_R_inv ||
+      !grad_coeff_Qf || !grad_log_gamma_A || !grad_log_gamma_B || !grad_log_gamma_Q || !grad_h0 ||
+      (!stable && !u) || !aligned16(B_basis) || !aligned16(Q_basis))
+    return TTC_LQR_EINVAL;
   const int H = heads;
-  if (stable) {
-    if (n_fallback) *n_fallback = n_tokens * heads;
-    return stable_backward(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, d_u, n_tokens, H, d,
-                           T, flags, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f, grad_log_gamma_A,
-                           grad_log_gamma_B, grad_log_gamma_Q, grad_h0, ws, workspace_bytes, grad_limit, status, s);
-  }
-  const bool with_stash = stash != nullptr;
-  // largest token chunk whose layout fits the workspace (the layout grows with the chunk)
-  if (workspace_bytes < fast_layout(1, H, d, du, T, with_stash).total) return TTC_LQR_EINVAL;
-  int64_t chunk = 1, hi = n_tokens;
-  while (chunk < hi) {
-    const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (fast_layout(mid, H, d, du, T, with_stash).total <= workspace_bytes) chunk = mid;
-    else hi = mid - 1;
-  }
-  const int64_t dd = (int64_t)d * d;
-  const float tau = TTC_LQR_CERT_TOL;
+  const bool with_stash = stash != nullptr && !stable;
+  const int64_t chunk = fact_chunk(n_tokens, H, d, du, b_rank, q_rank, T, with_stash, true, workspace_bytes);
+  if (chunk == 0) return TTC_LQR_EINVAL;
+  const int64_t P = n_tokens * H, dd = (int64_t)d * d;
   int64_t total_fb = 0;
   for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H, Pc = nc * H;
-    const FastLayout L = fast_layout(nc, H, d, du, T, with_stash);
-    const float *a = A_diag + p0 * d, *b = B + n0 * dd, *q = Q + n0 * dd, *r = R_inv + p0 * du;
-    const float *qf = Q_f + p0 * dd, *la = log_gamma_A + p0, *lb = log_gamma_B + p0 * du;
-    const float *lq = log_gamma_Q + p0 * d, *hz = h0 + p0 * d, *dz = d_u + p0 * du, *uz = u + p0 * du;
-    float *gA = grad_A_diag + p0 * d, *gR = grad_R_inv + p0 * du, *gQf = grad_Q_f + p0 * dd;
-    float *glA = grad_log_gamma_A + p0, *glB = grad_log_gamma_B + p0 * du, *glQ = grad_log_gamma_Q + p0 * d;
-    float* gh = grad_h0 + p0 * d;
-    const float *v1, *q0;
-    int rc = TTC_LQR_OK;
-    if (with_stash) {
-      v1 = stash + p0 * dd;
-      q0 = stash + n_tokens * H * dd + p0 * (int64_t)du * du;
-    } else {
-      float* v1w = reinterpret_cast<float*>(ws + L.v1);
-      float* q0w = reinterpret_cast<float*>(ws + L.q0);
-      rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, Pc, H, T, nullptr, v1w, q0w, kStashV1, nullptr, s, flags);
-      if (rc != TTC_LQR_OK) return rc;
-      v1 = v1w;
-      q0 = q0w;
-    }
-    float* gBp = reinterpret_cast<float*>(ws + L.gBp);
-    float* gQp = reinterpret_cast<float*>(ws + L.gQp);
-    int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
-    int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
-    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
-    switch (d) {
-      case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
-      case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
-      case 64: rc = launch_ham_d64(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
-      default: return TTC_LQR_EUNSUPPORTED;
-    }
+    const FactLayout L = fact_layout(nc, H, d, du, b_rank, q_rank, T, with_stash, true);
+    float* Bx = reinterpret_cast<float*>(ws + L.Bx);
+    float* Qx = reinterpret_cast<float*>(ws + L.Qx);
+    float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
+    float* gB = reinterpret_cast<float*>(ws + L.gB);
+    float* gQ = reinterpret_cast<float*>(ws + L.gQ);
+    float* gQf = reinterpret_cast<float*>(ws + L.gQf);
+    float* part = reinterpret_cast<float*>(ws + L.part);
+    const float *cB = coeff_B + n0 * b_rank, *cQ = coeff_Q + n0 * q_rank, *cQf = coeff_Qf + p0 * q_rank;
+    int rc = expand_chunk(cB, cQ, cQf, B_basis, Q_basis, nc, H, d, du, b_rank, q_rank, Bx, Qx, Qfx, s);
     if (rc != TTC_LQR_OK) return rc;
-    // how many problems the certificate rejected (one stream synchronisation per chunk)
-    int32_t nfail = 0;
-    if (hipMemcpyAsync(&nfail, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;
-    if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
-    if (nfail < 0 || nfail > Pc) return TTC_LQR_ELAUNCH;
-    total_fb += nfail;
-    const Compact c = compact_at(ws + L.fb, L.F, d, du);
-    for (int64_t f0 = 0; f0 < nfail; f0 += L.F) {
-      const int64_t fc = (f0 + L.F <= nfail) ? L.F : (nfail - f0);
-      hipLaunchKernelGGL(gather_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q, r, qf, la,
-                         lb, lq, hz, dz, c);
-      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
-      rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags, c.gA, c.gB,
-                           c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable,
-                           L.total - L.fb_stable, grad_limit, status, s);
-      if (rc != TTC_LQR_OK) return rc;
-      hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
-                         glB, glQ, gh, gBp, gQp);
-      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
-    }
-    rc = launch_headsum(gBp, nc, H, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
+    const float* v1 = with_stash ? stash + p0 * dd : nullptr;
+    const float* q0 = with_stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
+    int64_t nfb = 0;
+    rc = backward_core(A_diag + p0 * d, Bx, Qx, R_inv + p0 * du, Qfx, log_gamma_A + p0, log_gamma_B + p0 * du,
+                       log_gamma_Q + p0 * d, h0 + p0 * d, u ? u + p0 * du : nullptr, d_u + p0 * du, nc, H, d, du, T,
+                       flags, v1, q0, grad_A_diag + p0 * d, gB, gQ, grad_R_inv + p0 * du, gQf,
+                       grad_log_gamma_A + p0, grad_log_gamma_B + p0 * du, grad_log_gamma_Q + p0 * d,
+                       grad_h0 + p0 * d, ws + L.inner, L.total - L.inner, grad_limit, status, &nfb, s);
     if (rc != TTC_LQR_OK) return rc;
-    rc = launch_headsum(gQp, nc, H, (int)dd, grad_Q + n0 * dd, grad_limit, status, s);
+    total_fb += nfb;
+    // chain rule of the expansion: coefficient gradients, then the basis sums
+    rc = launch_project(gB, nc, Eb, B_basis, b_rank, grad_coeff_B + n0 * b_rank, s);
+    if (rc == TTC_LQR_OK) rc = launch_project(gQ, nc, Eq, Q_basis, q_rank, grad_coeff_Q + n0 * q_rank, s);
+    if (rc == TTC_LQR_OK) rc = launch_project(gQf, Pc, Eq, Q_basis, q_rank, grad_coeff_Qf + p0 * q_rank, s);
+    const int first = n0 == 0 ? 0 : 1;
+    if (rc == TTC_LQR_OK) rc = launch_reduce(cB, nc, b_rank, gB, Eb, part, grad_B_basis, first, s);
+    if (rc == TTC_LQR_OK) rc = launch_reduce(cQ, nc, q_rank, gQ, Eq, part, grad_Q_basis, first, s);
+    if (rc == TTC_LQR_OK) rc = launch_reduce(cQf, Pc, q_rank, gQf, Eq, part, grad_Q_basis, 1, s);
     if (rc != TTC_LQR_OK) return rc;
   }
   if (n_fallback) *n_fallback = total_fb;

@@ -61,4 +61,12 @@ int launch_ham_d64(const float* A, const float* B, const float* Q, const float* 
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
                   hipStream_t s);
+// Low-rank front-end (ttc_lqr_factored.hip): expansion of coefficient x basis sums and
+// their chain rule.  Rows of E = d * du floats; ranks R <= 64; E in {256, 1024, 4096}.
+int launch_expand(const float* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s);
+int launch_project(const float* X, int64_t M, int E, const float* basis, int R, float* out, hipStream_t s);
+int launch_reduce(const float* coeff, int64_t M, int R, const float* X, int E, float* partial, float* out,
+                  int accumulate, hipStream_t s);
+int64_t factor_slabs(int64_t M, int R, int E);
+size_t factor_partial_floats(int64_t M, int R, int E);
 }  // namespace ttc

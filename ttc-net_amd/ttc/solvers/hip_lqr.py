@@ -55,7 +55,8 @@ import torch
 
 from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS
 
-__all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "padded_dim", "SUPPORTED_DIMS", "last_backward_stats"]
+__all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
+           "SUPPORTED_DIMS", "last_backward_stats"]
 
 SUPPORTED_DIMS = (16, 32, 64)
 FP64_HORIZON = 512
@@ -205,7 +206,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
             "h0": torch.empty(bs, nh, Dp, device=dev),
         }
         status = torch.zeros(1, device=dev, dtype=torch.int32)
-        budget = _env_bytes("TTC_LQR_WORKSPACE_BYTES", min(16 << 30, max(1 << 30, _stash_budget(dev))))
+        budget = _workspace_budget(dev)
         with_st = 1 if st is not None else 0
         # one pass over all tokens when it fits the budget; the library picks the largest
         # token chunk that fits whatever it is given (at least one token's worth)
@@ -248,3 +249,127 @@ def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_
     """
     return HipLQRSolveFunc.apply(A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T,
                                  grad_limit, stash, precision, stable_backward)
+
+
+def _workspace_budget(dev) -> int:
+    return _env_bytes("TTC_LQR_WORKSPACE_BYTES", min(16 << 30, max(1 << 30, _stash_budget(dev))))
+
+
+class HipLQRFactoredFunc(torch.autograd.Function):
+    """The solve on the layer's low-rank factors (``ttc_layer.py:117-123``): ``B``, ``Q`` and
+    ``Q_f`` are never materialised in full; the library expands them per token chunk.
+
+    Inputs: ``A_diag [N,H,d]``, ``coeff_B [N,rb]``, ``coeff_Q [N,rq]``, ``R_inv [N,H,du]``,
+    ``coeff_Qf [N,H,rq]``, ``log_gamma_A [N,H]``, ``log_gamma_B [N,H,du]``,
+    ``log_gamma_Q [N,H,d]``, ``h0 [N,H,d]``, ``B_basis [rb,d,du]``, ``Q_basis [rq,d,d]``, ``T``;
+    ``B = einsum("nr,rij->nij", coeff_B, B_basis)``, ``Q`` likewise, ``Q_f[n,h] =
+    einsum("r,rij->ij", coeff_Qf[n,h], Q_basis)``.  Same ``u``, arithmetic, certificate,
+    stash and error behaviour as :class:`HipLQRSolveFunc` on the expanded tensors.
+    """
+
+    @staticmethod
+    def forward(ctx, A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0,
+                B_basis, Q_basis, T: int, grad_limit: float = 1e6, stash: str | None = None,
+                precision: str = "auto", stable_backward: bool = False):
+        ins = [A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0,
+               B_basis, Q_basis]
+        assert all(x.is_cuda for x in ins), "hip LQR solver inputs must be on a GPU"
+        bs, nh, d = A_diag.shape
+        rb, _, du = B_basis.shape
+        rq = Q_basis.shape[0]
+        T = int(T)
+        assert T > 0
+        assert coeff_B.shape == (bs, rb) and coeff_Q.shape == (bs, rq) and coeff_Qf.shape == (bs, nh, rq)
+        assert B_basis.shape == (rb, d, du) and Q_basis.shape == (rq, d, d)
+        assert R_inv_diag.shape == (bs, nh, du) and log_gamma_A.shape == (bs, nh)
+        assert log_gamma_B.shape == (bs, nh, du) and log_gamma_Q.shape == (bs, nh, d) and h0.shape == (bs, nh, d)
+        assert 1 <= rb <= 64 and 1 <= rq <= 64, f"ranks 1..64 are supported, got b_rank={rb}, q_rank={rq}"
+        dev = A_diag.device
+        out_dtype = A_diag.dtype
+        Dp = padded_dim(d, du)
+        flags = riccati_flags(precision, T, Dp)
+        F = torch.nn.functional
+        f32 = [x.detach().to(torch.float32).contiguous() for x in ins]
+        pd, pu = Dp - d, Dp - du
+        if pd or pu:  # zero-padded states / unit-cost dummy controls, as HipLQRSolveFunc
+            f32[0] = F.pad(f32[0], (0, pd))
+            f32[3] = F.pad(f32[3], (0, pu), value=1.0)
+            f32[6] = F.pad(f32[6], (0, pu))
+            f32[7] = F.pad(f32[7], (0, pd))
+            f32[8] = F.pad(f32[8], (0, pd))
+            f32[9] = F.pad(f32[9], (0, pu, 0, pd))
+            f32[10] = F.pad(f32[10], (0, pd, 0, pd))
+            f32 = [t.contiguous() for t in f32]
+        u = torch.empty(bs, nh, Dp, device=dev, dtype=torch.float32)
+        status = torch.zeros(1, device=dev, dtype=torch.int32)
+        policy = stash or os.environ.get("TTC_LQR_STASH", "auto")
+        assert policy in ("auto", "always", "never"), f"unknown stash policy {policy}"
+        need_grad = any(ctx.needs_input_grad[:11])
+        stash_bytes = lib.ttc_lqr_stash_bytes(bs, nh, Dp, Dp, T)
+        keep = (need_grad and bs > 0 and not stable_backward
+                and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev))))
+        st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32) if keep else None
+        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, 0, 0)
+        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, 0, 0)
+        ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
+        with torch.cuda.device(dev):
+            rc = lib.ttc_lqr_forward_factored(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, rb, rq, T, flags,
+                                              u.data_ptr(), None if st is None else st.data_ptr(), ws.data_ptr(),
+                                              ws.numel(), status.data_ptr(), _stream_handle(dev))
+        check(rc, "ttc_lqr_forward_factored")
+        del ws
+        if int(status.item()) & _ERROR_BITS:
+            raise RuntimeError(_FWD_MSG)
+        if need_grad:
+            ctx.save_for_backward(*f32, u, *([st] if st is not None else []))
+        ctx.meta = (bs, nh, d, du, Dp, rb, rq, T, float(grad_limit), st is not None, [x.dtype for x in ins],
+                    flags | (FLAG_STABLE_BWD if stable_backward else 0))
+        return u[..., :du].to(out_dtype)
+
+    @staticmethod
+    def backward(ctx, d_u):
+        bs, nh, d, du, Dp, rb, rq, T, grad_limit, has_stash, dtypes, flags = ctx.meta
+        saved = ctx.saved_tensors
+        f32 = list(saved[:11])
+        u = saved[11]
+        st = saved[12] if has_stash else None
+        dev = f32[0].device
+        if du == Dp:
+            dU = d_u.to(torch.float32).contiguous()
+        else:
+            dU = torch.zeros(bs, nh, Dp, device=dev, dtype=torch.float32)
+            dU[..., :du] = d_u.to(torch.float32)
+        E = lambda *shape: torch.empty(*shape, device=dev, dtype=torch.float32)  # noqa: E731
+        g = [E(bs, nh, Dp), E(bs, rb), E(bs, rq), E(bs, nh, Dp), E(bs, nh, rq), E(bs, nh), E(bs, nh, Dp),
+             E(bs, nh, Dp), E(bs, nh, Dp), E(rb, Dp, Dp), E(rq, Dp, Dp)]
+        status = torch.zeros(1, device=dev, dtype=torch.int32)
+        with_st = 1 if st is not None else 0
+        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, with_st, 1)
+        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, with_st, 1)
+        ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
+        limit = grad_limit if math.isfinite(grad_limit) else float("inf")
+        n_fb = ctypes.c_int64(0)
+        with torch.cuda.device(dev):
+            rc = lib.ttc_lqr_backward_factored(
+                *[t.data_ptr() for t in f32], u.data_ptr(), dU.data_ptr(), bs, nh, Dp, Dp, rb, rq, T, flags,
+                None if st is None else st.data_ptr(), *[t.data_ptr() for t in g], ws.data_ptr(), ws.numel(),
+                limit, status.data_ptr(), ctypes.byref(n_fb), _stream_handle(dev))
+        check(rc, "ttc_lqr_backward_factored")
+        last_backward_stats.update(problems=bs * nh, fallback=int(n_fb.value))
+        if int(status.item()) & _ERROR_BITS:
+            raise RuntimeError(_BWD_MSG)
+        out = (g[0][..., :d], g[1], g[2], g[3][..., :du], g[4], g[5], g[6][..., :du], g[7][..., :d],
+               g[8][..., :d], g[9][:, :d, :du], g[10][:, :d, :d])
+        out = tuple(o.to(dt) if need else None for o, dt, need in zip(out, dtypes, ctx.needs_input_grad[:11]))
+        return out + (None, None, None, None, None)
+
+
+def hip_lqr_solve_factored(A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q,
+                           h0, B_basis, Q_basis, T: int, grad_limit: float = 1e6, stash: str | None = None,
+                           precision: str = "auto", stable_backward: bool = False) -> torch.Tensor:
+    """``hip_lqr_solve`` on the layer's low-rank factors (see :class:`HipLQRFactoredFunc`):
+    equal to ``hip_lqr_solve(A_diag, einsum(coeff_B, B_basis), einsum(coeff_Q, Q_basis), R_inv,
+    einsum(coeff_Qf, Q_basis), ...)`` with gradients for the coefficients and both bases."""
+    return HipLQRFactoredFunc.apply(A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B,
+                                    log_gamma_Q, h0, B_basis, Q_basis, T, grad_limit, stash, precision,
+                                    stable_backward)
