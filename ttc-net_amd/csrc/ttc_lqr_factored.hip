@@ -18,7 +18,6 @@
 #include "ttc_lqr_internal.h"
 
 namespace ttc {
-namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
@@ -194,9 +193,7 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_
 
 constexpr int kSlabGroup = 64;  // first-level group of sum_slabs_kernel
 
-bool launched() { return hipGetLastError() == hipSuccess; }
-
-}  // namespace
+static bool launched() { return hipGetLastError() == hipSuccess; }
 
 // Tile shape of reduce_kernel for rank R: (RT, ET) = (1, 16), (2, 16) or (4, 8).
 static void reduce_shape(int R, int& RT, int& ET) {
