@@ -108,6 +108,43 @@ def test_certificate_rejects_stress_problems_and_fallback():
         assert _relerr(fast[k], slow[k]) <= TOL, k
 
 
+def _regroup_heads(ins, H_new):
+    """Problems of consecutive tokens regrouped into tokens of H_new heads (the token-shared
+    B and Q of each new token are those of its first old token)."""
+    A, B, Q, R, Qf, lA, lB, lQ, h0 = ins
+    N, H = A.shape[:2]
+    k = H_new // H
+    N2 = N // k
+    per = lambda t: t[:N2 * k].reshape(N2, H_new, *t.shape[2:])  # noqa: E731
+    return [per(A), B[:N2 * k:k], Q[:N2 * k:k], per(R), per(Qf), per(lA), per(lB), per(lQ), per(h0)]
+
+
+@pytest.mark.parametrize("N,H,T", [(3, 8, 64), (2, 16, 40), (2, 24, 17), (4, 8, 1), (3, 16, 2)])
+def test_d16_head_groups_matrix_core_backward(N, H, T):
+    """The d = 16 backward over head groups of 8 on the matrix cores: one group per token
+    (H = 8, head sums written directly) and several (H = 16, 24: group sums, then head
+    sums), T = 1 and 2 included."""
+    ins = bench_solver_inputs(N, H, 16, seed=N + H + T)
+    out = check_case(f"groups N={N} H={H}", ins, T)
+    assert out["_fallback"] % 8 == 0
+
+
+def test_d16_head_groups_with_rejected_groups():
+    """Config-5 stress problems regrouped to 16 heads per token: groups that fail the
+    certificate go through the stable path as whole groups, and the head sums of grad_B /
+    grad_Q combine matrix-core groups and stable-path groups of the same token."""
+    x = make_x(5, n_tokens=24, seed=11)
+    ins = _regroup_heads(layer_solver_inputs(5, x), 16)
+    pb = LQRProblem(*ins, 64)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(4)).double().numpy()
+    fast = run_hip(ins, 64, dU, grad_limit=math.inf)
+    print(f"fallback {fast['_fallback']}/{pb.P}", flush=True)
+    assert 0 < fast["_fallback"] < pb.P and fast["_fallback"] % 8 == 0
+    ref = solve_grads(pb, dU)
+    for k in ["u"] + NAMES:
+        assert _relerr(fast[k], ref[k]) <= TOL, k
+
+
 def test_config3_layer_slice():
     c = CONFIGS[3]
     x = make_x(3, n_tokens=2, seed=2)

@@ -82,6 +82,51 @@ __global__ void scatter_kernel(const int* __restrict__ list, int64_t base, int d
   copy_span(gQp + p * d * d, c.gQ + i * d * d, d * d);
 }
 
+// Head groups (8 consecutive heads of one token, chunk-local index list[base + i]) gathered
+// as compact 8-head tokens for the stable path, and their gradients scattered back: per
+// problem, and the group's sums of grad_B / grad_Q (to the token's outputs when H == 8).
+__global__ void gather_group_kernel(const int* __restrict__ list, int64_t base, int H, int d, int du,
+                                    const float* __restrict__ A, const float* __restrict__ B,
+                                    const float* __restrict__ Q, const float* __restrict__ R,
+                                    const float* __restrict__ Qf, const float* __restrict__ lA,
+                                    const float* __restrict__ lB, const float* __restrict__ lQ,
+                                    const float* __restrict__ h0, const float* __restrict__ dU, Compact c) {
+  const int64_t i = blockIdx.x;
+  const int64_t p0 = (int64_t)list[base + i] * 8;
+  const int64_t n = p0 / H;
+  const int64_t q0 = i * 8;  // compact problems of this group
+  copy_span(c.B + i * d * du, B + n * d * du, d * du);
+  copy_span(c.Q + i * d * d, Q + n * d * d, d * d);
+  copy_span(c.A + q0 * d, A + p0 * d, 8 * d);
+  copy_span(c.R + q0 * du, R + p0 * du, 8 * du);
+  copy_span(c.Qf + q0 * d * d, Qf + p0 * d * d, 8 * d * d);
+  copy_span(c.lA + q0, lA + p0, 8);
+  copy_span(c.lB + q0 * du, lB + p0 * du, 8 * du);
+  copy_span(c.lQ + q0 * d, lQ + p0 * d, 8 * d);
+  copy_span(c.h0 + q0 * d, h0 + p0 * d, 8 * d);
+  copy_span(c.dU + q0 * du, dU + p0 * du, 8 * du);
+}
+
+__global__ void scatter_group_kernel(const int* __restrict__ list, int64_t base, int H, int d, int du, Compact c,
+                                     float* __restrict__ gA, float* __restrict__ gR, float* __restrict__ gQf,
+                                     float* __restrict__ glA, float* __restrict__ glB, float* __restrict__ glQ,
+                                     float* __restrict__ gh0, float* __restrict__ gBg, float* __restrict__ gQg) {
+  const int64_t i = blockIdx.x;
+  const int64_t G = list[base + i];
+  const int64_t p0 = G * 8;
+  const int64_t q0 = i * 8;
+  const int64_t o = (H == 8) ? p0 / H : G;
+  copy_span(gA + p0 * d, c.gA + q0 * d, 8 * d);
+  copy_span(gR + p0 * du, c.gR + q0 * du, 8 * du);
+  copy_span(gQf + p0 * d * d, c.gQf + q0 * d * d, 8 * d * d);
+  copy_span(glA + p0, c.glA + q0, 8);
+  copy_span(glB + p0 * du, c.glB + q0 * du, 8 * du);
+  copy_span(glQ + p0 * d, c.glQ + q0 * d, 8 * d);
+  copy_span(gh0 + p0 * d, c.gh0 + q0 * d, 8 * d);
+  copy_span(gBg + o * d * du, c.gB + i * d * du, d * du);
+  copy_span(gQg + o * d * d, c.gQ + i * d * d, d * d);
+}
+
 static int launch_headsum(const float* part, int64_t N, int H, int DD, float* out, float limit, int32_t* status,
                           hipStream_t s) {
   const int64_t total = N * DD;
@@ -179,7 +224,7 @@ static size_t compact_floats(int d, int du) {  // inputs + gradients of one prob
 static int64_t fallback_capacity(int64_t Pc, int d, int du, int T) {
   const size_t per = compact_floats(d, du) * sizeof(float) + 19 * 256 + stable_layout(1, 1, d, T).total;
   int64_t cap = (int64_t)((size_t)256 << 20) / (int64_t)per;
-  if (cap < 1) cap = 1;
+  if (cap < 8) cap = 8;  // at least one head group of 8 (the d = 16 matrix-core backward's unit)
   return Pc < cap ? Pc : cap;
 }
 
@@ -293,6 +338,43 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
     hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
+    if (d == 16 && H % 8 == 0) {
+      // head groups of 8 on the matrix cores: grad_B / grad_Q summed inside the kernel
+      // (straight into the outputs when a group is a token, H == 8)
+      const bool direct = H == 8;
+      float* gBg = direct ? grad_B + n0 * dd : gBp;
+      float* gQg = direct ? grad_Q + n0 * dd : gQp;
+      rc = launch_ham16_mfma(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB,
+                             glQ, gh, gBg, gQg, grad_limit, list, cnt, status, s);
+      if (rc != TTC_LQR_OK) return rc;
+      int32_t nfail = 0;
+      if (hipMemcpyAsync(&nfail, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;
+      if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
+      if (nfail < 0 || nfail > Pc / 8) return TTC_LQR_ELAUNCH;
+      total_fb += 8 * (int64_t)nfail;
+      const Compact c = compact_at(ws + L.fb, L.F, d, du);
+      const int64_t Fg = L.F / 8;  // groups per fallback batch
+      for (int64_t f0 = 0; f0 < nfail; f0 += Fg) {
+        const int64_t fc = (f0 + Fg <= nfail) ? Fg : (nfail - f0);
+        hipLaunchKernelGGL(gather_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q,
+                           r, qf, la, lb, lq, hz, dz, c);
+        if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+        rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 8, d, T, flags, c.gA, c.gB,
+                             c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable, L.total - L.fb_stable,
+                             grad_limit, status, s);
+        if (rc != TTC_LQR_OK) return rc;
+        hipLaunchKernelGGL(scatter_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, c, gA, gR,
+                           gQf, glA, glB, glQ, gh, gBg, gQg);
+        if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+      }
+      if (!direct) {
+        rc = launch_headsum(gBg, nc, H / 8, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
+        if (rc != TTC_LQR_OK) return rc;
+        rc = launch_headsum(gQg, nc, H / 8, (int)dd, grad_Q + n0 * dd, grad_limit, status, s);
+        if (rc != TTC_LQR_OK) return rc;
+      }
+      continue;
+    }
     switch (d) {
       case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
       case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;

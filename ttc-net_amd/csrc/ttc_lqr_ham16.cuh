@@ -1,0 +1,377 @@
+#pragma once
+// ttc_lqr_ham16.cuh -- certified Hamiltonian backward for d = du = 16 on the matrix cores.
+//
+// Same recursion, certificate and outputs as lqr_ham_bwd_kernel (the reference's forward
+// Hamiltonian differentiation, ttc/solvers/symplectic_iter.py:764-885, rolled from
+// lambda_1 = V_1 h_1): per step t
+//   lambda_{t+1} = A_t^{-1} (lambda_t - Qc_t h_t),  u_t = -R^{-1} B_t' lambda_{t+1},
+//   h_{t+1} = A_t h_t + B_t u_t                       (primal and adjoint at once),
+// with every gradient term of step t formed when step t is rolled.
+//
+// Layout: one wave rolls a *head group* -- 8 consecutive heads of one token (H % 8 == 0),
+// primal and adjoint, as the 16 columns of one 16 x 16 tile in the MFMA C layout (lane
+// (g, c) holds rows 4g..4g+3 of column c; column c = problem c & 7, adjoint when c >= 8).
+// B and Q are shared by the group, so each per-step matrix-vector product of the 16
+// trajectories is one 16x16x16 product on v_mfma_f32_16x16x4f32: Q (q o S), B' Lambda,
+// B (beta o U).  The head-summed gradients are products over the trajectory index,
+//   grad_B += Lambda Pi (beta o U)',   grad_Q += (q o S) Pi (q o S)'   (Pi swaps primal and
+// adjoint columns), so they accumulate on the matrix cores too and need no head sums
+// afterwards; their operands are the step's tiles read back row-major from LDS.  Per-row
+// quantities (discounts, the gradients of A_diag, R_inv, the log-discounts and h0) stay in
+// the C layout; primal / adjoint cross terms pair lanes c and c ^ 8 (DPP row_ror:8).
+// The per-problem pieces -- the adjoint feed-forward w_0 = -Quu_0^{-1} d_u, lambda_1 = V_1 h_1
+// and the terminal certificate lambda_T = Q_f h_T -- run in the row layout (16 lanes per
+// problem, two passes of 4 problems).
+//
+// A group whose problems all pass the certificate writes its per-problem gradients and
+// the group sums of grad_B / grad_Q (the token's sums when H == 8); otherwise it writes
+// nothing and appends its index to fail_list, and the caller recomputes the whole group
+// with the stable path.
+#include "ttc_lqr_mfma16.cuh"
+
+namespace ttc {
+
+struct Ham16 {
+  static constexpr int LD = 20;             // row stride of a 16 x 16 tile in LDS (floats)
+  static constexpr int MAT = 16 * LD;       // 320 floats
+  static constexpr int NTILE = 6;           // Z, X, Y double-buffered by step parity
+  static constexpr int OFF_ROW = NTILE * MAT;
+  static constexpr int ROW_PER = 24;        // per row-layout problem: the pivot row (20) + skew
+  static constexpr int PER_WAVE = OFF_ROW + 4 * ROW_PER;
+  static constexpr int WPB = 4;             // waves per block (independent: no block barrier)
+  static constexpr int THREADS = 64 * WPB;
+  static constexpr size_t LDS_BYTES = sizeof(float) * WPB * PER_WAVE;
+};
+
+__device__ __forceinline__ float swap8(float v) { return ror16f<8>(v); }  // lane c <-> c ^ 8
+
+__device__ __forceinline__ v4f swap8(v4f v) { return v4f{swap8(v[0]), swap8(v[1]), swap8(v[2]), swap8(v[3])}; }
+
+// C-layout tile (lane (g, c): rows 4g..4g+3 of column c) -> row-major LDS tile.
+__device__ __forceinline__ void st_tile_rowmajor(float* t, int g, int c, v4f v) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) t[(4 * g + r) * Ham16::LD + c] = v[r];
+}
+
+// C-layout tile -> column-major LDS tile (row c of the result = column c of the tile).
+__device__ __forceinline__ void st_tile_colmajor(float* t, int g, int c, v4f v) {
+  st4(t + c * Ham16::LD + 4 * g, v);
+}
+
+// acc += X Pi Y' over the trajectory index, X and Y row-major in LDS:
+// acc[i][j] += sum_k X[i][k] Y[j][k ^ 8].
+__device__ __forceinline__ v4f mfma_cross(const float* X, const float* Y, int g, int c, v4f acc) {
+  const v4f a = ld4(X + c * Ham16::LD + 4 * g);
+  const v4f b = ld4(Y + c * Ham16::LD + 4 * (g ^ 2));
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mfma16x16x4(a[s], b[s], acc);
+  return acc;
+}
+
+template <bool DIRECT>
+__global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(3, 4))) void lqr_ham16_mfma_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    const float* __restrict__ u0g, const float* __restrict__ dU, const float* __restrict__ v1s,
+    const float* __restrict__ q0s, int64_t P, int H, int T, float tau, float* __restrict__ gA,
+    float* __restrict__ gRinv, float* __restrict__ gQf, float* __restrict__ glgA, float* __restrict__ glgB,
+    float* __restrict__ glgQ, float* __restrict__ gh0, float* __restrict__ gBg, float* __restrict__ gQg,
+    float grad_limit, int* __restrict__ fail_list, int* __restrict__ fail_count, int* __restrict__ status) {
+  extern __shared__ __align__(16) float sm[];
+  constexpr float kLog2e = 1.4426950408889634f;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int g = lane >> 4;        // MFMA row block; problem slot of the row-layout passes
+  const int c = lane & 15;        // MFMA column = trajectory; row of the row-layout passes
+  const int j = c & 7;            // my column's problem within the group
+  const bool adj = c >= 8;
+  const int64_t G = (int64_t)blockIdx.x * Ham16::WPB + wv;
+  if (G * 8 >= P) return;         // whole waves only: no barrier follows
+  const int64_t p0 = G * 8;
+  const int64_t n = p0 / H;       // the group's token
+  const int64_t p = p0 + j;
+  float* wbase = sm + wv * Ham16::PER_WAVE;
+  float* tile = wbase;                                   // 6 tiles of 16 x LD
+  float* prow = wbase + Ham16::OFF_ROW + g * Ham16::ROW_PER;
+
+  // ---- per-lane constants: rows 4g..4g+3 of problem j --------------------------------
+  const v4f a4 = ld4(A_diag + p * 16 + 4 * g);
+  v4f lb2, lq2, rinv, nrr2;  // nrr2 = -1 / (2 R_inv^2): half of d(1/R_inv)/dR_inv per lane
+  {
+    const v4f b = ld4(lgB + p * 16 + 4 * g), q = ld4(lgQ + p * 16 + 4 * g), r = ld4(Rinv + p * 16 + 4 * g);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lb2[k] = b[k] * kLog2e;
+      lq2[k] = q[k] * kLog2e;
+      rinv[k] = r[k];
+      const float rr = 1.0f / r[k];
+      nrr2[k] = -0.5f * rr * rr;
+    }
+  }
+  const float la2 = lgA[p] * kLog2e;
+  // matrix fragments of the token (A operands): B rows, B' rows, sym(Q) rows
+  float Bm[4], Bt[4], Qa[4];
+  {
+    const float* bq = Bg + n * 256;
+    const float* qq = Qg + n * 256;
+    const v4f brow = ld4(bq + c * 16 + 4 * g);
+    const v4f qrow = ld4(qq + c * 16 + 4 * g);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      Bm[s] = brow[s];
+      Bt[s] = bq[(4 * g + s) * 16 + c];
+      Qa[s] = 0.5f * (qrow[s] + qq[(4 * g + s) * 16 + c]);
+    }
+  }
+
+  // ---- t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (row layout, two passes) ----
+  float* TS = tile;          // trajectory-major exchange tile [traj][state]
+  float* TL = tile + Ham16::MAT;
+#pragma unroll
+  for (int pa = 0; pa < 2; ++pa) {
+    const int64_t pp = p0 + 4 * pa + g;
+    float aug[20];
+    ld_global_row<16>(q0s + (pp * 16 + c) * 16, *reinterpret_cast<float(*)[16]>(aug));
+    aug[16] = dU[pp * 16 + c];
+    aug[17] = aug[18] = aug[19] = 0.f;
+    float piv;
+    int pos;
+    gauss_jordan<16, 20>(aug, c, prow, piv, pos);
+    TS[(8 + 4 * pa + g) * Ham16::LD + pos] = -aug[16] / piv;  // adjoint column of problem 4pa+g
+  }
+  wave_sync();
+  v4f U;  // u_0 (primal columns) / w_0 (adjoint columns), rows 4g..4g+3
+  if (adj) U = ld4(TS + c * Ham16::LD + 4 * g);
+  else U = ld4(u0g + p * 16 + 4 * g);
+  v4f S;  // h_0 / h~_0 = 0
+  if (adj) S = v4f{0.f, 0.f, 0.f, 0.f};
+  else S = ld4(h0 + p * 16 + 4 * g);
+
+  const float eA0 = __builtin_amdgcn_exp2f(la2);
+  v4f al0, be0, BU;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    al0[k] = fmaf(a4[k], eA0, 1.0f);
+    be0[k] = __builtin_amdgcn_exp2f(lb2[k]);
+    BU[k] = be0[k] * U[k];
+  }
+  // h_1 = alpha_0 h_0 + B (beta_0 u_0)
+  v4f S1 = al0 * S;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) S1 = mfma16x16x4(Bm[s], BU[s], S1);
+  // lambda_1 = V_1 h_1 (row layout)
+  wave_sync();
+  st_tile_colmajor(TS, g, c, S1);
+  wave_sync();
+#pragma unroll
+  for (int pa = 0; pa < 2; ++pa) {
+    const int jj = 4 * pa + g;
+    const int64_t pp = p0 + jj;
+    float vrow[16], hv[16], hbv[16];
+    ld_global_row<16>(v1s + (pp * 16 + c) * 16, vrow);
+    ld_row<16>(TS + jj * Ham16::LD, hv);
+    ld_row<16>(TS + (8 + jj) * Ham16::LD, hbv);
+    float lam = 0.f, lamb = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      lam = fmaf(vrow[k], hv[k], lam);
+      lamb = fmaf(vrow[k], hbv[k], lamb);
+    }
+    TL[jj * Ham16::LD + c] = lam;
+    TL[(8 + jj) * Ham16::LD + c] = lamb;
+  }
+  wave_sync();
+  v4f L = ld4(TL + c * Ham16::LD + 4 * g);
+  // B' lambda_1
+  v4f BtL = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) BtL = mfma16x16x4(Bt[s], L[s], BtL);
+
+  // per-lane partial accumulators (primal and adjoint lanes are summed at the end)
+  v4f accA, accLA, accLB, accR, accLQ, accH0;
+  {
+    const v4f Lx = swap8(L), BtLx = swap8(BtL), Ux = swap8(U);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float gAt = S[k] * Lx[k];                  // h_0 lambda~_1 (h~_0 = 0)
+      accA[k] = gAt * eA0;
+      accLA[k] = gAt * eA0;                            // times a at the end
+      accLB[k] = be0[k] * U[k] * BtLx[k];              // beta_0 (u_0 B'lambda~_1 | w_0 B'lambda_1)
+      accR[k] = U[k] * Ux[k] * nrr2[k];                // -u_0 w_0 / R_inv^2, half per lane
+      accLQ[k] = 0.f;
+      accH0[k] = adj ? al0[k] * L[k] : 0.f;            // alpha_0 lambda~_1
+    }
+  }
+  // grad_B += Lambda Pi (beta o U)'
+  v4f gB = v4f{0.f, 0.f, 0.f, 0.f}, gQ = v4f{0.f, 0.f, 0.f, 0.f};
+  {
+    float* X = tile + 2 * Ham16::MAT;
+    float* Y = tile + 3 * Ham16::MAT;
+    st_tile_rowmajor(X, g, c, L);
+    st_tile_rowmajor(Y, g, c, BU);
+    wave_sync();
+    gB = mfma_cross(X, Y, g, c, gB);
+  }
+  S = S1;
+
+  for (int t = 1; t < T; ++t) {
+    const float tf = (float)t, tp1 = tf + 1.0f;
+    float* Z = tile + (t & 1) * 3 * Ham16::MAT;
+    float* X = Z + Ham16::MAT;
+    float* Y = X + Ham16::MAT;
+    // state cost on h_t: Qc_t = D_t Q D_t, D_t = diag(exp(lgQ t))
+    v4f q, X1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      q[k] = __builtin_amdgcn_exp2f(lq2[k] * tf);
+      X1[k] = q[k] * S[k];
+    }
+    v4f QX = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) QX = mfma16x16x4(Qa[s], X1[s], QX);
+    const v4f Qh = q * QX;
+    st_tile_rowmajor(Z, g, c, X1);
+    const float eA = __builtin_amdgcn_exp2f(la2 * tp1);
+    v4f al, be;
+    {
+      const v4f Qhx = swap8(Qh);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        accLQ[k] = fmaf(tf * S[k], Qhx[k], accLQ[k]);  // t (h Qc h~ | h~ Qc h)
+        al[k] = fmaf(a4[k], eA, 1.0f);
+        L[k] = (L[k] - Qh[k]) * __builtin_amdgcn_rcpf(al[k]);
+        be[k] = __builtin_amdgcn_exp2f(lb2[k] * tp1);
+      }
+    }
+    BtL = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) BtL = mfma16x16x4(Bt[s], L[s], BtL);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      U[k] = -rinv[k] * be[k] * BtL[k];
+      BU[k] = be[k] * U[k];
+    }
+    st_tile_rowmajor(X, g, c, L);
+    st_tile_rowmajor(Y, g, c, BU);
+    {
+      const v4f Lx = swap8(L), BtLx = swap8(BtL), Ux = swap8(U);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float gAt = S[k] * Lx[k];                // h_t lambda~_{t+1} | h~_t lambda_{t+1}
+        accA[k] = fmaf(gAt, eA, accA[k]);
+        accLA[k] = fmaf(gAt, tp1 * eA, accLA[k]);
+        accLB[k] = fmaf(tp1 * be[k], U[k] * BtLx[k], accLB[k]);
+        accR[k] = fmaf(U[k] * Ux[k], nrr2[k], accR[k]);
+      }
+    }
+    // h_{t+1} = alpha_t h_t + B (beta o U)
+    v4f Sn = al * S;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) Sn = mfma16x16x4(Bm[s], BU[s], Sn);
+    S = Sn;
+    wave_sync();  // Z, X, Y written
+    gQ = mfma_cross(Z, Z, g, c, gQ);
+    gB = mfma_cross(X, Y, g, c, gB);
+  }
+
+  // ---- terminal: grad Q_f = sym(h_T h~_T'), certificate lambda_T = Q_f h_T (row layout) ----
+  wave_sync();
+  st_tile_colmajor(TS, g, c, S);
+  st_tile_colmajor(TL, g, c, L);
+  wave_sync();
+  unsigned bad = 0u;
+  float fin = 0.f;
+#pragma unroll
+  for (int pa = 0; pa < 2; ++pa) {
+    const int jj = 4 * pa + g;
+    const int64_t pp = p0 + jj;
+    float hv[16], hbv[16];
+    ld_row<16>(TS + jj * Ham16::LD, hv);
+    ld_row<16>(TS + (8 + jj) * Ham16::LD, hbv);
+    const float lam = TL[jj * Ham16::LD + c], lamb = TL[(8 + jj) * Ham16::LD + c];
+    const float* qfp = Qf + pp * 256;
+    float fh = 0.f, fhb = 0.f;
+    const float hc = TS[jj * Ham16::LD + c], hbc = TS[(8 + jj) * Ham16::LD + c];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float qf = 0.5f * (qfp[c * 16 + k] + qfp[k * 16 + c]);
+      fh = fmaf(qf, hv[k], fh);
+      fhb = fmaf(qf, hbv[k], fhb);
+      fin += fabsf(0.5f * fmaf(hc, hbv[k], hbc * hv[k]));  // grad Q_f row c (stored below)
+    }
+    const float E1 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(lam - fh))));
+    const float E2 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(lamb - fhb))));
+    const float M1 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(fh) + fabsf(lam))));
+    const float M2 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(fhb) + fabsf(lamb))));
+    if (!(E1 <= tau * M1 && E2 <= tau * M2)) bad = 1u;
+  }
+
+  // finish the per-problem sums: primal + adjoint lanes, then glgA over the 16 rows
+#pragma unroll
+  for (int k = 0; k < 4; ++k) gQ[k] *= 0.5f;
+  const v4f fA = accA + swap8(accA), fLB = accLB + swap8(accLB), fR = accR + swap8(accR);
+  const v4f fLQ = accLQ + swap8(accLQ), fH0 = accH0 + swap8(accH0);
+  float la_sum = accLA[0] * a4[0] + accLA[1] * a4[1] + accLA[2] * a4[2] + accLA[3] * a4[3];
+  la_sum += swap8(la_sum);
+  la_sum += __shfl_xor(la_sum, 16, 64);
+  la_sum += __shfl_xor(la_sum, 32, 64);
+  fin += fabsf(la_sum);
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    fin += fabsf(fA[k]) + fabsf(fLB[k]) + fabsf(fR[k]) + fabsf(fLQ[k]) + fabsf(fH0[k]) + fabsf(gB[k]) + fabsf(gQ[k]);
+  if (!isfinite(fin)) bad = 1u;
+  // every accumulator finite <=> the sum is (a sum of finite values overflows only near 1e38)
+  if (__ballot(bad != 0u) != 0ull) {
+    if (lane == 0) fail_list[atomicAdd(fail_count, 1)] = (int)G;
+    return;
+  }
+
+  int flags = 0;
+  if (!adj) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      flag_value<16>(fA[k], grad_limit, flags);
+      flag_value<16>(fLB[k], grad_limit, flags);
+      flag_value<16>(fR[k], grad_limit, flags);
+      flag_value<16>(fLQ[k], grad_limit, flags);
+      flag_value<16>(fH0[k], grad_limit, flags);
+    }
+    st4(gA + p * 16 + 4 * g, fA);
+    st4(glgB + p * 16 + 4 * g, fLB);
+    st4(gRinv + p * 16 + 4 * g, fR);
+    st4(glgQ + p * 16 + 4 * g, fLQ);
+    st4(gh0 + p * 16 + 4 * g, fH0);
+    if (g == 0) {
+      flag_value<16>(la_sum, grad_limit, flags);
+      glgA[p] = la_sum;
+    }
+  }
+#pragma unroll
+  for (int pa = 0; pa < 2; ++pa) {
+    const int jj = 4 * pa + g;
+    const int64_t pp = p0 + jj;
+    float hv[16], hbv[16], gq[16];
+    ld_row<16>(TS + jj * Ham16::LD, hv);
+    ld_row<16>(TS + (8 + jj) * Ham16::LD, hbv);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      gq[k] = 0.5f * fmaf(hv[c], hbv[k], hbv[c] * hv[k]);
+      flag_value<16>(gq[k], grad_limit, flags);
+    }
+    st_global_row<16>(gQf + (pp * 16 + c) * 16, gq);
+  }
+  // group sums of grad_B / grad_Q: [i = 4g + r][j = c]
+  float* ob = gBg + (DIRECT ? n : G) * 256;
+  float* oq = gQg + (DIRECT ? n : G) * 256;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    flag_value<16>(gB[r], grad_limit, flags);
+    flag_value<16>(gQ[r], grad_limit, flags);
+    ob[(4 * g + r) * 16 + c] = gB[r];
+    oq[(4 * g + r) * 16 + c] = gQ[r];
+  }
+  if (flags && status != nullptr) atomicOr(status, flags);
+}
+
+}  // namespace ttc
