@@ -157,10 +157,11 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
 /* Workspace bytes of the factored entry points for `chunk_tokens` tokens per pass:
  * backward = 0 for ttc_lqr_forward_factored (the expanded B, Q, Q_f of a chunk),
  * backward != 0 for ttc_lqr_backward_factored (plus the chunk's B / Q / Q_f gradients,
- * the reduction partials and ttc_lqr_backward's own workspace). */
+ * the reduction partials and ttc_lqr_backward's own workspace); bf16 != 0 for the _bf16
+ * entry points (plus fp32 copies of the chunk's inputs, gradients and the bases). */
 size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du,
                                         int32_t b_rank, int32_t q_rank, int32_t T, int32_t with_stash,
-                                        int32_t backward);
+                                        int32_t backward, int32_t bf16);
 
 /* Forward on factored inputs; u, stash, status and flags as ttc_lqr_forward.
  * workspace_bytes >= ttc_lqr_factored_workspace_bytes(1, ..., backward = 0). */
@@ -192,6 +193,33 @@ int ttc_lqr_backward_factored(const float* A_diag, const float* coeff_B, const f
                               float* grad_B_basis, float* grad_Q_basis, void* workspace,
                               size_t workspace_bytes, float grad_limit, int32_t* status,
                               int64_t* n_fallback, void* stream);
+
+/* bf16 storage (config 4 stores its activations in bf16): the same two entry points with
+ * every input, d_u and every gradient stored as bf16 (raw bit patterns, uint16_t); u and
+ * the stash stay fp32 (the backward's rollout starts from u).  Each token chunk is widened
+ * to fp32 inside `workspace` (exact), the kernels keep their fp32 state and arithmetic, and
+ * the gradients are rounded to bf16 (nearest even) when stored: the results are the fp32
+ * entry points' on the widened inputs, rounded.  No 16-byte alignment is required. */
+int ttc_lqr_forward_factored_bf16(const uint16_t* A_diag, const uint16_t* coeff_B, const uint16_t* coeff_Q,
+                                  const uint16_t* R_inv, const uint16_t* coeff_Qf, const uint16_t* log_gamma_A,
+                                  const uint16_t* log_gamma_B, const uint16_t* log_gamma_Q, const uint16_t* h0,
+                                  const uint16_t* B_basis, const uint16_t* Q_basis, int64_t n_tokens,
+                                  int32_t heads, int32_t d, int32_t du, int32_t b_rank, int32_t q_rank, int32_t T,
+                                  int32_t flags, float* u, float* stash, void* workspace, size_t workspace_bytes,
+                                  int32_t* status, void* stream);
+
+int ttc_lqr_backward_factored_bf16(const uint16_t* A_diag, const uint16_t* coeff_B, const uint16_t* coeff_Q,
+                                   const uint16_t* R_inv, const uint16_t* coeff_Qf, const uint16_t* log_gamma_A,
+                                   const uint16_t* log_gamma_B, const uint16_t* log_gamma_Q, const uint16_t* h0,
+                                   const uint16_t* B_basis, const uint16_t* Q_basis, const float* u,
+                                   const uint16_t* d_u, int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
+                                   int32_t b_rank, int32_t q_rank, int32_t T, int32_t flags, const float* stash,
+                                   uint16_t* grad_A_diag, uint16_t* grad_coeff_B, uint16_t* grad_coeff_Q,
+                                   uint16_t* grad_R_inv, uint16_t* grad_coeff_Qf, uint16_t* grad_log_gamma_A,
+                                   uint16_t* grad_log_gamma_B, uint16_t* grad_log_gamma_Q, uint16_t* grad_h0,
+                                   uint16_t* grad_B_basis, uint16_t* grad_Q_basis, void* workspace,
+                                   size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
+                                   void* stream);
 
 #ifdef __cplusplus
 }

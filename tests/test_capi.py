@@ -17,7 +17,7 @@ HEADER = os.path.join(ROOT, "include", "ttc_lqr.h")
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ttc_lqr_[a-z_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(ttc_lqr_[a-z0-9_]+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
@@ -30,7 +30,8 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
         "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes",
-        "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored"])
+        "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
+        "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -119,14 +120,20 @@ def test_backward_argument_validation(L):
 def test_factored_workspace_bytes(L):
     # forward: the expanded B, Q (per token) and Q_f (per problem) of one chunk
     N, H, d, T = 1000, 8, 16, 64
-    f = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0)
+    f = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0, 0)
     assert 4 * N * (2 * d * d + H * d * d) <= f < 4 * N * (2 * d * d + H * d * d) + 1024
     # backward: also the chunk's gradients of B, Q, Q_f and ttc_lqr_backward's own workspace
-    b = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1)
+    b = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1, 0)
     assert b >= 2 * f + L.ttc_lqr_workspace_bytes(N, H, d, d, T, 1)
-    assert L.ttc_lqr_factored_workspace_bytes(2 * N, H, d, d, 16, 16, T, 1, 1) > b
+    assert L.ttc_lqr_factored_workspace_bytes(2 * N, H, d, d, 16, 16, T, 1, 1, 0) > b
+    # bf16 storage: plus fp32 copies of the chunk's inputs (and d_u, gradients) and of the bases
+    per_in = 3 * d + 2 * d + 1 + 16              # A, R, lgB, lgQ, h0, lgA, coeff_Qf per problem
+    fb = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0, 1)
+    assert fb - f >= 4 * (N * H * per_in + 2 * 16 * d * d)
+    bb = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1, 1)
+    assert bb - b >= 4 * (N * H * (2 * per_in + d) + 4 * 16 * d * d)
     for bad in [(N, H, d, d, 0, 16), (N, H, d, d, 16, 65), (0, H, d, d, 16, 16), (N, H, 16, 32, 16, 16)]:
-        assert L.ttc_lqr_factored_workspace_bytes(*bad, T, 0, 0) == 0
+        assert L.ttc_lqr_factored_workspace_bytes(*bad, T, 0, 0, 0) == 0
 
 
 def test_factored_argument_validation(L):

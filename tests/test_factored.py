@@ -135,7 +135,7 @@ def test_factored_token_chunks_match_single_pass(monkeypatch):
     T = 16
     dU = torch.randn(37, 8, 16, generator=torch.Generator().manual_seed(9)).double().numpy()
     one = run_factored(ins, T, dU, stash="never")
-    ws = lib.ttc_lqr_factored_workspace_bytes(5, 8, 16, 16, 16, 16, T, 0, 1)
+    ws = lib.ttc_lqr_factored_workspace_bytes(5, 8, 16, 16, 16, 16, T, 0, 1, 0)
     monkeypatch.setenv("TTC_LQR_WORKSPACE_BYTES", str(ws))
     many = run_factored(ins, T, dU, stash="never")
     assert np.array_equal(one["u"], many["u"])
@@ -198,3 +198,72 @@ def test_layer_factored_equals_materialised(q_reparam):
     assert _relerr(ya.detach().cpu(), yb.detach().cpu()) <= 1e-5
     for (n, pa), (_, pb) in zip(a.named_parameters(), b.named_parameters()):
         assert _relerr(pa.grad.cpu(), pb.grad.cpu()) <= 1e-4, n
+
+
+def _run_grads(ins, T, dU, dtype, **kw):
+    """u and the eleven gradients of sum(dU * u), inputs of `dtype` (outputs as returned)."""
+    from ttc.solvers.hip_lqr import hip_lqr_solve_factored
+    dev = torch.device("cuda:0")
+    xs = [t.detach().to(dev).to(dtype).requires_grad_(True) for t in ins]
+    u = hip_lqr_solve_factored(*xs, T, **kw)
+    torch.autograd.backward(u, torch.as_tensor(dU, device=dev).to(u.dtype))
+    return [u.detach()] + [t.grad.detach() for t in xs]
+
+
+@pytest.mark.parametrize("cfg,n_tok,d", [(2, 24, None), (4, 2, None), (2, 9, 24)])
+def test_factored_bf16_storage_is_rounded_fp32(cfg, n_tok, d):
+    """bf16 storage (ttc_lqr_*_factored_bf16): inputs widened per chunk, fp32 arithmetic,
+    gradients rounded on store -- so every output equals the fp32 entry points' output on the
+    widened inputs, rounded to bf16, bit for bit (d = 24 also checks bf16 padding)."""
+    ins = [t.to(torch.bfloat16) for t in factored_inputs(cfg, n_tok, d=d)]
+    N, H, dd = ins[0].shape
+    T = CONFIGS[cfg]["T"]
+    dU = torch.randn(N, H, ins[3].shape[-1], generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    got = _run_grads(ins, T, dU, torch.bfloat16)
+    ref = _run_grads([t.float() for t in ins], T, dU.float(), torch.float32)
+    for k, (a, b) in enumerate(zip(got, ref)):
+        assert a.dtype == torch.bfloat16
+        assert torch.equal(a, b.to(torch.bfloat16)), (["u"] + NAMES11)[k]
+
+
+def test_factored_bf16_token_chunks(monkeypatch):
+    """bf16 storage over many token chunks: u bitwise equal to one pass; gradients equal up
+    to the fp32 summation order of the basis sums (one bf16 ulp)."""
+    from ttc.solvers._lib import lib
+    ins = [t.to(torch.bfloat16) for t in factored_inputs(2, 30, seed=6)]
+    T = 16
+    dU = torch.randn(30, 8, 16, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    one = _run_grads(ins, T, dU, torch.bfloat16, stash="never")
+    monkeypatch.setenv("TTC_LQR_WORKSPACE_BYTES", str(lib.ttc_lqr_factored_workspace_bytes(4, 8, 16, 16, 16, 16,
+                                                                                        T, 0, 1, 1)))
+    many = _run_grads(ins, T, dU, torch.bfloat16, stash="never")
+    assert torch.equal(one[0], many[0])
+    for k in range(1, 12):
+        a, b = one[k].float(), many[k].float()
+        assert float((a - b).abs().max()) <= 2 ** -7 * float(b.abs().max()), NAMES11[k - 1]
+
+
+def test_layer_bf16_runs_on_bf16_storage():
+    """A bf16 TTCLayer (config 4's storage) passes bf16 tensors to the solver; output and
+    parameter gradients track the fp32 layer to bf16 accuracy."""
+    from ttc import TTCLayer
+    torch.manual_seed(1)
+    a = TTCLayer(64, 64, 32, 4, 32, 32, solver_impl="hip").cuda()
+    b = TTCLayer(64, 64, 32, 4, 32, 32, solver_impl="hip").cuda()
+    b.load_state_dict(a.state_dict())
+    b = b.to(torch.bfloat16)
+    with torch.no_grad():
+        for m in (a, b):
+            m.Bs.mul_(10.0)
+            m.Qs.mul_(10.0)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    x = (0.02 * torch.randn(2, 16, 4, 64, device="cuda", generator=gen)).to(torch.bfloat16)
+    ya, yb = a(x.float(), T=32), b(x, T=32)
+    assert yb.dtype == torch.bfloat16
+    dy = torch.randn(ya.shape, device="cuda", generator=gen)
+    (ya * dy).sum().backward()
+    (yb.float() * dy).sum().backward()
+    assert _relerr(yb.detach().float().cpu(), ya.detach().cpu()) <= 3e-2
+    for (n, pa), (_, pb) in zip(a.named_parameters(), b.named_parameters()):
+        assert pb.grad.dtype == torch.bfloat16
+        assert _relerr(pb.grad.float().cpu(), pa.grad.cpu()) <= 5e-2, n

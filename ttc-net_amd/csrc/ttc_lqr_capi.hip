@@ -5,6 +5,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "ttc_lqr.h"
 #include "ttc_lqr_internal.h"
 
@@ -414,15 +416,33 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
 
 
 // ---- factored inputs: expanded B / Q / Q_f per token chunk ---------------------------
+// Workspace of the factored entry points, for token chunks of nc tokens.  Chunk-independent
+// regions first: the bases and the basis gradients in fp32 (bf16 storage only).  Then the
+// chunk's expanded B, Q, Q_f; for the backward their gradients, the reduction partials;
+// for bf16 storage the chunk's inputs (and d_u) and per-problem gradients in fp32; last,
+// ttc_lqr_backward's own workspace for the chunk.
 struct FactLayout {
-  size_t Bx, Qx, Qfx, gB, gQ, gQf, part, inner, total;
+  size_t bas, gbas, Bx, Qx, Qfx, gB, gQ, gQf, part, cin[10], cg[9], inner, total;
 };
 
+// Elements of the per-problem / per-token arrays of a chunk, in argument order:
+// A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, lgA, lgB, lgQ, h0 (and d_u).
+static void io_counts(int64_t nc, int H, int d, int du, int rb, int rq, size_t (&n)[10]) {
+  const size_t N = (size_t)nc, P = (size_t)nc * (size_t)H;
+  const size_t v[10] = {P * d, N * rb, N * rq, P * du, P * rq, P, P * du, P * d, P * d, P * du};
+  for (int k = 0; k < 10; ++k) n[k] = v[k];
+}
+
 static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                              bool backward) {
+                              bool backward, bool bf16) {
   const size_t N = (size_t)nc, P = (size_t)nc * (size_t)H, Eb = (size_t)d * du, Eq = (size_t)d * d;
+  const size_t nbas = (size_t)rb * Eb + (size_t)rq * Eq;
   FactLayout L{};
   size_t off = 0;
+  L.bas = off;
+  off += bf16 ? align256(nbas * sizeof(float)) : 0;
+  L.gbas = off;
+  off += (bf16 && backward) ? align256(nbas * sizeof(float)) : 0;
   L.Bx = off;
   off += align256(N * Eb * sizeof(float));
   L.Qx = off;
@@ -442,6 +462,22 @@ static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, 
     part = part > pf ? part : pf;
     L.part = off;
     off += align256(part * sizeof(float));
+  }
+  if (bf16) {
+    size_t n[10];
+    io_counts(nc, H, d, du, rb, rq, n);
+    for (int k = 0; k < (backward ? 10 : 9); ++k) {
+      L.cin[k] = off;
+      off += align256(n[k] * sizeof(float));
+    }
+    if (backward) {
+      for (int k = 0; k < 9; ++k) {
+        L.cg[k] = off;
+        off += align256(n[k] * sizeof(float));
+      }
+    }
+  }
+  if (backward) {
     L.inner = off;
     // ttc_lqr_backward's workspace for this chunk in one pass; the stable path (flag
     // TTC_LQR_FLAG_STABLE_BWD) splits the chunk further inside it (one token at least)
@@ -460,12 +496,12 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Largest token chunk whose factored layout fits ws_bytes (0 when not even one token fits).
 static int64_t fact_chunk(int64_t n_tokens, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                          bool backward, size_t ws_bytes) {
-  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward).total > ws_bytes) return 0;
+                          bool backward, bool bf16, size_t ws_bytes) {
+  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward, bf16).total > ws_bytes) return 0;
   int64_t chunk = 1, hi = n_tokens;
   while (chunk < hi) {
     const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward).total <= ws_bytes) chunk = mid;
+    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward, bf16).total <= ws_bytes) chunk = mid;
     else hi = mid - 1;
   }
   return chunk;
@@ -478,6 +514,234 @@ static int expand_chunk(const float* cB, const float* cQ, const float* cQf, cons
   if (rc == TTC_LQR_OK) rc = launch_expand(cQ, nc, rq, Gs, d * d, Qx, s);
   if (rc == TTC_LQR_OK) rc = launch_expand(cQf, nc * H, rq, Gs, d * d, Qfx, s);
   return rc;
+}
+
+// Storage of the factored inputs and gradients: fp32 as is, bf16 (bit patterns) converted
+// to / from fp32 arrays in the workspace.
+template <typename TS>
+struct Store {
+  static constexpr bool BF16 = std::is_same<TS, uint16_t>::value;
+  // fp32 view of in[off .. off + n): the array itself, or its conversion into dst
+  static const float* in(const TS* a, int64_t off, size_t n, float* dst, hipStream_t s, int& rc) {
+    if constexpr (BF16) {
+      if (rc == TTC_LQR_OK) rc = launch_bf16_to_f32(a + off, (int64_t)n, dst, s);
+      return dst;
+    } else {
+      (void)n; (void)dst; (void)s;
+      return a + off;
+    }
+  }
+  // where the kernels write out[off ..): the array itself, or a workspace array converted afterwards
+  static float* out(TS* a, int64_t off, float* tmp) {
+    if constexpr (BF16) {
+      (void)a; (void)off;
+      return tmp;
+    } else {
+      (void)tmp;
+      return a + off;
+    }
+  }
+  static void flush(TS* a, int64_t off, size_t n, const float* tmp, hipStream_t s, int& rc) {
+    if constexpr (BF16) {
+      if (rc == TTC_LQR_OK) rc = launch_f32_to_bf16(tmp, (int64_t)n, a + off, s);
+    } else {
+      (void)a; (void)off; (void)n; (void)tmp; (void)s;
+    }
+  }
+};
+
+template <typename TS>
+static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff_Q, const TS* R_inv,
+                            const TS* coeff_Qf, const TS* log_gamma_A, const TS* log_gamma_B, const TS* log_gamma_Q,
+                            const TS* h0, const TS* B_basis, const TS* Q_basis, int64_t n_tokens, int H, int d,
+                            int du, int rb, int rq, int T, int flags, float* u, float* stash, char* ws,
+                            size_t ws_bytes, int32_t* status, hipStream_t s) {
+  using St = Store<TS>;
+  const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, false, false, St::BF16, ws_bytes);
+  if (chunk == 0) return TTC_LQR_EINVAL;
+  const int64_t P = n_tokens * H, dd = (int64_t)d * d;
+  const size_t nb = (size_t)rb * d * du, nq = (size_t)rq * d * d;
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, false, false, St::BF16);
+  int rc = TTC_LQR_OK;
+  float* bas = reinterpret_cast<float*>(ws + L0.bas);
+  const float* Bs = St::in(B_basis, 0, nb, bas, s, rc);
+  const float* Gs = St::in(Q_basis, 0, nq, bas + nb, s, rc);
+  for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
+    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
+    const int64_t p0 = n0 * H;
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, false, false, St::BF16);
+    size_t n[10];
+    io_counts(nc, H, d, du, rb, rq, n);
+    auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
+    const float* a = St::in(A_diag, p0 * d, n[0], cin(0), s, rc);
+    const float* cb = St::in(coeff_B, n0 * rb, n[1], cin(1), s, rc);
+    const float* cq = St::in(coeff_Q, n0 * rq, n[2], cin(2), s, rc);
+    const float* r = St::in(R_inv, p0 * du, n[3], cin(3), s, rc);
+    const float* cqf = St::in(coeff_Qf, p0 * rq, n[4], cin(4), s, rc);
+    const float* la = St::in(log_gamma_A, p0, n[5], cin(5), s, rc);
+    const float* lb = St::in(log_gamma_B, p0 * du, n[6], cin(6), s, rc);
+    const float* lq = St::in(log_gamma_Q, p0 * d, n[7], cin(7), s, rc);
+    const float* hz = St::in(h0, p0 * d, n[8], cin(8), s, rc);
+    if (rc != TTC_LQR_OK) return rc;
+    float* Bx = reinterpret_cast<float*>(ws + L.Bx);
+    float* Qx = reinterpret_cast<float*>(ws + L.Qx);
+    float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
+    rc = expand_chunk(cb, cq, cqf, Bs, Gs, nc, H, d, du, rb, rq, Bx, Qx, Qfx, s);
+    if (rc != TTC_LQR_OK) return rc;
+    float* v1 = stash ? stash + p0 * dd : nullptr;
+    float* q0 = stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
+    rc = fwd_d(d, a, Bx, Qx, r, Qfx, la, lb, lq, hz, nc * H, H, T, u + p0 * du, v1, q0, stash ? kStashV1 : 0, status,
+               s, flags);
+  }
+  return rc;
+}
+
+template <typename TS>
+static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff_Q, const TS* R_inv,
+                             const TS* coeff_Qf, const TS* log_gamma_A, const TS* log_gamma_B,
+                             const TS* log_gamma_Q, const TS* h0, const TS* B_basis, const TS* Q_basis,
+                             const float* u, const TS* d_u, int64_t n_tokens, int H, int d, int du, int rb, int rq,
+                             int T, int flags, const float* stash, TS* grad_A_diag, TS* grad_coeff_B,
+                             TS* grad_coeff_Q, TS* grad_R_inv, TS* grad_coeff_Qf, TS* grad_log_gamma_A,
+                             TS* grad_log_gamma_B, TS* grad_log_gamma_Q, TS* grad_h0, TS* grad_B_basis,
+                             TS* grad_Q_basis, char* ws, size_t ws_bytes, float grad_limit, int32_t* status,
+                             int64_t* n_fallback, hipStream_t s) {
+  using St = Store<TS>;
+  const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
+  const bool with_stash = stash != nullptr && !stable;
+  const int Eb = d * du, Eq = d * d;
+  const size_t nb = (size_t)rb * Eb, nq = (size_t)rq * Eq;
+  const int64_t chunk = fact_chunk(n_tokens > 0 ? n_tokens : 1, H, d, du, rb, rq, T, with_stash, true, St::BF16,
+                                   ws_bytes);
+  if (chunk == 0) return TTC_LQR_EINVAL;
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, with_stash, true, St::BF16);
+  int rc = TTC_LQR_OK;
+  float* bas = reinterpret_cast<float*>(ws + L0.bas);
+  float* gbas = reinterpret_cast<float*>(ws + L0.gbas);
+  float* gBs = St::out(grad_B_basis, 0, gbas);
+  float* gGs = St::out(grad_Q_basis, 0, gbas + nb);
+  if (n_tokens == 0) {  // the basis gradients are sums over no tokens
+    rc = launch_reduce(nullptr, 0, rb, nullptr, Eb, nullptr, gBs, 0, s);
+    if (rc == TTC_LQR_OK) rc = launch_reduce(nullptr, 0, rq, nullptr, Eq, nullptr, gGs, 0, s);
+    St::flush(grad_B_basis, 0, nb, gBs, s, rc);
+    St::flush(grad_Q_basis, 0, nq, gGs, s, rc);
+    return rc;
+  }
+  const float* Bs = St::in(B_basis, 0, nb, bas, s, rc);
+  const float* Gs = St::in(Q_basis, 0, nq, bas + nb, s, rc);
+  const int64_t P = n_tokens * H, dd = (int64_t)d * d;
+  int64_t total_fb = 0;
+  for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
+    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
+    const int64_t p0 = n0 * H, Pc = nc * H;
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, with_stash, true, St::BF16);
+    size_t n[10];
+    io_counts(nc, H, d, du, rb, rq, n);
+    auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
+    auto cg = [&](int k) { return reinterpret_cast<float*>(ws + L.cg[k]); };
+    const float* a = St::in(A_diag, p0 * d, n[0], cin(0), s, rc);
+    const float* cB = St::in(coeff_B, n0 * rb, n[1], cin(1), s, rc);
+    const float* cQ = St::in(coeff_Q, n0 * rq, n[2], cin(2), s, rc);
+    const float* r = St::in(R_inv, p0 * du, n[3], cin(3), s, rc);
+    const float* cQf = St::in(coeff_Qf, p0 * rq, n[4], cin(4), s, rc);
+    const float* la = St::in(log_gamma_A, p0, n[5], cin(5), s, rc);
+    const float* lb = St::in(log_gamma_B, p0 * du, n[6], cin(6), s, rc);
+    const float* lq = St::in(log_gamma_Q, p0 * d, n[7], cin(7), s, rc);
+    const float* hz = St::in(h0, p0 * d, n[8], cin(8), s, rc);
+    const float* dz = St::in(d_u, p0 * du, n[9], cin(9), s, rc);
+    float* gA = St::out(grad_A_diag, p0 * d, cg(0));
+    float* gcB = St::out(grad_coeff_B, n0 * rb, cg(1));
+    float* gcQ = St::out(grad_coeff_Q, n0 * rq, cg(2));
+    float* gR = St::out(grad_R_inv, p0 * du, cg(3));
+    float* gcQf = St::out(grad_coeff_Qf, p0 * rq, cg(4));
+    float* glA = St::out(grad_log_gamma_A, p0, cg(5));
+    float* glB = St::out(grad_log_gamma_B, p0 * du, cg(6));
+    float* glQ = St::out(grad_log_gamma_Q, p0 * d, cg(7));
+    float* gh = St::out(grad_h0, p0 * d, cg(8));
+    if (rc != TTC_LQR_OK) return rc;
+    float* Bx = reinterpret_cast<float*>(ws + L.Bx);
+    float* Qx = reinterpret_cast<float*>(ws + L.Qx);
+    float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
+    float* gB = reinterpret_cast<float*>(ws + L.gB);
+    float* gQ = reinterpret_cast<float*>(ws + L.gQ);
+    float* gQf = reinterpret_cast<float*>(ws + L.gQf);
+    float* part = reinterpret_cast<float*>(ws + L.part);
+    rc = expand_chunk(cB, cQ, cQf, Bs, Gs, nc, H, d, du, rb, rq, Bx, Qx, Qfx, s);
+    if (rc != TTC_LQR_OK) return rc;
+    const float* v1 = with_stash ? stash + p0 * dd : nullptr;
+    const float* q0 = with_stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
+    int64_t nfb = 0;
+    rc = backward_core(a, Bx, Qx, r, Qfx, la, lb, lq, hz, u ? u + p0 * du : nullptr, dz, nc, H, d, du, T, flags, v1,
+                       q0, gA, gB, gQ, gR, gQf, glA, glB, glQ, gh, ws + L.inner, L.total - L.inner, grad_limit, status,
+                       &nfb, s);
+    if (rc != TTC_LQR_OK) return rc;
+    total_fb += nfb;
+    // chain rule of the expansion: coefficient gradients, then the basis sums
+    rc = launch_project(gB, nc, Eb, Bs, rb, gcB, s);
+    if (rc == TTC_LQR_OK) rc = launch_project(gQ, nc, Eq, Gs, rq, gcQ, s);
+    if (rc == TTC_LQR_OK) rc = launch_project(gQf, Pc, Eq, Gs, rq, gcQf, s);
+    const int first = n0 == 0 ? 0 : 1;
+    if (rc == TTC_LQR_OK) rc = launch_reduce(cB, nc, rb, gB, Eb, part, gBs, first, s);
+    if (rc == TTC_LQR_OK) rc = launch_reduce(cQ, nc, rq, gQ, Eq, part, gGs, first, s);
+    if (rc == TTC_LQR_OK) rc = launch_reduce(cQf, Pc, rq, gQf, Eq, part, gGs, 1, s);
+    St::flush(grad_A_diag, p0 * d, n[0], gA, s, rc);
+    St::flush(grad_coeff_B, n0 * rb, n[1], gcB, s, rc);
+    St::flush(grad_coeff_Q, n0 * rq, n[2], gcQ, s, rc);
+    St::flush(grad_R_inv, p0 * du, n[3], gR, s, rc);
+    St::flush(grad_coeff_Qf, p0 * rq, n[4], gcQf, s, rc);
+    St::flush(grad_log_gamma_A, p0, n[5], glA, s, rc);
+    St::flush(grad_log_gamma_B, p0 * du, n[6], glB, s, rc);
+    St::flush(grad_log_gamma_Q, p0 * d, n[7], glQ, s, rc);
+    St::flush(grad_h0, p0 * d, n[8], gh, s, rc);
+  }
+  St::flush(grad_B_basis, 0, nb, gBs, s, rc);
+  St::flush(grad_Q_basis, 0, nq, gGs, s, rc);
+  if (n_fallback && rc == TTC_LQR_OK) *n_fallback = total_fb;
+  return rc;
+}
+
+template <typename TS>
+static int forward_factored_entry(const TS* A_diag, const TS* coeff_B, const TS* coeff_Q, const TS* R_inv,
+                                  const TS* coeff_Qf, const TS* lgA, const TS* lgB, const TS* lgQ, const TS* h0,
+                                  const TS* B_basis, const TS* Q_basis, int64_t n_tokens, int32_t heads, int32_t d,
+                                  int32_t du, int32_t rb, int32_t rq, int32_t T, int32_t flags, float* u,
+                                  float* stash, void* workspace, size_t workspace_bytes, int32_t* status,
+                                  void* stream) {
+  if (!fact_args_ok(n_tokens, heads, d, du, rb, rq, T)) return TTC_LQR_EINVAL;
+  if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  if (n_tokens == 0) return TTC_LQR_OK;
+  if (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !lgA || !lgB || !lgQ || !h0 || !B_basis ||
+      !Q_basis || !u || !workspace)
+    return TTC_LQR_EINVAL;
+  if (!Store<TS>::BF16 && (!aligned16(B_basis) || !aligned16(Q_basis))) return TTC_LQR_EINVAL;
+  return forward_factored<TS>(A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, lgA, lgB, lgQ, h0, B_basis, Q_basis,
+                              n_tokens, heads, d, du, rb, rq, T, flags, u, stash, static_cast<char*>(workspace),
+                              workspace_bytes, status, reinterpret_cast<hipStream_t>(stream));
+}
+
+template <typename TS>
+static int backward_factored_entry(const TS* A_diag, const TS* coeff_B, const TS* coeff_Q, const TS* R_inv,
+                                   const TS* coeff_Qf, const TS* lgA, const TS* lgB, const TS* lgQ, const TS* h0,
+                                   const TS* B_basis, const TS* Q_basis, const float* u, const TS* d_u,
+                                   int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t rb, int32_t rq,
+                                   int32_t T, int32_t flags, const float* stash, TS* gA, TS* gcB, TS* gcQ, TS* gR,
+                                   TS* gcQf, TS* glA, TS* glB, TS* glQ, TS* gh0, TS* gBs, TS* gQs, void* workspace,
+                                   size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
+                                   void* stream) {
+  if (n_fallback) *n_fallback = 0;
+  if (!fact_args_ok(n_tokens, heads, d, du, rb, rq, T)) return TTC_LQR_EINVAL;
+  if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
+  if (!gBs || !gQs || !workspace) return TTC_LQR_EINVAL;
+  if (n_tokens > 0 &&
+      (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !lgA || !lgB || !lgQ || !h0 || !B_basis ||
+       !Q_basis || !d_u || !gA || !gcB || !gcQ || !gR || !gcQf || !glA || !glB || !glQ || !gh0 || (!stable && !u)))
+    return TTC_LQR_EINVAL;
+  if (n_tokens > 0 && !Store<TS>::BF16 && (!aligned16(B_basis) || !aligned16(Q_basis))) return TTC_LQR_EINVAL;
+  return backward_factored<TS>(A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, lgA, lgB, lgQ, h0, B_basis, Q_basis, u, d_u,
+                               n_tokens, heads, d, du, rb, rq, T, flags, stash, gA, gcB, gcQ, gR, gcQf, glA, glB, glQ,
+                               gh0, gBs, gQs, static_cast<char*>(workspace), workspace_bytes, grad_limit, status,
+                               n_fallback, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // namespace ttc
@@ -564,9 +828,10 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
 
 
 size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t b_rank,
-                                        int32_t q_rank, int32_t T, int32_t with_stash, int32_t backward) {
+                                        int32_t q_rank, int32_t T, int32_t with_stash, int32_t backward,
+                                        int32_t bf16) {
   if (chunk_tokens <= 0 || !fact_args_ok(chunk_tokens, heads, d, du, b_rank, q_rank, T) || du != d) return 0;
-  return fact_layout(chunk_tokens, heads, d, du, b_rank, q_rank, T, with_stash != 0, backward != 0).total;
+  return fact_layout(chunk_tokens, heads, d, du, b_rank, q_rank, T, with_stash != 0, backward != 0, bf16 != 0).total;
 }
 
 int ttc_lqr_forward_factored(const float* A_diag, const float* coeff_B, const float* coeff_Q, const float* R_inv,
@@ -575,36 +840,21 @@ int ttc_lqr_forward_factored(const float* A_diag, const float* coeff_B, const fl
                              int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t b_rank, int32_t q_rank,
                              int32_t T, int32_t flags, float* u, float* stash, void* workspace,
                              size_t workspace_bytes, int32_t* status, void* stream) {
-  if (!fact_args_ok(n_tokens, heads, d, du, b_rank, q_rank, T)) return TTC_LQR_EINVAL;
-  if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
-  if (n_tokens == 0) return TTC_LQR_OK;
-  if (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !log_gamma_A || !log_gamma_B || !log_gamma_Q ||
-      !h0 || !B_basis || !Q_basis || !u || !workspace || !aligned16(B_basis) || !aligned16(Q_basis))
-    return TTC_LQR_EINVAL;
-  const int H = heads;
-  const int64_t chunk = fact_chunk(n_tokens, H, d, du, b_rank, q_rank, T, false, false, workspace_bytes);
-  if (chunk == 0) return TTC_LQR_EINVAL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const int64_t P = n_tokens * H, dd = (int64_t)d * d;
-  for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
-    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
-    const int64_t p0 = n0 * H;
-    const FactLayout L = fact_layout(nc, H, d, du, b_rank, q_rank, T, false, false);
-    float* Bx = reinterpret_cast<float*>(ws + L.Bx);
-    float* Qx = reinterpret_cast<float*>(ws + L.Qx);
-    float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
-    int rc = expand_chunk(coeff_B + n0 * b_rank, coeff_Q + n0 * q_rank, coeff_Qf + p0 * q_rank, B_basis, Q_basis,
-                          nc, H, d, du, b_rank, q_rank, Bx, Qx, Qfx, s);
-    if (rc != TTC_LQR_OK) return rc;
-    float* v1 = stash ? stash + p0 * dd : nullptr;
-    float* q0 = stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
-    rc = fwd_d(d, A_diag + p0 * d, Bx, Qx, R_inv + p0 * du, Qfx, log_gamma_A + p0, log_gamma_B + p0 * du,
-               log_gamma_Q + p0 * d, h0 + p0 * d, nc * H, H, T, u + p0 * du, v1, q0, stash ? kStashV1 : 0, status, s,
-               flags);
-    if (rc != TTC_LQR_OK) return rc;
-  }
-  return TTC_LQR_OK;
+  return forward_factored_entry<float>(A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, log_gamma_A, log_gamma_B,
+                                       log_gamma_Q, h0, B_basis, Q_basis, n_tokens, heads, d, du, b_rank, q_rank, T,
+                                       flags, u, stash, workspace, workspace_bytes, status, stream);
+}
+
+int ttc_lqr_forward_factored_bf16(const uint16_t* A_diag, const uint16_t* coeff_B, const uint16_t* coeff_Q,
+                                  const uint16_t* R_inv, const uint16_t* coeff_Qf, const uint16_t* log_gamma_A,
+                                  const uint16_t* log_gamma_B, const uint16_t* log_gamma_Q, const uint16_t* h0,
+                                  const uint16_t* B_basis, const uint16_t* Q_basis, int64_t n_tokens, int32_t heads,
+                                  int32_t d, int32_t du, int32_t b_rank, int32_t q_rank, int32_t T, int32_t flags,
+                                  float* u, float* stash, void* workspace, size_t workspace_bytes, int32_t* status,
+                                  void* stream) {
+  return forward_factored_entry<uint16_t>(A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, log_gamma_A, log_gamma_B,
+                                          log_gamma_Q, h0, B_basis, Q_basis, n_tokens, heads, d, du, b_rank, q_rank,
+                                          T, flags, u, stash, workspace, workspace_bytes, status, stream);
 }
 
 int ttc_lqr_backward_factored(const float* A_diag, const float* coeff_B, const float* coeff_Q, const float* R_inv,
@@ -617,65 +867,30 @@ int ttc_lqr_backward_factored(const float* A_diag, const float* coeff_B, const f
                               float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0,
                               float* grad_B_basis, float* grad_Q_basis, void* workspace, size_t workspace_bytes,
                               float grad_limit, int32_t* status, int64_t* n_fallback, void* stream) {
-  if (n_fallback) *n_fallback = 0;
-  if (!fact_args_ok(n_tokens, heads, d, du, b_rank, q_rank, T)) return TTC_LQR_EINVAL;
-  if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
-  const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
-  if (!grad_B_basis || !grad_Q_basis || !workspace) return TTC_LQR_EINVAL;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  char* ws = static_cast<char*>(workspace);
-  const int Eb = d * du, Eq = d * d;
-  if (n_tokens == 0) {  // the basis gradients are sums over no tokens
-    int rc = launch_reduce(nullptr, 0, b_rank, nullptr, Eb, nullptr, grad_B_basis, 0, s);
-    return rc == TTC_LQR_OK ? launch_reduce(nullptr, 0, q_rank, nullptr, Eq, nullptr, grad_Q_basis, 0, s) : rc;
-  }
-  if (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !log_gamma_A || !log_gamma_B || !log_gamma_Q ||
-      !h0 || !B_basis || !Q_basis || !d_u || !grad_A_diag || !grad_coeff_B || !grad_coeff_Q || !grad_R_inv ||
-      !grad_coeff_Qf || !grad_log_gamma_A || !grad_log_gamma_B || !grad_log_gamma_Q || !grad_h0 ||
-      (!stable && !u) || !aligned16(B_basis) || !aligned16(Q_basis))
-    return TTC_LQR_EINVAL;
-  const int H = heads;
-  const bool with_stash = stash != nullptr && !stable;
-  const int64_t chunk = fact_chunk(n_tokens, H, d, du, b_rank, q_rank, T, with_stash, true, workspace_bytes);
-  if (chunk == 0) return TTC_LQR_EINVAL;
-  const int64_t P = n_tokens * H, dd = (int64_t)d * d;
-  int64_t total_fb = 0;
-  for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
-    const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
-    const int64_t p0 = n0 * H, Pc = nc * H;
-    const FactLayout L = fact_layout(nc, H, d, du, b_rank, q_rank, T, with_stash, true);
-    float* Bx = reinterpret_cast<float*>(ws + L.Bx);
-    float* Qx = reinterpret_cast<float*>(ws + L.Qx);
-    float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
-    float* gB = reinterpret_cast<float*>(ws + L.gB);
-    float* gQ = reinterpret_cast<float*>(ws + L.gQ);
-    float* gQf = reinterpret_cast<float*>(ws + L.gQf);
-    float* part = reinterpret_cast<float*>(ws + L.part);
-    const float *cB = coeff_B + n0 * b_rank, *cQ = coeff_Q + n0 * q_rank, *cQf = coeff_Qf + p0 * q_rank;
-    int rc = expand_chunk(cB, cQ, cQf, B_basis, Q_basis, nc, H, d, du, b_rank, q_rank, Bx, Qx, Qfx, s);
-    if (rc != TTC_LQR_OK) return rc;
-    const float* v1 = with_stash ? stash + p0 * dd : nullptr;
-    const float* q0 = with_stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
-    int64_t nfb = 0;
-    rc = backward_core(A_diag + p0 * d, Bx, Qx, R_inv + p0 * du, Qfx, log_gamma_A + p0, log_gamma_B + p0 * du,
-                       log_gamma_Q + p0 * d, h0 + p0 * d, u ? u + p0 * du : nullptr, d_u + p0 * du, nc, H, d, du, T,
-                       flags, v1, q0, grad_A_diag + p0 * d, gB, gQ, grad_R_inv + p0 * du, gQf,
-                       grad_log_gamma_A + p0, grad_log_gamma_B + p0 * du, grad_log_gamma_Q + p0 * d,
-                       grad_h0 + p0 * d, ws + L.inner, L.total - L.inner, grad_limit, status, &nfb, s);
-    if (rc != TTC_LQR_OK) return rc;
-    total_fb += nfb;
-    // chain rule of the expansion: coefficient gradients, then the basis sums
-    rc = launch_project(gB, nc, Eb, B_basis, b_rank, grad_coeff_B + n0 * b_rank, s);
-    if (rc == TTC_LQR_OK) rc = launch_project(gQ, nc, Eq, Q_basis, q_rank, grad_coeff_Q + n0 * q_rank, s);
-    if (rc == TTC_LQR_OK) rc = launch_project(gQf, Pc, Eq, Q_basis, q_rank, grad_coeff_Qf + p0 * q_rank, s);
-    const int first = n0 == 0 ? 0 : 1;
-    if (rc == TTC_LQR_OK) rc = launch_reduce(cB, nc, b_rank, gB, Eb, part, grad_B_basis, first, s);
-    if (rc == TTC_LQR_OK) rc = launch_reduce(cQ, nc, q_rank, gQ, Eq, part, grad_Q_basis, first, s);
-    if (rc == TTC_LQR_OK) rc = launch_reduce(cQf, Pc, q_rank, gQf, Eq, part, grad_Q_basis, 1, s);
-    if (rc != TTC_LQR_OK) return rc;
-  }
-  if (n_fallback) *n_fallback = total_fb;
-  return TTC_LQR_OK;
+  return backward_factored_entry<float>(
+      A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0, B_basis, Q_basis, u, d_u,
+      n_tokens, heads, d, du, b_rank, q_rank, T, flags, stash, grad_A_diag, grad_coeff_B, grad_coeff_Q, grad_R_inv,
+      grad_coeff_Qf, grad_log_gamma_A, grad_log_gamma_B, grad_log_gamma_Q, grad_h0, grad_B_basis, grad_Q_basis,
+      workspace, workspace_bytes, grad_limit, status, n_fallback, stream);
+}
+
+int ttc_lqr_backward_factored_bf16(const uint16_t* A_diag, const uint16_t* coeff_B, const uint16_t* coeff_Q,
+                                   const uint16_t* R_inv, const uint16_t* coeff_Qf, const uint16_t* log_gamma_A,
+                                   const uint16_t* log_gamma_B, const uint16_t* log_gamma_Q, const uint16_t* h0,
+                                   const uint16_t* B_basis, const uint16_t* Q_basis, const float* u,
+                                   const uint16_t* d_u, int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
+                                   int32_t b_rank, int32_t q_rank, int32_t T, int32_t flags, const float* stash,
+                                   uint16_t* grad_A_diag, uint16_t* grad_coeff_B, uint16_t* grad_coeff_Q,
+                                   uint16_t* grad_R_inv, uint16_t* grad_coeff_Qf, uint16_t* grad_log_gamma_A,
+                                   uint16_t* grad_log_gamma_B, uint16_t* grad_log_gamma_Q, uint16_t* grad_h0,
+                                   uint16_t* grad_B_basis, uint16_t* grad_Q_basis, void* workspace,
+                                   size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
+                                   void* stream) {
+  return backward_factored_entry<uint16_t>(
+      A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0, B_basis, Q_basis, u, d_u,
+      n_tokens, heads, d, du, b_rank, q_rank, T, flags, stash, grad_A_diag, grad_coeff_B, grad_coeff_Q, grad_R_inv,
+      grad_coeff_Qf, grad_log_gamma_A, grad_log_gamma_B, grad_log_gamma_Q, grad_h0, grad_B_basis, grad_Q_basis,
+      workspace, workspace_bytes, grad_limit, status, n_fallback, stream);
 }
 
 }  // extern "C"

@@ -193,7 +193,38 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ p, int64_
 
 constexpr int kSlabGroup = 64;  // first-level group of sum_slabs_kernel
 
+// bf16 storage (bit patterns) <-> fp32: widening is exact; narrowing rounds to nearest even
+// (NaN stays NaN), as torch's .to(torch.bfloat16).
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t* __restrict__ in, int64_t n,
+                                                          float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) out[i] = __uint_as_float((uint32_t)in[i] << 16);
+}
+
+__global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ in, int64_t n,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t u = __float_as_uint(in[i]);
+  uint16_t r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) r = (uint16_t)((u >> 16) | 0x40u);  // NaN: quiet, keep the sign
+  else r = (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  out[i] = r;
+}
+
 static bool launched() { return hipGetLastError() == hipSuccess; }
+
+int launch_bf16_to_f32(const uint16_t* in, int64_t n, float* out, hipStream_t s) {
+  if (n <= 0) return TTC_LQR_OK;
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, n, out);
+  return launched() ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+}
+
+int launch_f32_to_bf16(const float* in, int64_t n, uint16_t* out, hipStream_t s) {
+  if (n <= 0) return TTC_LQR_OK;
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in, n, out);
+  return launched() ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+}
 
 // Tile shape of reduce_kernel for rank R: (RT, ET) = (1, 16), (2, 16) or (4, 8).
 static void reduce_shape(int R, int& RT, int& ET) {

@@ -265,6 +265,10 @@ class HipLQRFactoredFunc(torch.autograd.Function):
     ``B = einsum("nr,rij->nij", coeff_B, B_basis)``, ``Q`` likewise, ``Q_f[n,h] =
     einsum("r,rij->ij", coeff_Qf[n,h], Q_basis)``.  Same ``u``, arithmetic, certificate,
     stash and error behaviour as :class:`HipLQRSolveFunc` on the expanded tensors.
+    When all eleven tensors are bf16 they are handed to the library as bf16 (the ``_bf16``
+    entry points widen each token chunk to fp32 in the workspace, and store the gradients as
+    bf16); ``u`` is computed and kept in fp32 and returned as bf16.  Any other dtype mix is
+    computed from fp32 copies.
     """
 
     @staticmethod
@@ -286,20 +290,22 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         assert 1 <= rb <= 64 and 1 <= rq <= 64, f"ranks 1..64 are supported, got b_rank={rb}, q_rank={rq}"
         dev = A_diag.device
         out_dtype = A_diag.dtype
+        bf16 = all(x.dtype == torch.bfloat16 for x in ins)
+        store = torch.bfloat16 if bf16 else torch.float32
         Dp = padded_dim(d, du)
         flags = riccati_flags(precision, T, Dp)
         F = torch.nn.functional
-        f32 = [x.detach().to(torch.float32).contiguous() for x in ins]
+        xs = [x.detach().to(store).contiguous() for x in ins]
         pd, pu = Dp - d, Dp - du
         if pd or pu:  # zero-padded states / unit-cost dummy controls, as HipLQRSolveFunc
-            f32[0] = F.pad(f32[0], (0, pd))
-            f32[3] = F.pad(f32[3], (0, pu), value=1.0)
-            f32[6] = F.pad(f32[6], (0, pu))
-            f32[7] = F.pad(f32[7], (0, pd))
-            f32[8] = F.pad(f32[8], (0, pd))
-            f32[9] = F.pad(f32[9], (0, pu, 0, pd))
-            f32[10] = F.pad(f32[10], (0, pd, 0, pd))
-            f32 = [t.contiguous() for t in f32]
+            xs[0] = F.pad(xs[0], (0, pd))
+            xs[3] = F.pad(xs[3], (0, pu), value=1.0)
+            xs[6] = F.pad(xs[6], (0, pu))
+            xs[7] = F.pad(xs[7], (0, pd))
+            xs[8] = F.pad(xs[8], (0, pd))
+            xs[9] = F.pad(xs[9], (0, pu, 0, pd))
+            xs[10] = F.pad(xs[10], (0, pd, 0, pd))
+            xs = [t.contiguous() for t in xs]
         u = torch.empty(bs, nh, Dp, device=dev, dtype=torch.float32)
         status = torch.zeros(1, device=dev, dtype=torch.int32)
         policy = stash or os.environ.get("TTC_LQR_STASH", "auto")
@@ -309,52 +315,54 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         keep = (need_grad and bs > 0 and not stable_backward
                 and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev))))
         st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32) if keep else None
-        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, 0, 0)
-        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, 0, 0)
+        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, 0, 0, int(bf16))
+        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, 0, 0, int(bf16))
         ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
+        fwd = lib.ttc_lqr_forward_factored_bf16 if bf16 else lib.ttc_lqr_forward_factored
         with torch.cuda.device(dev):
-            rc = lib.ttc_lqr_forward_factored(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, rb, rq, T, flags,
-                                              u.data_ptr(), None if st is None else st.data_ptr(), ws.data_ptr(),
-                                              ws.numel(), status.data_ptr(), _stream_handle(dev))
-        check(rc, "ttc_lqr_forward_factored")
+            rc = fwd(*[t.data_ptr() for t in xs], bs, nh, Dp, Dp, rb, rq, T, flags, u.data_ptr(),
+                     None if st is None else st.data_ptr(), ws.data_ptr(), ws.numel(), status.data_ptr(),
+                     _stream_handle(dev))
+        check(rc, "ttc_lqr_forward_factored" + ("_bf16" if bf16 else ""))
         del ws
         if int(status.item()) & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
-            ctx.save_for_backward(*f32, u, *([st] if st is not None else []))
+            ctx.save_for_backward(*xs, u, *([st] if st is not None else []))
         ctx.meta = (bs, nh, d, du, Dp, rb, rq, T, float(grad_limit), st is not None, [x.dtype for x in ins],
-                    flags | (FLAG_STABLE_BWD if stable_backward else 0))
+                    flags | (FLAG_STABLE_BWD if stable_backward else 0), bf16)
         return u[..., :du].to(out_dtype)
 
     @staticmethod
     def backward(ctx, d_u):
-        bs, nh, d, du, Dp, rb, rq, T, grad_limit, has_stash, dtypes, flags = ctx.meta
+        bs, nh, d, du, Dp, rb, rq, T, grad_limit, has_stash, dtypes, flags, bf16 = ctx.meta
         saved = ctx.saved_tensors
-        f32 = list(saved[:11])
+        xs = list(saved[:11])
         u = saved[11]
         st = saved[12] if has_stash else None
-        dev = f32[0].device
+        dev = xs[0].device
+        store = torch.bfloat16 if bf16 else torch.float32
         if du == Dp:
-            dU = d_u.to(torch.float32).contiguous()
+            dU = d_u.to(store).contiguous()
         else:
-            dU = torch.zeros(bs, nh, Dp, device=dev, dtype=torch.float32)
-            dU[..., :du] = d_u.to(torch.float32)
-        E = lambda *shape: torch.empty(*shape, device=dev, dtype=torch.float32)  # noqa: E731
+            dU = torch.zeros(bs, nh, Dp, device=dev, dtype=store)
+            dU[..., :du] = d_u.to(store)
+        E = lambda *shape: torch.empty(*shape, device=dev, dtype=store)  # noqa: E731
         g = [E(bs, nh, Dp), E(bs, rb), E(bs, rq), E(bs, nh, Dp), E(bs, nh, rq), E(bs, nh), E(bs, nh, Dp),
              E(bs, nh, Dp), E(bs, nh, Dp), E(rb, Dp, Dp), E(rq, Dp, Dp)]
         status = torch.zeros(1, device=dev, dtype=torch.int32)
         with_st = 1 if st is not None else 0
-        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, with_st, 1)
-        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, with_st, 1)
+        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16))
+        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16))
         ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         n_fb = ctypes.c_int64(0)
+        bwd = lib.ttc_lqr_backward_factored_bf16 if bf16 else lib.ttc_lqr_backward_factored
         with torch.cuda.device(dev):
-            rc = lib.ttc_lqr_backward_factored(
-                *[t.data_ptr() for t in f32], u.data_ptr(), dU.data_ptr(), bs, nh, Dp, Dp, rb, rq, T, flags,
-                None if st is None else st.data_ptr(), *[t.data_ptr() for t in g], ws.data_ptr(), ws.numel(),
-                limit, status.data_ptr(), ctypes.byref(n_fb), _stream_handle(dev))
-        check(rc, "ttc_lqr_backward_factored")
+            rc = bwd(*[t.data_ptr() for t in xs], u.data_ptr(), dU.data_ptr(), bs, nh, Dp, Dp, rb, rq, T, flags,
+                     None if st is None else st.data_ptr(), *[t.data_ptr() for t in g], ws.data_ptr(), ws.numel(),
+                     limit, status.data_ptr(), ctypes.byref(n_fb), _stream_handle(dev))
+        check(rc, "ttc_lqr_backward_factored" + ("_bf16" if bf16 else ""))
         last_backward_stats.update(problems=bs * nh, fallback=int(n_fb.value))
         if int(status.item()) & _ERROR_BITS:
             raise RuntimeError(_BWD_MSG)
