@@ -194,6 +194,23 @@ int ttc_lqr_backward_factored(const float* A_diag, const float* coeff_B, const f
                               size_t workspace_bytes, float grad_limit, int32_t* status,
                               int64_t* n_fallback, void* stream);
 
+/* ---- Layer epilogue: the rescale of the solver output (ttc/layers/ttc_layer.py:142-147) ----
+ * y = rescale(u) per problem over the control dim, on `stream`; d == du in {16, 32, 64}
+ * (padded dims: padded controls are 0, padded states of h0 are 0, so norms are unchanged).
+ *   TTC_LQR_RESCALE_L2NORM:  y = u / sqrt(sum(u^2) + 1e-6)   (fla's l2norm; h0 unused)
+ *   TTC_LQR_RESCALE_H0NORM:  y = u / ||u|| * ||h0||           (norms treated as constants
+ *                            in the backward, as the reference detaches them)
+ * ttc_lqr_rescale_backward maps d_y to d_u (the gradient into ttc_lqr_backward*); no
+ * gradient flows to h0.  Replaces the torch ops of the layer's back-end; with them the
+ * layer needs no NaN check of its own (ttc_layer.py:139): non-finite u already sets
+ * TTC_LQR_STATUS_NONFINITE in the forward's status word. */
+#define TTC_LQR_RESCALE_L2NORM 1
+#define TTC_LQR_RESCALE_H0NORM 2
+int ttc_lqr_rescale(const float* u, const float* h0, int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
+                    int32_t mode, float* y, void* stream);
+int ttc_lqr_rescale_backward(const float* u, const float* h0, const float* d_y, int64_t n_tokens,
+                             int32_t heads, int32_t d, int32_t du, int32_t mode, float* d_u, void* stream);
+
 /* bf16 storage (config 4 stores its activations in bf16): the same two entry points with
  * every input, d_u and every gradient stored as bf16 (raw bit patterns, uint16_t); u and
  * the stash stay fp32 (the backward's rollout starts from u).  Each token chunk is widened

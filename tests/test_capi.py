@@ -31,7 +31,8 @@ def test_header_declares_expected_entry_points():
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
         "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
-        "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16"])
+        "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
+        "ttc_lqr_rescale_backward"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -158,3 +159,12 @@ def test_factored_argument_validation(L):
     assert bwd(rb=70) == (1, 0)
     assert bwd(basis=odd) == (1, 0)
     assert bwd(work=64) == (1, 0)
+
+
+def test_rescale_argument_validation(L):
+    p = ctypes.c_void_p(16)
+    assert L.ttc_lqr_rescale(p, p, 1, 1, 16, 16, 3, p, None) == 1          # unknown mode
+    assert L.ttc_lqr_rescale(p, None, 1, 1, 16, 16, 2, p, None) == 1       # h0_norm needs h0
+    assert L.ttc_lqr_rescale(p, p, 1, 1, 24, 24, 1, p, None) == 2          # unpadded dims
+    assert L.ttc_lqr_rescale(p, p, 0, 1, 16, 16, 1, p, None) == 0          # nothing to do
+    assert L.ttc_lqr_rescale_backward(p, p, None, 1, 1, 16, 16, 1, p, None) == 1

@@ -267,3 +267,45 @@ def test_layer_bf16_runs_on_bf16_storage():
     for (n, pa), (_, pb) in zip(a.named_parameters(), b.named_parameters()):
         assert pb.grad.dtype == torch.bfloat16
         assert _relerr(pb.grad.float().cpu(), pa.grad.cpu()) <= 5e-2, n
+
+
+@pytest.mark.parametrize("mode", ["l2_norm", "h0_norm"])
+@pytest.mark.parametrize("d", [16, 24, 64])
+def test_fused_rescale_matches_torch_backend(mode, d):
+    """ttc_lqr_rescale / _backward (the layer's back-end, ttc_layer.py:142-147) fused into the
+    factored call: values and the gradients of all eleven inputs equal the unfused call
+    followed by the torch rescale (detached norms for h0_norm), to fp32 rounding."""
+    from ttc.solvers.hip_lqr import hip_lqr_solve_factored
+    from ttc.layers.ttc_layer import l2norm
+    ins = factored_inputs(3 if d != 16 else 2, 4, d=None if d == 16 else d, rb=12, rq=20)
+    dev = torch.device("cuda:0")
+    N, H, dd = ins[0].shape
+    dY = torch.randn(N, H, ins[3].shape[-1], device=dev, generator=torch.Generator(device=dev).manual_seed(3))
+    xa = [t.to(dev).float().requires_grad_(True) for t in ins]
+    ya = hip_lqr_solve_factored(*xa, 24, rescale=mode)
+    (ya * dY).sum().backward()
+    xb = [t.to(dev).float().requires_grad_(True) for t in ins]
+    u = hip_lqr_solve_factored(*xb, 24)
+    if mode == "l2_norm":
+        yb = l2norm(u)
+    else:
+        yb = u / torch.linalg.norm(u, dim=-1).detach()[..., None] * torch.linalg.norm(xb[8], dim=-1).detach()[..., None]
+    (yb * dY).sum().backward()
+    assert _relerr(ya.detach().cpu(), yb.detach().cpu()) <= 1e-6
+    for n, a, b in zip(NAMES11, xa, xb):
+        assert _relerr(a.grad.cpu(), b.grad.cpu()) <= 1e-5, n
+
+
+def test_layer_h0_norm_factored_equals_materialised():
+    from ttc import TTCLayer
+    torch.manual_seed(2)
+    a = TTCLayer(32, 32, 16, 8, 16, 16, rescale="h0_norm", solver_impl="hip", factored=True).cuda()
+    b = TTCLayer(32, 32, 16, 8, 16, 16, rescale="h0_norm", solver_impl="hip", factored=False).cuda()
+    b.load_state_dict(a.state_dict())
+    x = torch.randn(2, 9, 8, 32, device="cuda", generator=torch.Generator(device="cuda").manual_seed(5))
+    ya, yb = a(x, T=16), b(x, T=16)
+    ya.square().sum().backward()
+    yb.square().sum().backward()
+    assert _relerr(ya.detach().cpu(), yb.detach().cpu()) <= 1e-5
+    for (n, pa), (_, pb) in zip(a.named_parameters(), b.named_parameters()):
+        assert _relerr(pa.grad.cpu(), pb.grad.cpu()) <= 1e-4, n

@@ -12,8 +12,11 @@ With ``factored=True`` (the default wherever the solver has a factored form,
 ``LQR_FACTORED_IMPL_MAP``) the layer hands the solver the mixture coefficients and
 bases instead of ``B``, ``Q`` and ``Q_f``: the library expands them per token chunk on
 the device, so the ``[N, H, h, h]`` ``Q_f`` (and its gradient) is never formed in full
--- 137 GB at h_dim = 64 with 8.4 M problems.  Same values and gradients up to fp32
-rounding; ``factored=False`` runs the reference's materialised formulation.
+-- 137 GB at h_dim = 64 with 8.4 M problems.  On that path the rescale of ``u``
+(``ttc_layer.py:142-147``) runs fused into the solver call (fp32), and the NaN check of
+``:139`` is the solver's device status word instead of a separate reduction and host
+sync.  Same values and gradients up to fp32 rounding; ``factored=False`` runs the
+reference's materialised formulation and back-end.
 
 Generalisations over the reference (each keeps the reference result whenever
 the reference runs at all):
@@ -150,18 +153,22 @@ class TTCLayer(nn.Module):
         if T == 0:
             # horizon zero disables the layer (ttc_layer.py:101-102)
             return torch.zeros(*lead, self.out_dim, device=h0.device, dtype=h0.dtype)
+        rescaled = False
         if self.factored:
             ins = self.factored_inputs(h0)
             x0 = ins[8]
-            u = self.solver_factored(*ins, T)
+            # fp32: the rescale runs fused into the solver call; the solver's device status word
+            # already raises on a non-finite u, so no separate NaN reduction / host sync
+            rescaled = self.rescale != "none" and all(t.dtype == torch.float32 for t in ins)
+            u = self.solver_factored(*ins, T, rescale=self.rescale if rescaled else "none")
         else:
             A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, x0 = self.solver_inputs(h0)
             u = self.solver(A_diag, B, Q, R_inv, Q_f, lgA, lgB, lgQ, x0, T)
-        if torch.isnan(u).any():
-            raise RuntimeError("NaN detected in TTC layer solver output.")
-        if self.rescale == "l2_norm":
+            if torch.isnan(u).any():
+                raise RuntimeError("NaN detected in TTC layer solver output.")
+        if not rescaled and self.rescale == "l2_norm":
             u = l2norm(u)
-        elif self.rescale == "h0_norm":
+        elif not rescaled and self.rescale == "h0_norm":
             h0_norm = torch.linalg.norm(x0, dim=-1, ord=2).detach()
             u_norm = torch.linalg.norm(u, dim=-1, ord=2).detach()
             u = u / u_norm[..., None] * h0_norm[..., None]

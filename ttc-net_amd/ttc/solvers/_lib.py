@@ -67,6 +67,10 @@ def _load():
     L.ttc_lqr_backward_factored.argtypes = ([f32p] * 13 + [i64, i32, i32, i32, i32, i32, i32, i32] + [f32p]
                                             + [f32p] * 11 + [ctypes.c_void_p, sz, ctypes.c_float, f32p,
                                                              ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p])
+    L.ttc_lqr_rescale.restype = ctypes.c_int
+    L.ttc_lqr_rescale.argtypes = [f32p, f32p, i64, i32, i32, i32, i32, f32p, ctypes.c_void_p]
+    L.ttc_lqr_rescale_backward.restype = ctypes.c_int
+    L.ttc_lqr_rescale_backward.argtypes = [f32p, f32p, f32p, i64, i32, i32, i32, i32, f32p, ctypes.c_void_p]
     for suffix in ("", "_bf16"):
         getattr(L, "ttc_lqr_forward_factored" + suffix).restype = ctypes.c_int
         getattr(L, "ttc_lqr_forward_factored" + suffix).argtypes = L.ttc_lqr_forward_factored.argtypes

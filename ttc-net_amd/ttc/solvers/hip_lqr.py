@@ -63,6 +63,7 @@ FP64_HORIZON = 512
 _FWD_MSG = "Numerical instability detected during fused LQR forward recurrence."
 _BWD_MSG = "Numerical instability detected during fused LQR backward pass."
 _ERROR_BITS = 1 | 2  # TTC_LQR_STATUS_NONFINITE | TTC_LQR_STATUS_LARGE (4 = RESCUED is informational)
+_RESCALE_MODES = {"none": 0, "l2_norm": 1, "h0_norm": 2}  # TTC_LQR_RESCALE_*
 
 # problems / fallback problems of the most recent backward call (observability)
 last_backward_stats = {"problems": 0, "fallback": 0}
@@ -269,14 +270,18 @@ class HipLQRFactoredFunc(torch.autograd.Function):
     entry points widen each token chunk to fp32 in the workspace, and store the gradients as
     bf16); ``u`` is computed and kept in fp32 and returned as bf16.  Any other dtype mix is
     computed from fp32 copies.
+    ``rescale`` (``"none" | "l2_norm" | "h0_norm"``, fp32 storage): the layer's rescale of
+    ``u`` (``ttc_layer.py:142-147``) fused into the call -- the result is the rescaled output
+    and the backward takes its gradient (``ttc_lqr_rescale`` / ``ttc_lqr_rescale_backward``).
     """
 
     @staticmethod
     def forward(ctx, A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0,
                 B_basis, Q_basis, T: int, grad_limit: float = 1e6, stash: str | None = None,
-                precision: str = "auto", stable_backward: bool = False):
+                precision: str = "auto", stable_backward: bool = False, rescale: str = "none"):
         ins = [A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0,
                B_basis, Q_basis]
+        assert rescale in _RESCALE_MODES, f"Unknown rescale method {rescale}"
         assert all(x.is_cuda for x in ins), "hip LQR solver inputs must be on a GPU"
         bs, nh, d = A_diag.shape
         rb, _, du = B_basis.shape
@@ -292,6 +297,8 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         out_dtype = A_diag.dtype
         bf16 = all(x.dtype == torch.bfloat16 for x in ins)
         store = torch.bfloat16 if bf16 else torch.float32
+        mode = _RESCALE_MODES[rescale]
+        assert not (mode and bf16), "the fused rescale runs on fp32 storage; rescale bf16 outputs outside"
         Dp = padded_dim(d, du)
         flags = riccati_flags(precision, T, Dp)
         F = torch.nn.functional
@@ -325,17 +332,24 @@ class HipLQRFactoredFunc(torch.autograd.Function):
                      _stream_handle(dev))
         check(rc, "ttc_lqr_forward_factored" + ("_bf16" if bf16 else ""))
         del ws
+        y = u
+        if mode:
+            y = torch.empty_like(u)
+            with torch.cuda.device(dev):
+                rc = lib.ttc_lqr_rescale(u.data_ptr(), xs[8].data_ptr(), bs, nh, Dp, Dp, mode, y.data_ptr(),
+                                         _stream_handle(dev))
+            check(rc, "ttc_lqr_rescale")
         if int(status.item()) & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
             ctx.save_for_backward(*xs, u, *([st] if st is not None else []))
         ctx.meta = (bs, nh, d, du, Dp, rb, rq, T, float(grad_limit), st is not None, [x.dtype for x in ins],
-                    flags | (FLAG_STABLE_BWD if stable_backward else 0), bf16)
-        return u[..., :du].to(out_dtype)
+                    flags | (FLAG_STABLE_BWD if stable_backward else 0), bf16, mode)
+        return y[..., :du].to(out_dtype)
 
     @staticmethod
     def backward(ctx, d_u):
-        bs, nh, d, du, Dp, rb, rq, T, grad_limit, has_stash, dtypes, flags, bf16 = ctx.meta
+        bs, nh, d, du, Dp, rb, rq, T, grad_limit, has_stash, dtypes, flags, bf16, mode = ctx.meta
         saved = ctx.saved_tensors
         xs = list(saved[:11])
         u = saved[11]
@@ -347,6 +361,12 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         else:
             dU = torch.zeros(bs, nh, Dp, device=dev, dtype=store)
             dU[..., :du] = d_u.to(store)
+        if mode:  # d_y -> d_u through the fused rescale
+            dY, dU = dU, torch.empty_like(dU)
+            with torch.cuda.device(dev):
+                rc = lib.ttc_lqr_rescale_backward(u.data_ptr(), xs[8].data_ptr(), dY.data_ptr(), bs, nh, Dp, Dp, mode,
+                                                  dU.data_ptr(), _stream_handle(dev))
+            check(rc, "ttc_lqr_rescale_backward")
         E = lambda *shape: torch.empty(*shape, device=dev, dtype=store)  # noqa: E731
         g = [E(bs, nh, Dp), E(bs, rb), E(bs, rq), E(bs, nh, Dp), E(bs, nh, rq), E(bs, nh), E(bs, nh, Dp),
              E(bs, nh, Dp), E(bs, nh, Dp), E(rb, Dp, Dp), E(rq, Dp, Dp)]
@@ -369,15 +389,16 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         out = (g[0][..., :d], g[1], g[2], g[3][..., :du], g[4], g[5], g[6][..., :du], g[7][..., :d],
                g[8][..., :d], g[9][:, :d, :du], g[10][:, :d, :d])
         out = tuple(o.to(dt) if need else None for o, dt, need in zip(out, dtypes, ctx.needs_input_grad[:11]))
-        return out + (None, None, None, None, None)
+        return out + (None, None, None, None, None, None)
 
 
 def hip_lqr_solve_factored(A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q,
                            h0, B_basis, Q_basis, T: int, grad_limit: float = 1e6, stash: str | None = None,
-                           precision: str = "auto", stable_backward: bool = False) -> torch.Tensor:
+                           precision: str = "auto", stable_backward: bool = False,
+                           rescale: str = "none") -> torch.Tensor:
     """``hip_lqr_solve`` on the layer's low-rank factors (see :class:`HipLQRFactoredFunc`):
     equal to ``hip_lqr_solve(A_diag, einsum(coeff_B, B_basis), einsum(coeff_Q, Q_basis), R_inv,
     einsum(coeff_Qf, Q_basis), ...)`` with gradients for the coefficients and both bases."""
     return HipLQRFactoredFunc.apply(A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B,
                                     log_gamma_Q, h0, B_basis, Q_basis, T, grad_limit, stash, precision,
-                                    stable_backward)
+                                    stable_backward, rescale)
