@@ -72,6 +72,14 @@ extern "C" {
  * end, a conditioning certificate per problem and a row-layout recompute of the
  * problems that miss it).  Same results to fp32 rounding. */
 #define TTC_LQR_FLAG_RICCATI_STEPS 8
+/* TTC_LQR_FLAG_COMPACT_STASH (factored entry points only): the stash holds only the upper
+ * triangle of each problem's V_1 (ttc_lqr_compact_stash_bytes: d(d+1)/2 floats per problem,
+ * rows i <= j packed row by row, problem-major) and the backward recomputes Quu_0 =
+ * R + B_0' V_1 B_0 from it on the matrix cores -- 4x smaller at d = 64, so the stash of an
+ * 8.4 M-problem d = 64 batch fits beside its inputs (70 GB instead of 275 GB) and the
+ * backward needs no forward sweep.  Pass the same flag to both calls.  Same results to
+ * fp32 rounding. */
+#define TTC_LQR_FLAG_COMPACT_STASH 16
 
 /* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
  * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds
@@ -95,6 +103,9 @@ int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags);
  * value matrix V_1 (d*d floats, the cost-to-go Hessian at step 1) and the step-0 control
  * Hessian Quu_0 (du*du floats).  `T` is accepted for signature stability (unused). */
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T);
+
+/* Bytes of the compact stash (TTC_LQR_FLAG_COMPACT_STASH): 4 * N * H * d(d+1)/2. */
+size_t ttc_lqr_compact_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du);
 
 /* Workspace bytes ttc_lqr_backward needs to process `chunk_tokens` tokens per pass
  * (it loops over the tokens in chunks of that size).  `with_stash` != 0 when the
@@ -155,6 +166,7 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
  * proposed as its next component; the entry points keep the conventions above. */
 
 /* Workspace bytes of the factored entry points for `chunk_tokens` tokens per pass:
+ * with_stash = 0 (no stash), 1 (stash), 2 (compact stash: plus the chunk's full V_1 and Quu_0);
  * backward = 0 for ttc_lqr_forward_factored (the expanded B, Q, Q_f of a chunk),
  * backward != 0 for ttc_lqr_backward_factored (plus the chunk's B / Q / Q_f gradients,
  * the reduction partials and ttc_lqr_backward's own workspace); bf16 != 0 for the _bf16

@@ -30,6 +30,7 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
         "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes",
+        "ttc_lqr_compact_stash_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
         "ttc_lqr_rescale_backward"])
@@ -61,7 +62,8 @@ def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 8) == 1 and L.ttc_lqr_supported_flags(32, 32, 8 | 4) == 1
-    assert L.ttc_lqr_supported_flags(16, 16, 16) == 0
+    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 32) == 0
+    assert _fwd(L, flags=16) == 2          # the compact stash needs the factored entry points
     assert _fwd(L, d=64, du=64, flags=1) == 2
 
 
@@ -168,3 +170,12 @@ def test_rescale_argument_validation(L):
     assert L.ttc_lqr_rescale(p, p, 1, 1, 24, 24, 1, p, None) == 2          # unpadded dims
     assert L.ttc_lqr_rescale(p, p, 0, 1, 16, 16, 1, p, None) == 0          # nothing to do
     assert L.ttc_lqr_rescale_backward(p, p, None, 1, 1, 16, 16, 1, p, None) == 1
+
+
+def test_compact_stash_bytes(L):
+    assert L.ttc_lqr_compact_stash_bytes(1000, 16, 64, 64) == 4 * 16000 * 2080
+    assert 4 * L.ttc_lqr_compact_stash_bytes(10, 8, 64, 64) < L.ttc_lqr_stash_bytes(10, 8, 64, 64, 1) * 1.02
+    # the compact layout holds the chunk's full V_1 and Quu_0 besides
+    a = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 1, 1, 0)
+    b = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 2, 1, 0)
+    assert b - a >= 4 * 800 * 2 * 256

@@ -105,7 +105,7 @@ def check_factored(label, ins, T, seed=0, tol=TOL, **kw):
 
 
 @pytest.mark.parametrize("cfg,n_tok", [(2, 24), (3, 2), (4, 1)])
-@pytest.mark.parametrize("stash", ["always", "never"])
+@pytest.mark.parametrize("stash", ["always", "compact", "never"])
 def test_factored_config_slices(cfg, n_tok, stash):
     check_factored(f"cfg{cfg}", factored_inputs(cfg, n_tok), CONFIGS[cfg]["T"], stash=stash)
 
@@ -309,3 +309,26 @@ def test_layer_h0_norm_factored_equals_materialised():
     assert _relerr(ya.detach().cpu(), yb.detach().cpu()) <= 1e-5
     for (n, pa), (_, pb) in zip(a.named_parameters(), b.named_parameters()):
         assert _relerr(pa.grad.cpu(), pb.grad.cpu()) <= 1e-4, n
+
+
+@pytest.mark.parametrize("cfg,n_tok", [(2, 40), (3, 3), (4, 2)])
+def test_compact_stash_matches_full_stash(cfg, n_tok, monkeypatch):
+    """The compact stash (V_1's upper triangles; Quu_0 recomputed on the matrix cores in the
+    backward) against the full stash: u bitwise (same forward), gradients to fp32 rounding;
+    also over several token chunks."""
+    from ttc.solvers._lib import lib
+    ins = factored_inputs(cfg, n_tok, seed=8)
+    N, H, d = ins[0].shape
+    T = CONFIGS[cfg]["T"]
+    dU = torch.randn(N, H, d, generator=torch.Generator().manual_seed(6)).double().numpy()
+    full = run_factored(ins, T, dU, stash="always")
+    comp = run_factored(ins, T, dU, stash="compact")
+    assert np.array_equal(full["u"], comp["u"])
+    for k in NAMES11:
+        assert _relerr(comp[k], full[k]) <= 2e-5, k
+    ws = lib.ttc_lqr_factored_workspace_bytes(1, H, d, d, ins[1].shape[1], ins[2].shape[1], T, 2, 1, 0)
+    monkeypatch.setenv("TTC_LQR_WORKSPACE_BYTES", str(ws))
+    chunked = run_factored(ins, T, dU, stash="compact")
+    assert np.array_equal(full["u"], chunked["u"])
+    for k in NAMES11:
+        assert _relerr(chunked[k], full[k]) <= 2e-5, k

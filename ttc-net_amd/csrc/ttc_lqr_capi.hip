@@ -422,7 +422,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
 // for bf16 storage the chunk's inputs (and d_u) and per-problem gradients in fp32; last,
 // ttc_lqr_backward's own workspace for the chunk.
 struct FactLayout {
-  size_t bas, gbas, Bx, Qx, Qfx, gB, gQ, gQf, part, cin[10], cg[9], inner, total;
+  size_t bas, gbas, Bx, Qx, Qfx, gB, gQ, gQf, part, cin[10], cg[9], v1t, q0t, inner, total;
 };
 
 // Elements of the per-problem / per-token arrays of a chunk, in argument order:
@@ -433,8 +433,11 @@ static void io_counts(int64_t nc, int H, int d, int du, int rb, int rq, size_t (
   for (int k = 0; k < 10; ++k) n[k] = v[k];
 }
 
+// with_stash: the forward's stash is passed (compact: as the upper triangles of V_1, whose
+// full V_1 and Quu_0 the chunk then holds in v1t / q0t, in the forward before packing and in
+// the backward after unpacking).
 static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                              bool backward, bool bf16) {
+                              bool backward, bool bf16, bool compact = false) {
   const size_t N = (size_t)nc, P = (size_t)nc * (size_t)H, Eb = (size_t)d * du, Eq = (size_t)d * d;
   const size_t nbas = (size_t)rb * Eb + (size_t)rq * Eq;
   FactLayout L{};
@@ -477,6 +480,12 @@ static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, 
       }
     }
   }
+  if (compact && with_stash) {
+    L.v1t = off;
+    off += align256(P * Eq * sizeof(float));
+    L.q0t = off;
+    off += align256(P * (size_t)du * du * sizeof(float));
+  }
   if (backward) {
     L.inner = off;
     // ttc_lqr_backward's workspace for this chunk in one pass; the stable path (flag
@@ -496,12 +505,12 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Largest token chunk whose factored layout fits ws_bytes (0 when not even one token fits).
 static int64_t fact_chunk(int64_t n_tokens, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                          bool backward, bool bf16, size_t ws_bytes) {
-  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward, bf16).total > ws_bytes) return 0;
+                          bool backward, bool bf16, bool compact, size_t ws_bytes) {
+  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward, bf16, compact).total > ws_bytes) return 0;
   int64_t chunk = 1, hi = n_tokens;
   while (chunk < hi) {
     const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward, bf16).total <= ws_bytes) chunk = mid;
+    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward, bf16, compact).total <= ws_bytes) chunk = mid;
     else hi = mid - 1;
   }
   return chunk;
@@ -557,11 +566,13 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
                             int du, int rb, int rq, int T, int flags, float* u, float* stash, char* ws,
                             size_t ws_bytes, int32_t* status, hipStream_t s) {
   using St = Store<TS>;
-  const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, false, false, St::BF16, ws_bytes);
+  const bool compact = stash != nullptr && (flags & TTC_LQR_FLAG_COMPACT_STASH);
+  const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact,
+                                   ws_bytes);
   if (chunk == 0) return TTC_LQR_EINVAL;
   const int64_t P = n_tokens * H, dd = (int64_t)d * d;
   const size_t nb = (size_t)rb * d * du, nq = (size_t)rq * d * d;
-  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, false, false, St::BF16);
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact);
   int rc = TTC_LQR_OK;
   float* bas = reinterpret_cast<float*>(ws + L0.bas);
   const float* Bs = St::in(B_basis, 0, nb, bas, s, rc);
@@ -569,7 +580,7 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
   for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H;
-    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, false, false, St::BF16);
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact);
     size_t n[10];
     io_counts(nc, H, d, du, rb, rq, n);
     auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
@@ -590,8 +601,13 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
     if (rc != TTC_LQR_OK) return rc;
     float* v1 = stash ? stash + p0 * dd : nullptr;
     float* q0 = stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
+    if (compact) {  // full V_1 / Quu_0 of the chunk in the workspace, V_1's upper triangle to the stash
+      v1 = reinterpret_cast<float*>(ws + L.v1t);
+      q0 = reinterpret_cast<float*>(ws + L.q0t);
+    }
     rc = fwd_d(d, a, Bx, Qx, r, Qfx, la, lb, lq, hz, nc * H, H, T, u + p0 * du, v1, q0, stash ? kStashV1 : 0, status,
-               s, flags);
+               s, flags & ~TTC_LQR_FLAG_COMPACT_STASH);
+    if (compact && rc == TTC_LQR_OK) rc = launch_pack_upper(v1, nc * H, d, stash + p0 * (dd + d) / 2, s);
   }
   return rc;
 }
@@ -609,12 +625,14 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
   using St = Store<TS>;
   const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
   const bool with_stash = stash != nullptr && !stable;
+  const bool compact = with_stash && (flags & TTC_LQR_FLAG_COMPACT_STASH);
+  flags &= ~TTC_LQR_FLAG_COMPACT_STASH;
   const int Eb = d * du, Eq = d * d;
   const size_t nb = (size_t)rb * Eb, nq = (size_t)rq * Eq;
   const int64_t chunk = fact_chunk(n_tokens > 0 ? n_tokens : 1, H, d, du, rb, rq, T, with_stash, true, St::BF16,
-                                   ws_bytes);
+                                   compact, ws_bytes);
   if (chunk == 0) return TTC_LQR_EINVAL;
-  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, with_stash, true, St::BF16);
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact);
   int rc = TTC_LQR_OK;
   float* bas = reinterpret_cast<float*>(ws + L0.bas);
   float* gbas = reinterpret_cast<float*>(ws + L0.gbas);
@@ -634,7 +652,7 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
   for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H, Pc = nc * H;
-    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, with_stash, true, St::BF16);
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact);
     size_t n[10];
     io_counts(nc, H, d, du, rb, rq, n);
     auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
@@ -670,6 +688,14 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
     if (rc != TTC_LQR_OK) return rc;
     const float* v1 = with_stash ? stash + p0 * dd : nullptr;
     const float* q0 = with_stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
+    if (compact) {  // V_1 from its upper triangle, Quu_0 = R + B_0' V_1 B_0 recomputed
+      float* v1w = reinterpret_cast<float*>(ws + L.v1t);
+      float* q0w = reinterpret_cast<float*>(ws + L.q0t);
+      rc = launch_unpack_quu0(stash + p0 * (dd + d) / 2, Bx, lb, r, Pc, H, d, v1w, q0w, s);
+      if (rc != TTC_LQR_OK) return rc;
+      v1 = v1w;
+      q0 = q0w;
+    }
     int64_t nfb = 0;
     rc = backward_core(a, Bx, Qx, r, Qfx, la, lb, lq, hz, u ? u + p0 * du : nullptr, dz, nc, H, d, du, T, flags, v1,
                        q0, gA, gB, gQ, gR, gQf, glA, glB, glQ, gh, ws + L.inner, L.total - L.inner, grad_limit, status,
@@ -768,8 +794,13 @@ int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if (!ttc_lqr_supported(d, du)) return 0;
   if ((flags & TTC_LQR_FLAG_FP64_RICCATI) && d > 32) return 0;
   const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD |
-                        TTC_LQR_FLAG_RICCATI_STEPS;
+                        TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH;
   return (flags & ~known) ? 0 : 1;
+}
+
+size_t ttc_lqr_compact_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du) {
+  if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0) return 0;
+  return sizeof(float) * (size_t)n_tokens * (size_t)heads * ((size_t)d * (d + 1) / 2);
 }
 
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {
@@ -790,6 +821,7 @@ int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const f
                     float* stash, int32_t* status, void* stream) {
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  if (flags & TTC_LQR_FLAG_COMPACT_STASH) return TTC_LQR_EUNSUPPORTED;  // factored entry points only
   if (n_tokens == 0) return TTC_LQR_OK;
   if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !u)
     return TTC_LQR_EINVAL;
@@ -811,6 +843,7 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
   if (n_fallback) *n_fallback = 0;
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  if (flags & TTC_LQR_FLAG_COMPACT_STASH) return TTC_LQR_EUNSUPPORTED;  // factored entry points only
   if (n_tokens == 0) return TTC_LQR_OK;
   const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
   if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !d_u ||
@@ -831,7 +864,9 @@ size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int
                                         int32_t q_rank, int32_t T, int32_t with_stash, int32_t backward,
                                         int32_t bf16) {
   if (chunk_tokens <= 0 || !fact_args_ok(chunk_tokens, heads, d, du, b_rank, q_rank, T) || du != d) return 0;
-  return fact_layout(chunk_tokens, heads, d, du, b_rank, q_rank, T, with_stash != 0, backward != 0, bf16 != 0).total;
+  return fact_layout(chunk_tokens, heads, d, du, b_rank, q_rank, T, with_stash != 0, backward != 0, bf16 != 0,
+                     with_stash == 2)
+      .total;
 }
 
 int ttc_lqr_forward_factored(const float* A_diag, const float* coeff_B, const float* coeff_Q, const float* R_inv,

@@ -77,6 +77,9 @@ int launch_project(const float* X, int64_t M, int E, const float* basis, int R, 
 int launch_reduce(const float* coeff, int64_t M, int R, const float* X, int E, float* partial, float* out,
                   int accumulate, hipStream_t s);
 int64_t factor_slabs(int64_t M, int R, int E);
+int launch_pack_upper(const float* in, int64_t P, int D, float* out, hipStream_t s);
+int launch_unpack_quu0(const float* packed, const float* B, const float* lgB, const float* Rinv, int64_t P, int H,
+                       int D, float* v1, float* q0, hipStream_t s);
 int launch_bf16_to_f32(const uint16_t* in, int64_t n, float* out, hipStream_t s);
 int launch_f32_to_bf16(const float* in, int64_t n, uint16_t* out, hipStream_t s);
 size_t factor_partial_floats(int64_t M, int R, int E);

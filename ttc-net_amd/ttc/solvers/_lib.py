@@ -11,12 +11,13 @@ import ctypes
 import os
 
 __all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI", "FLAG_ROW_KERNEL",
-           "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS"]
+           "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS", "FLAG_COMPACT_STASH"]
 
 FLAG_FP64_RICCATI = 1  # TTC_LQR_FLAG_FP64_RICCATI
 FLAG_ROW_KERNEL = 2    # TTC_LQR_FLAG_ROW_KERNEL
 FLAG_STABLE_BWD = 4    # TTC_LQR_FLAG_STABLE_BWD
 FLAG_RICCATI_STEPS = 8  # TTC_LQR_FLAG_RICCATI_STEPS
+FLAG_COMPACT_STASH = 16  # TTC_LQR_FLAG_COMPACT_STASH
 
 LIB_NAME = "libttc_lqr.so"
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -58,6 +59,8 @@ def _load():
     L.ttc_lqr_backward.argtypes = ([f32p] * 11 + [i64, i32, i32, i32, i32, i32] + [f32p] + [f32p] * 9
                                    + [ctypes.c_void_p, sz, ctypes.c_float, f32p, ctypes.POINTER(ctypes.c_int64),
                                       ctypes.c_void_p])
+    L.ttc_lqr_compact_stash_bytes.restype = sz
+    L.ttc_lqr_compact_stash_bytes.argtypes = [i64, i32, i32, i32]
     L.ttc_lqr_factored_workspace_bytes.restype = sz
     L.ttc_lqr_factored_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32, i32, i32, i32, i32]
     L.ttc_lqr_forward_factored.restype = ctypes.c_int

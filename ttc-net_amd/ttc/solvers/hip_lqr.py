@@ -53,7 +53,8 @@ import os
 
 import torch
 
-from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS
+from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS, \
+    FLAG_COMPACT_STASH
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
            "SUPPORTED_DIMS", "last_backward_stats"]
@@ -270,6 +271,10 @@ class HipLQRFactoredFunc(torch.autograd.Function):
     entry points widen each token chunk to fp32 in the workspace, and store the gradients as
     bf16); ``u`` is computed and kept in fp32 and returned as bf16.  Any other dtype mix is
     computed from fp32 copies.
+    Stash: as :class:`HipLQRSolveFunc`; when the full stash does not fit the budget (``"auto"``)
+    or ``stash="compact"``, only the upper triangles of ``V_1`` are kept
+    (``TTC_LQR_FLAG_COMPACT_STASH``: 4x smaller at d = 64) and the backward recomputes
+    ``Quu_0`` from them instead of re-running the forward sweep.
     ``rescale`` (``"none" | "l2_norm" | "h0_norm"``, fp32 storage): the layer's rescale of
     ``u`` (``ttc_layer.py:142-147``) fused into the call -- the result is the rescaled output
     and the backward takes its gradient (``ttc_lqr_rescale`` / ``ttc_lqr_rescale_backward``).
@@ -316,14 +321,24 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         u = torch.empty(bs, nh, Dp, device=dev, dtype=torch.float32)
         status = torch.zeros(1, device=dev, dtype=torch.int32)
         policy = stash or os.environ.get("TTC_LQR_STASH", "auto")
-        assert policy in ("auto", "always", "never"), f"unknown stash policy {policy}"
+        assert policy in ("auto", "always", "compact", "never"), f"unknown stash policy {policy}"
         need_grad = any(ctx.needs_input_grad[:11])
         stash_bytes = lib.ttc_lqr_stash_bytes(bs, nh, Dp, Dp, T)
-        keep = (need_grad and bs > 0 and not stable_backward
-                and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev))))
-        st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32) if keep else None
-        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, 0, 0, int(bf16))
-        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, 0, 0, int(bf16))
+        compact_bytes = lib.ttc_lqr_compact_stash_bytes(bs, nh, Dp, Dp)
+        kind = None  # full / compact stash, or none (the backward re-runs the forward sweep)
+        if need_grad and bs > 0 and not stable_backward and policy != "never":
+            budget = _stash_budget(dev) if policy == "auto" else None
+            if policy == "always" or (policy == "auto" and stash_bytes <= budget):
+                kind = "full"
+            elif policy == "compact" or compact_bytes <= budget:
+                kind = "compact"
+        if kind == "compact":
+            flags |= FLAG_COMPACT_STASH
+        st = None if kind is None else torch.empty((stash_bytes if kind == "full" else compact_bytes) // 4,
+                                                   device=dev, dtype=torch.float32)
+        ws_stash = {None: 0, "full": 1, "compact": 2}[kind]
+        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16))
+        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16))
         ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
         fwd = lib.ttc_lqr_forward_factored_bf16 if bf16 else lib.ttc_lqr_forward_factored
         with torch.cuda.device(dev):
@@ -371,7 +386,7 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         g = [E(bs, nh, Dp), E(bs, rb), E(bs, rq), E(bs, nh, Dp), E(bs, nh, rq), E(bs, nh), E(bs, nh, Dp),
              E(bs, nh, Dp), E(bs, nh, Dp), E(rb, Dp, Dp), E(rq, Dp, Dp)]
         status = torch.zeros(1, device=dev, dtype=torch.int32)
-        with_st = 1 if st is not None else 0
+        with_st = 0 if st is None else (2 if flags & FLAG_COMPACT_STASH else 1)
         full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16))
         one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16))
         ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
