@@ -169,12 +169,14 @@ def test_wide_configs_row_kernel(cfg, n_tok, precision):
 @pytest.mark.parametrize("d,N,H,T", [(32, 3, 3, 40), (64, 2, 3, 33), (32, 1, 1, 1), (64, 1, 2, 2),
                                      (32, 2, 16, 24), (64, 2, 4, 24), (32, 1, 16, 1), (64, 1, 4, 1)])
 @pytest.mark.parametrize("stash", ["always", "never"])
-def test_wide_matrix_core_ragged(d, N, H, T, stash):
+@pytest.mark.parametrize("precision", ["fp32", "fp32-riccati"])
+def test_wide_matrix_core_ragged(d, N, H, T, stash, precision):
     """d = 32 / 64 matrix-core kernels on the reference's bench distribution: odd problem
     counts (an idle problem slot in the last d = 32 wave), head counts that select the
     one-wave (H = 1, 2, 3) or the 4-wave shared-B/Q workgroups (H = 16 at d = 32, H = 4 at
-    d = 64), and short horizons (T = 1: step 0 only)."""
-    check_case(f"mc{d}", bench_solver_inputs(N, H, d, seed=d + T), T, stash=stash, precision="fp32")
+    d = 64), and short horizons (T = 1: step 0 only).  d = 32 with an even head count runs
+    the symplectic sweep under "fp32" and blocked-Cholesky Riccati steps under "fp32-riccati"."""
+    check_case(f"mc{d}", bench_solver_inputs(N, H, d, seed=d + T), T, stash=stash, precision=precision)
 
 
 def _indefinite_wide_inputs(d, mode, H=2, seed=2):
@@ -203,10 +205,29 @@ def _indefinite_wide_inputs(d, mode, H=2, seed=2):
 @pytest.mark.parametrize("d,H", [(32, 2), (64, 2), (32, 16), (64, 4)])
 @pytest.mark.parametrize("mode", ["terminal", "mid"])
 @pytest.mark.parametrize("stash", ["always", "never"])
-def test_wide_indefinite_Quu_rescued(d, H, mode, stash):
+@pytest.mark.parametrize("precision", ["fp32", "fp32-riccati"])
+def test_wide_indefinite_Quu_rescued(d, H, mode, stash, precision):
     """H = 2: one-wave workgroups; H = 16 (d = 32) / 4 (d = 64): workgroups of 4 waves that
-    share the token's B and Q in LDS."""
-    check_case(f"indef{d}-H{H}-{mode}", _indefinite_wide_inputs(d, mode, H), 6, stash=stash, precision="fp32")
+    share the token's B and Q in LDS.  ("fp32" at d = 32 runs the symplectic sweep, which
+    has no Cholesky to break down: these inputs then check it on indefinite Q and Q_f.)"""
+    check_case(f"indef{d}-H{H}-{mode}", _indefinite_wide_inputs(d, mode, H), 6, stash=stash, precision=precision)
+
+
+@pytest.mark.parametrize("T", [64, 256])
+def test_d32_symplectic_stress(T):
+    """The d = 32 symplectic sweep on inputs with a wide conditioning spread (per-token
+    log-normal scalings of Q, Q_f and R_inv, barely discounted): u and all gradients within
+    the bound, whatever its certificate accepts or hands to the rescue pass."""
+    ins = bench_solver_inputs(6, 2, 32, seed=T)
+    g = torch.Generator().manual_seed(T + 1)
+    s = torch.exp(1.5 * torch.randn(6, generator=g))
+    A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0 = ins
+    Q = Q * s[:, None, None]
+    Qf = Qf * s[:, None, None, None].flip(0)
+    R_inv = R_inv * torch.exp(torch.randn(6, 2, 1, generator=g))
+    lgA, lgB, lgQ = lgA * 0.05, lgB * 0.05, lgQ * 0.05
+    check_case(f"sym32-T{T}", [A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0], T, grad_limit=math.inf,
+               precision="fp32")
 
 
 @pytest.mark.parametrize("cfg,T", [(5, 64), (5, 1024), ("5b", 1024)])

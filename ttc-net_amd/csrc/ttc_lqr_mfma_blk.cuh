@@ -57,27 +57,36 @@ struct MB {
   static constexpr int NT = NB * (NB + 1) / 2;      // upper tiles (I <= J)
   static constexpr int LDX = D + kPad;              // LDS row stride of D-wide rows
   static constexpr int LDG = 20;                    // LDS row stride of a 16 x 16 tile
-  // B and -sym(Q) in LDS, shared by the workgroup (d = 64 always; d = 32 with several waves)
-  static constexpr bool BQ_LDS = D == 64 || WPB > 1;
-  // workgroup-shared region: [B' (column-major B) | -sym(Q) fragments]
-  static constexpr int OFF_Q = D * LDX;
-  static constexpr int SH = BQ_LDS ? OFF_Q + NT * 256 : 0;
+  // symplectic sweep over NB x NB tiles (d = 32): its three products take B', B and -sym(Q)
+  // as A operands, read from LDS
+  static constexpr bool SYMW = SYM && D > 16;
+  // B and -sym(Q) in LDS, shared by the workgroup (d = 64 always; d = 32 with several waves
+  // or the symplectic sweep)
+  static constexpr bool BQ_LDS = D == 64 || WPB > 1 || SYMW;
+  // workgroup-shared region: [B' (column-major B) | -sym(Q) fragments], or for SYMW
+  // [B' | B (row-major) | -sym(Q) (row-major)]
+  static constexpr int OFF_BR = D * LDX;
+  static constexpr int OFF_Q = SYMW ? 2 * D * LDX : D * LDX;
+  static constexpr int SH = !BQ_LDS ? 0 : (SYMW ? 3 * D * LDX : OFF_Q + NT * 256);
   // per-problem region: transpose buffer (CH block-rows per round), also the 16x16 tile
   // buffer and the step-0 row buffer
   static constexpr int CH = BQ_LDS ? NB / 2 : NB;
   static constexpr int XROWS = CH * 16;
   static constexpr int LDS2 = 2 * D + 4;            // symplectic: rows of [Y1 | -Y2]
   static constexpr int REG0 = XROWS * LDX;
-  static constexpr int REG = (SYM && D * LDS2 > REG0) ? D * LDS2 : REG0;
-  static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4, "per-problem LDS region");
-  static_assert(!SYM || (D == 16 && !BQ_LDS), "the symplectic sweep is built for d = 16");
+  // SYMW stages 16 rows of D at a time through it (the final solve's input and output)
+  static constexpr int REG = (SYM && !SYMW && D * LDS2 > REG0) ? D * LDS2
+                                                             : ((SYMW && 16 * LDX > REG0) ? 16 * LDX : REG0);
+  static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4 && (!SYMW || REG >= 3 * D + 4),
+                "per-problem LDS region");
+  static_assert(!SYM || (D == 16 && !BQ_LDS) || (D == 32 && BQ_LDS), "symplectic sweep: d = 16, or d = 32 from LDS");
   // per-problem vectors: alpha, q (step 0: alpha*h0), beta (step 0: rhs), -beta^2 R^{-1}, 1/alpha
   static constexpr int VEC = 5 * D;
   static constexpr int PER_WAVE = PPW * (REG + VEC);
   static constexpr int THREADS = 64 * WPB;
   // two waves per SIMD, except with four problems per wave that keep B and Q in registers;
   // the symplectic sweep's small state leaves room for four
-  static constexpr int MINW = SYM ? TTC_SYM_WAVES : (PPW == 4 && !BQ_LDS) ? 1 : 2;
+  static constexpr int MINW = SYMW ? 2 : SYM ? TTC_SYM_WAVES : (PPW == 4 && !BQ_LDS) ? 1 : 2;
   static constexpr int MAXW = MINW;
   static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)SH + (size_t)WPB * PER_WAVE);
 };
@@ -161,7 +170,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   float rr[PPW][NB];  // 1 / R_inv[16I + c]
   // symplectic sweep: B in the transposed operand layout, Bt[q][I][K][s] = B[16I + c][16K + 4g + s],
   // and Y1' (the sweep keeps Y-hat = Y' in the C layout; Y2' is -N)
-  float Bt[G::SYM ? PPW : 1][NB][NB][4];
+  float Bt[(G::SYM && !G::SYMW) ? PPW : 1][NB][NB][4];
   v4f Y1[G::SYM ? PPW : 1][NB][NB];
   if constexpr (BQL) {
     // the workgroup's token: B column-major, -sym(Q) as per-lane C-layout fragments
@@ -171,8 +180,12 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     for (int e = threadIdx.x; e < D * D; e += G::THREADS) {
       const int i = e / D, j = e % D;
       shb[j * LDX + i] = bq[e];
+      if constexpr (G::SYMW) {
+        sm[G::OFF_BR + i * LDX + j] = bq[e];
+        shq[i * LDX + j] = -0.5f * (qq[e] + qq[j * D + i]);
+      }
     }
-    for (int e = threadIdx.x; e < NT * 64; e += G::THREADS) {
+    for (int e = threadIdx.x; e < (G::SYMW ? 0 : NT * 64); e += G::THREADS) {
       const int tile = e >> 6, ln = e & 63;
       int I = 0, rem = tile;
       while (rem >= NB - I) {
@@ -209,7 +222,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
             if (I <= J) Qn[q][utile<NB>(I, J)][r] = -0.5f * (qq[i * D + j] + qq[j * D + i]);
           }
           if constexpr (G::SYM) {
-            Bt[q][I][J][r] = bq[(16 * I + c) * D + 16 * J + 4 * g + r];
+            if constexpr (!G::SYMW) Bt[q][I][J][r] = bq[(16 * I + c) * D + 16 * J + 4 * g + r];
             Y1[q][I][J][r] = (i == j) ? 1.0f : 0.0f;
           }
         }
@@ -450,7 +463,6 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   // Y-hat (rows of Y, which leave Y1^{-1} Y2 unchanged) are rescaled by powers of 2.
   auto sym_step = [&](const int t) {
     if constexpr (G::SYM) {
-    static_assert(NB == 1, "symplectic sweep: one tile per matrix");
     const float tp1 = (float)(t + 1);
 #pragma unroll
     for (int pa = 0; pa < NPASS; ++pa) {
@@ -464,6 +476,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     }
     wave_sync();
     const bool renorm = (T - 1 - t) % TTC_SYM_RENORM == TTC_SYM_RENORM - 1;
+    if constexpr (!G::SYMW) {
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
       const float* v = vecs + q * G::VEC;
@@ -506,6 +519,95 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
         }
       }
     }
+    } else {
+    // NB x NB tiles; A operands from the workgroup's LDS: tile (I, K) of B' is
+    // B[16K + 4g + s][16I + c] (shb, column-major B), of B is B[16I + c][16K + 4g + s] and of
+    // -sym(Q) is -Q[16I + c][16K + 4g + s] (row-major copies)
+    const float* shbr = sm + G::OFF_BR;
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      const float* v = vecs + q * G::VEC;
+      v4f M[NB][NB];
+#pragma unroll
+      for (int I = 0; I < NB; ++I)
+#pragma unroll
+        for (int J = 0; J < NB; ++J) M[I][J] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int I = 0; I < NB; ++I)
+#pragma unroll
+        for (int K = 0; K < NB; ++K) {
+          const v4f a = ld4(shb + (16 * I + c) * LDX + 16 * K + 4 * g);
+#pragma unroll
+          for (int J = 0; J < NB; ++J)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) M[I][J] = mfma16x16x4(a[s], NV[q][K][J][s], M[I][J]);
+        }
+#pragma unroll
+      for (int I = 0; I < NB; ++I) {
+        const v4f nf = ld4(v + 3 * D + 16 * I + 4 * g);
+#pragma unroll
+        for (int J = 0; J < NB; ++J)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) M[I][J][r] *= nf[r];
+      }
+#pragma unroll
+      for (int I = 0; I < NB; ++I) {
+#pragma unroll
+        for (int K = 0; K < NB; ++K) {
+          const v4f a = ld4(shbr + (16 * I + c) * LDX + 16 * K + 4 * g);
+#pragma unroll
+          for (int J = 0; J < NB; ++J)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) Y1[q][I][J] = mfma16x16x4(a[s], M[K][J][s], Y1[q][I][J]);
+        }
+        const v4f ia = ld4(v + 4 * D + 16 * I + 4 * g);
+        const v4f al = ld4(v + 16 * I + 4 * g);
+#pragma unroll
+        for (int J = 0; J < NB; ++J)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            Y1[q][I][J][r] *= ia[r];
+            NV[q][I][J][r] *= al[r];
+          }
+      }
+#pragma unroll
+      for (int I = 0; I < NB; ++I) {
+        const float qc = v[D + 16 * I + c];
+#pragma unroll
+        for (int K = 0; K < NB; ++K) {
+          const v4f qa = ld4(shq + (16 * I + c) * LDX + 16 * K + 4 * g);
+          const v4f qrw = ld4(v + D + 16 * K + 4 * g);
+          float op[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) op[s] = qa[s] * (qc * qrw[s]);
+#pragma unroll
+          for (int J = 0; J < NB; ++J)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) NV[q][I][J] = mfma16x16x4(op[s], Y1[q][K][J][s], NV[q][I][J]);
+        }
+      }
+      if (renorm) {  // per column 16J + c of Y-hat
+#pragma unroll
+        for (int J = 0; J < NB; ++J) {
+          float m = 0.f;
+#pragma unroll
+          for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(fabsf(Y1[q][I][J][r]), fabsf(NV[q][I][J][r])));
+          m = fmaxf(m, __shfl_xor(m, 16, 64));
+          m = fmaxf(m, __shfl_xor(m, 32, 64));
+          const int e = 1 - __builtin_amdgcn_frexp_expf(m);
+#pragma unroll
+          for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              Y1[q][I][J][r] = __builtin_amdgcn_ldexpf(Y1[q][I][J][r], e);
+              NV[q][I][J][r] = __builtin_amdgcn_ldexpf(NV[q][I][J][r], e);
+            }
+        }
+      }
+    }
+    }
     wave_sync();
     }
   };
@@ -516,6 +618,96 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   auto sym_finish = [&]() -> unsigned {
     if constexpr (!G::SYM) {
       return ~0u;
+    } else if constexpr (G::SYMW) {
+    // NB x NB tiles: rows go through each problem's region 16 at a time (Y1, then -Y2, then
+    // the solution), pass by pass (RPP problems of D lanes each)
+    unsigned bits = 0u;
+#pragma unroll
+    for (int pa = 0; pa < NPASS; ++pa) {
+      float aug[3 * D];
+#pragma unroll
+      for (int mtx = 0; mtx < 2; ++mtx)
+#pragma unroll
+        for (int h = 0; h < NB; ++h) {
+          wave_sync();  // the region's previous rows have been read
+#pragma unroll
+          for (int k = 0; k < RPP; ++k) {
+            const int q = pa * RPP + k;
+            float* buf = region(q);
+            // row 16h + c of Y1 (of -Y2) = column 16h + c of Y1' (of -Y2' = N)
+#pragma unroll
+            for (int I = 0; I < NB; ++I) st4(buf + c * LDX + 16 * I + 4 * g, mtx == 0 ? Y1[q][I][h] : NV[q][I][h]);
+          }
+          wave_sync();
+          if (li >= 16 * h && li < 16 * h + 16) {
+            float row[D];
+            ld_row<D>(region(qr[pa]) + (li - 16 * h) * LDX, row);
+#pragma unroll
+            for (int k = 0; k < D; ++k) aug[mtx * D + k] = row[k];
+          }
+        }
+#pragma unroll
+      for (int k = 0; k < D; ++k) aug[2 * D + k] = (k == li) ? 1.0f : 0.0f;
+      float rs = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) rs += fabsf(aug[k]);
+      const float n1 = dgroup_max<D>(rs);  // ||Y1||_inf
+      wave_sync();  // every row read before the pivot-row buffer (aliasing them) is written
+      float* buf = region(qr[pa]);
+      float piv;
+      int pos;
+      gauss_jordan<D, 3 * D>(aug, li, buf, piv, pos);
+      const float ip = 1.0f / piv;
+      float ri = 0.f, pn[D];
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        ri += fabsf(aug[2 * D + k]);
+        pn[k] = aug[D + k] * ip;  // row pos of -V_1
+      }
+      const float n2 = dgroup_max<D>(ri * fabsf(ip));  // ||Y1^{-1}||_inf
+      float da = 0.f, mx = 0.f;
+#pragma unroll
+      for (int k = 0; k < D; ++k) mx = fmaxf(mx, fabsf(pn[k]));
+#pragma unroll
+      for (int k = 0; k < RPP; ++k) {
+        const int q = pa * RPP + k;
+#pragma unroll
+        for (int I = 0; I < NB; ++I)
+#pragma unroll
+          for (int J = 0; J < NB; ++J) NV[q][I][J] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+      // rows 16h..16h+15 of -V_1: the asymmetry against my row, and their halves of
+      // N = sym(-V_1) in the C layout
+#pragma unroll
+      for (int h = 0; h < NB; ++h) {
+        wave_sync();
+        if (pos >= 16 * h && pos < 16 * h + 16) st_row<D>(buf + (pos - 16 * h) * LDX, pn);
+        wave_sync();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) da = fmaxf(da, fabsf(pn[16 * h + kk] - buf[kk * LDX + pos]));
+#pragma unroll
+        for (int k = 0; k < RPP; ++k) {
+          const int q = pa * RPP + k;
+          const float* b = region(q);
+#pragma unroll
+          for (int J = 0; J < NB; ++J)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) NV[q][h][J][r] += 0.5f * b[(4 * g + r) * LDX + 16 * J + c];
+#pragma unroll
+          for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) NV[q][I][h][r] += 0.5f * b[c * LDX + 16 * I + 4 * g + r];
+        }
+      }
+      da = dgroup_max<D>(da);
+      mx = dgroup_max<D>(mx);
+      const bool ok = (n1 * n2 <= kSymCondMax) && (da <= kSymAsymMax * mx);  // false on NaN
+      const unsigned long long bal = __ballot(ok);
+#pragma unroll
+      for (int k = 0; k < RPP; ++k) bits |= (unsigned)((bal >> (k * D)) & 1ull) << (pa * RPP + k);
+    }
+    wave_sync();
+    return bits;
     } else {
     constexpr int L2 = G::LDS2;
 #pragma unroll
