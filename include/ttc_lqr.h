@@ -66,12 +66,12 @@ extern "C" {
  * (feedback gains recomputed and stored per step, closed-loop costates) instead of the
  * certified Hamiltonian rollout.  Same results to fp32 rounding; slower. */
 #define TTC_LQR_FLAG_STABLE_BWD 4
-/* TTC_LQR_FLAG_RICCATI_STEPS makes the d = 16 and d = 32 fp32 forward take a Riccati step
- * (with its Cholesky factorisation) at every horizon step on the matrix cores, instead of
- * the default symplectic sweep (three matrix products per step, one pivoted solve at the
- * end, a conditioning certificate per problem and a row-layout recompute of the problems
- * that miss it; at d = 32 for even head counts).  Same results to fp32 rounding.  d = 64
- * always takes Riccati steps. */
+/* TTC_LQR_FLAG_RICCATI_STEPS makes the fp32 forward take a Riccati step (with its Cholesky
+ * factorisation) at every horizon step on the matrix cores, instead of the default
+ * symplectic sweep (three matrix products per step, one pivoted solve at the end, a
+ * conditioning certificate per problem and a row-layout recompute of the problems that
+ * miss it; at d = 32 for even head counts, at d = 64 for head counts that are multiples of
+ * 4, otherwise Riccati steps anyway).  Same results to fp32 rounding. */
 #define TTC_LQR_FLAG_RICCATI_STEPS 8
 /* TTC_LQR_FLAG_COMPACT_STASH (factored entry points only): the stash holds only the upper
  * triangle of each problem's V_1 (ttc_lqr_compact_stash_bytes: d(d+1)/2 floats per problem,

@@ -158,7 +158,8 @@ def test_config4_layer_slice(precision):
     check_case("cfg4", layer_solver_inputs(4, x), c["T"], precision=precision)
 
 
-@pytest.mark.parametrize("cfg,n_tok,precision", [(3, 3, "fp32-row"), (4, 2, "fp32-row")])
+@pytest.mark.parametrize("cfg,n_tok,precision", [(3, 3, "fp32-row"), (4, 2, "fp32-row"), (3, 2, "fp32-riccati"),
+                                              (4, 1, "fp32-riccati")])
 def test_wide_configs_row_kernel(cfg, n_tok, precision):
     """d = 64 / 32 through the row-layout kernel: an independent cross-check of the
     matrix-core kernel that the default precision selects."""
@@ -213,20 +214,20 @@ def test_wide_indefinite_Quu_rescued(d, H, mode, stash, precision):
     check_case(f"indef{d}-H{H}-{mode}", _indefinite_wide_inputs(d, mode, H), 6, stash=stash, precision=precision)
 
 
-@pytest.mark.parametrize("T", [64, 256])
-def test_d32_symplectic_stress(T):
-    """The d = 32 symplectic sweep on inputs with a wide conditioning spread (per-token
+@pytest.mark.parametrize("d,H,T", [(32, 2, 64), (32, 2, 256), (64, 4, 64), (64, 4, 128)])
+def test_wide_symplectic_stress(d, H, T):
+    """The d = 32 / 64 symplectic sweeps on inputs with a wide conditioning spread (per-token
     log-normal scalings of Q, Q_f and R_inv, barely discounted): u and all gradients within
-    the bound, whatever its certificate accepts or hands to the rescue pass."""
-    ins = bench_solver_inputs(6, 2, 32, seed=T)
+    the bound, whatever their certificate accepts or hands to the rescue pass."""
+    ins = bench_solver_inputs(6, H, d, seed=T + d)
     g = torch.Generator().manual_seed(T + 1)
     s = torch.exp(1.5 * torch.randn(6, generator=g))
     A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0 = ins
     Q = Q * s[:, None, None]
     Qf = Qf * s[:, None, None, None].flip(0)
-    R_inv = R_inv * torch.exp(torch.randn(6, 2, 1, generator=g))
+    R_inv = R_inv * torch.exp(torch.randn(6, H, 1, generator=g))
     lgA, lgB, lgQ = lgA * 0.05, lgB * 0.05, lgQ * 0.05
-    check_case(f"sym32-T{T}", [A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0], T, grad_limit=math.inf,
+    check_case(f"sym{d}-T{T}", [A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0], T, grad_limit=math.inf,
                precision="fp32")
 
 

@@ -6,10 +6,12 @@ namespace ttc {
 int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
-  // fp32 sweeps without per-step gains run on the matrix-core kernel unless the row-layout
-  // kernel is asked for
+  // fp32 sweeps without per-step gains run on the matrix cores unless the row-layout kernel
+  // is asked for: the certified symplectic sweep by default (head counts that are multiples
+  // of 4), per-step Riccati when asked for
   if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL)) && sm != STASH_GAINS)
-    return launch_fwd_d64_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
+    return launch_fwd_d64_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s,
+                               !(flags & TTC_LQR_FLAG_RICCATI_STEPS));
   return launch_fwd<64, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);
 }
 

@@ -19,7 +19,8 @@ int launch_fwd_d32_mfma(const float* A, const float* B, const float* Q, const fl
                         bool sym);
 int launch_fwd_d64_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s);
+                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
+                        bool sym);
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);

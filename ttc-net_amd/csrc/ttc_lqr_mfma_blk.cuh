@@ -70,16 +70,20 @@ struct MB {
   static constexpr int SH = !BQ_LDS ? 0 : (SYMW ? 3 * D * LDX : OFF_Q + NT * 256);
   // per-problem region: transpose buffer (CH block-rows per round), also the 16x16 tile
   // buffer and the step-0 row buffer
-  static constexpr int CH = BQ_LDS ? NB / 2 : NB;
+  static constexpr int CH = SYMW ? 1 : (BQ_LDS ? NB / 2 : NB);
   static constexpr int XROWS = CH * 16;
   static constexpr int LDS2 = 2 * D + 4;            // symplectic: rows of [Y1 | -Y2]
   static constexpr int REG0 = XROWS * LDX;
   // SYMW stages 16 rows of D at a time through it (the final solve's input and output)
   static constexpr int REG = (SYM && !SYMW && D * LDS2 > REG0) ? D * LDS2
                                                              : ((SYMW && 16 * LDX > REG0) ? 16 * LDX : REG0);
-  static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4 && (!SYMW || REG >= 3 * D + 4),
+  // the final solve of the symplectic sweep works on [Y1 | -Y2 | I] (Y1^{-1} for the condition
+  // number) up to d = 32; at d = 64 on [Y1 | -Y2], with the pivots' spread as the estimate
+  static constexpr bool SYM_INV = D < 64;
+  static constexpr int AUGW = SYM_INV ? 3 * D : 2 * D;
+  static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4 && (!SYMW || REG >= AUGW + 4),
                 "per-problem LDS region");
-  static_assert(!SYM || (D == 16 && !BQ_LDS) || (D == 32 && BQ_LDS), "symplectic sweep: d = 16, or d = 32 from LDS");
+  static_assert(!SYM || (D == 16 && !BQ_LDS) || (D >= 32 && BQ_LDS), "symplectic sweep: d = 16, or d = 32 / 64 from LDS");
   // per-problem vectors: alpha, q (step 0: alpha*h0), beta (step 0: rhs), -beta^2 R^{-1}, 1/alpha
   static constexpr int VEC = 5 * D;
   static constexpr int PER_WAVE = PPW * (REG + VEC);
@@ -622,9 +626,10 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     // NB x NB tiles: rows go through each problem's region 16 at a time (Y1, then -Y2, then
     // the solution), pass by pass (RPP problems of D lanes each)
     unsigned bits = 0u;
+    constexpr int W = G::AUGW;
 #pragma unroll
     for (int pa = 0; pa < NPASS; ++pa) {
-      float aug[3 * D];
+      float aug[W];
 #pragma unroll
       for (int mtx = 0; mtx < 2; ++mtx)
 #pragma unroll
@@ -646,8 +651,10 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
             for (int k = 0; k < D; ++k) aug[mtx * D + k] = row[k];
           }
         }
+      if constexpr (G::SYM_INV) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) aug[2 * D + k] = (k == li) ? 1.0f : 0.0f;
+        for (int k = 0; k < D; ++k) aug[2 * D + k] = (k == li) ? 1.0f : 0.0f;
+      }
       float rs = 0.f;
 #pragma unroll
       for (int k = 0; k < D; ++k) rs += fabsf(aug[k]);
@@ -656,15 +663,22 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       float* buf = region(qr[pa]);
       float piv;
       int pos;
-      gauss_jordan<D, 3 * D>(aug, li, buf, piv, pos);
+      gauss_jordan<D, W>(aug, li, buf, piv, pos);
       const float ip = 1.0f / piv;
-      float ri = 0.f, pn[D];
+      float pn[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        ri += fabsf(aug[2 * D + k]);
-        pn[k] = aug[D + k] * ip;  // row pos of -V_1
+      for (int k = 0; k < D; ++k) pn[k] = aug[D + k] * ip;  // row pos of -V_1
+      float n2;
+      if constexpr (G::SYM_INV) {
+        float ri = 0.f;
+#pragma unroll
+        for (int k = 0; k < D; ++k) ri += fabsf(aug[2 * D + k]);
+        n2 = dgroup_max<D>(ri * fabsf(ip));  // ||Y1^{-1}||_inf
+      } else {
+        // spread of the pivots (the diagonal of U in Y1 = L U): max|u_kk| / min|u_kk| <= cond(Y1),
+        // with ||Y1||_inf standing in for max|u_kk| (at most n times larger)
+        n2 = dgroup_max<D>(fabsf(ip));
       }
-      const float n2 = dgroup_max<D>(ri * fabsf(ip));  // ||Y1^{-1}||_inf
       float da = 0.f, mx = 0.f;
 #pragma unroll
       for (int k = 0; k < D; ++k) mx = fmaxf(mx, fabsf(pn[k]));
