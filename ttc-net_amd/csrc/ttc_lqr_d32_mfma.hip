@@ -5,15 +5,15 @@
 
 namespace ttc {
 
-template <int SM, bool WU, int PPW, int WPB, bool SYM>
+template <int SM, bool WU, int PPW, int WPB, bool SYM, bool RESC = false>
 static void launch_b32_w(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                          const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                          float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
   using G = MB<32, PPW, WPB, SYM>;
   constexpr int PPB = PPW * WPB;
   const dim3 grid((unsigned)((P + PPB - 1) / PPB)), block(G::THREADS);
-  hipLaunchKernelGGL((lqr_fwd_blk_kernel<32, PPW, WPB, SM, WU, SYM>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf,
-                     lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+  hipLaunchKernelGGL((lqr_fwd_blk_kernel<32, PPW, WPB, SM, WU, SYM, RESC>), grid, block, G::LDS_BYTES, s, A, B, Q, R,
+                     Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
 }
 
 // The symplectic sweep runs one-wave workgroups of 2 problems that share B and Q in LDS (an
@@ -25,9 +25,15 @@ template <int SM, bool WU>
 static void launch_b32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool sym) {
-  if (sym && H % 2 == 0)
+  if (sym && H % 2 == 0) {
     launch_b32_w<SM, WU, 2, 1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
-  else if (H % 16 == 0)
+    // problems the certificate rejected: Riccati steps on the matrix cores first (only the
+    // workgroups that hold one run), the row layout for what still breaks down
+    if (H % 16 == 0)
+      launch_b32_w<SM, WU, 4, 4, false, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    else
+      launch_b32_w<SM, WU, 2, 1, false, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+  } else if (H % 16 == 0)
     launch_b32_w<SM, WU, 4, 4, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
   else
     launch_b32_w<SM, WU, 2, 1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);

@@ -5,14 +5,14 @@
 
 namespace ttc {
 
-template <int SM, bool WU, int WPB, bool SYM>
+template <int SM, bool WU, int WPB, bool SYM, bool RESC = false>
 static void launch_b64_w(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                          const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                          float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
   using G = MB<64, 1, WPB, SYM>;
   const dim3 grid((unsigned)((P + WPB - 1) / WPB)), block(G::THREADS);
-  hipLaunchKernelGGL((lqr_fwd_blk_kernel<64, 1, WPB, SM, WU, SYM>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf,
-                     lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+  hipLaunchKernelGGL((lqr_fwd_blk_kernel<64, 1, WPB, SM, WU, SYM, RESC>), grid, block, G::LDS_BYTES, s, A, B, Q, R,
+                     Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
 }
 
 // Four-wave workgroups share one token's B and Q in LDS: every aligned group of four
@@ -22,9 +22,12 @@ template <int SM, bool WU>
 static void launch_b64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool sym) {
-  if (sym && H % 4 == 0)
+  if (sym && H % 4 == 0) {
     launch_b64_w<SM, WU, 4, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
-  else if (H % 4 == 0)
+    // problems the certificate rejected: Riccati steps on the matrix cores first (only the
+    // workgroups that hold one run), the row layout for what still breaks down
+    launch_b64_w<SM, WU, 4, false, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+  } else if (H % 4 == 0)
     launch_b64_w<SM, WU, 4, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
   else
     launch_b64_w<SM, WU, 1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);

@@ -119,7 +119,9 @@ __host__ __device__ constexpr int utile(int I, int J) {
   return I * NB - I * (I - 1) / 2 + (J - I);
 }
 
-template <int D, int PPW_, int WPB_, int SM, bool WRITE_U, bool SYM_ = false>
+// RESC_: rescue pass after the symplectic sweep (Riccati steps only): a workgroup runs only when
+// one of its problems carries the NaN marker, and stores the marked problems only.
+template <int D, int PPW_, int WPB_, int SM, bool WRITE_U, bool SYM_ = false, bool RESC_ = false>
 __global__ __launch_bounds__(64 * WPB_) __attribute__((amdgpu_waves_per_eu(MB<D, PPW_, WPB_, SYM_>::MINW,
                                                                            MB<D, PPW_, WPB_, SYM_>::MAXW))) void
 lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
@@ -144,6 +146,19 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   int64_t pid[PPW];
 #pragma unroll
   for (int q = 0; q < PPW; ++q) pid[q] = (pbase + q < P) ? (pbase + q) : (P - 1);  // idle: recompute, never store
+  static_assert(!(RESC_ && SYM_), "the rescue pass takes Riccati steps");
+  unsigned marked = ~0u;  // the problems this launch may store
+  if constexpr (RESC_) {
+    // the same decision in every wave of the workgroup, before its only barrier
+    if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
+    bool mk = false;
+    if (lane < PPW && pbase + lane < P) {
+      const float m = WRITE_U ? u_out[(pbase + lane) * D] : q0stash[(pbase + lane) * D * D];
+      mk = m != m;  // NaN marker of the sweep before
+    }
+    marked = (unsigned)(__ballot(mk) & ((1ull << PPW) - 1ull));
+    if (__syncthreads_or(marked != 0u) == 0) return;
+  }
   float* shb = sm;             // shared B' (d = 64)
   float* shq = sm + G::OFF_Q;  // shared -sym(Q) fragments (d = 64)
   float* wbase = sm + G::SH + wv * G::PER_WAVE;
@@ -783,7 +798,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     }
   };
 
-  unsigned okbits = ~0u;  // problems whose sweep is accepted (the symplectic certificate)
+  unsigned okbits = marked;  // problems whose results are stored (the symplectic certificate; rescue: marked)
 
   // Step 0: stash V_1, form W_0 and Quu_0, u0 = -Quu_0^{-1} W_0' (alpha_0 * h0).
   auto step0 = [&]() {
@@ -893,7 +908,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     else okbits = 0u;
   }
   // problems whose sweep broke down or was not certified: mark them for lqr_rescue_kernel
-  if (lane < PPW && pbase + lane < P && !((okbits >> lane) & 1u)) {
+  if (lane < PPW && pbase + lane < P && ((marked >> lane) & 1u) && !((okbits >> lane) & 1u)) {
     const float nan = __builtin_nanf("");
     if (WRITE_U) u_out[(pbase + lane) * D] = nan;
     else q0stash[(pbase + lane) * D * D] = nan;
