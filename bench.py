@@ -345,6 +345,7 @@ def main():
         extras.append({"config": f"cfg{cfg}", "x": xs_e, "d": de, "T": Te, "heads": He, "problems": Pe,
                        "fwd_ms": re_["fwd_ms"], "fwd_solves_per_s": Pe / (re_["fwd_ms"] * 1e-3),
                        "fwd_bwd_ms": re_["step_ms"], "fwd_bwd_solves_per_s": Pe / (re_["step_ms"] * 1e-3),
+                       "bwd_fallback_problems": re_["bwd_fallback_problems"],
                        "roofline_frac": ach / PEAK_FP32_MFMA, "achieved_tflops": ach / 1e12,
                        "traffic": traffic_from_profiles(f"lqr_fwd_cfg{cfg}")})
         del ins_e, du_e

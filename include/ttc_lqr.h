@@ -58,9 +58,10 @@ extern "C" {
  * for long, barely-discounted horizons (e.g. T = 1024 with log-normal inputs),
  * where fp32 rounding of V ~ 1e17 corrupts the gains. */
 #define TTC_LQR_FLAG_FP64_RICCATI 1
-/* TTC_LQR_FLAG_ROW_KERNEL selects the row-layout (vector-ALU only) fp32 kernel instead of
- * the matrix-core kernels.  Results agree to fp32 rounding; it serves as an independent
- * cross-check and as a fallback. */
+/* TTC_LQR_FLAG_ROW_KERNEL selects the row-layout (vector-ALU only) fp32 kernels -- the
+ * forward sweep and the backward's Hamiltonian rollout, one problem per d lanes -- instead
+ * of the matrix-core kernels (which roll the backward over head groups of 8 when H % 8 == 0).
+ * Results agree to fp32 rounding; it serves as an independent cross-check and as a fallback. */
 #define TTC_LQR_FLAG_ROW_KERNEL 2
 /* TTC_LQR_FLAG_STABLE_BWD makes ttc_lqr_backward take the stable path for every problem
  * (feedback gains recomputed and stored per step, closed-loop costates) instead of the

@@ -145,6 +145,35 @@ def test_d16_head_groups_with_rejected_groups():
         assert _relerr(fast[k], ref[k]) <= TOL, k
 
 
+@pytest.mark.parametrize("d", [32, 64])
+@pytest.mark.parametrize("N,H,T", [(3, 8, 40), (2, 16, 33), (1, 24, 2), (2, 8, 1)])
+def test_wide_head_groups_matrix_core_backward(d, N, H, T):
+    """The d = 32 / 64 backward over head groups of 8 on the matrix cores (d / 16 waves per
+    group): one group per token (H = 8, head sums written directly), several (H = 16, 24),
+    T = 1 and 2 included."""
+    ins = bench_solver_inputs(N, H, d, seed=d + N + H + T)
+    out = check_case(f"groups{d} N={N} H={H}", ins, T)
+    assert out["_fallback"] % 8 == 0
+
+
+@pytest.mark.parametrize("d,H,T", [(32, 16, 128), (64, 8, 96)])
+def test_wide_head_groups_on_stress_inputs(d, H, T):
+    """Head groups on the stress inputs of the symplectic tests (log-normal scalings of Q,
+    Q_f and R_inv, barely discounted): whatever groups the certificate rejects take the
+    stable path as whole groups, and every tensor stays within the bound."""
+    ins = bench_solver_inputs(4, H, d, seed=T + d + 1)
+    g = torch.Generator().manual_seed(T + 2)
+    s = torch.exp(1.5 * torch.randn(4, generator=g))
+    A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0 = ins
+    Q = Q * s[:, None, None]
+    Qf = Qf * s[:, None, None, None].flip(0)
+    R_inv = R_inv * torch.exp(torch.randn(4, H, 1, generator=g))
+    lgA, lgB, lgQ = lgA * 0.05, lgB * 0.05, lgQ * 0.05
+    out = check_case(f"groups{d}-stress-T{T}", [A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0], T,
+                     grad_limit=math.inf)
+    assert out["_fallback"] % 8 == 0
+
+
 def test_config3_layer_slice():
     c = CONFIGS[3]
     x = make_x(3, n_tokens=2, seed=2)

@@ -340,14 +340,15 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
     hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
-    if (d == 16 && H % 8 == 0) {
+    if (H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL)) {
       // head groups of 8 on the matrix cores: grad_B / grad_Q summed inside the kernel
       // (straight into the outputs when a group is a token, H == 8)
       const bool direct = H == 8;
       float* gBg = direct ? grad_B + n0 * dd : gBp;
       float* gQg = direct ? grad_Q + n0 * dd : gQp;
-      rc = launch_ham16_mfma(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB,
-                             glQ, gh, gBg, gQg, grad_limit, list, cnt, status, s);
+      auto* launch = d == 16 ? launch_ham16_mfma : (d == 32 ? launch_ham32_mfma : launch_ham64_mfma);
+      rc = launch(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBg,
+                  gQg, grad_limit, list, cnt, status, s);
       if (rc != TTC_LQR_OK) return rc;
       int32_t nfail = 0;
       if (hipMemcpyAsync(&nfail, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;

@@ -72,6 +72,19 @@ int launch_ham16_mfma(const float* A, const float* B, const float* Q, const floa
                       float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0,
                       float* gBg, float* gQg, float limit, int32_t* fail_list, int32_t* fail_count,
                       int32_t* status, hipStream_t s);
+// the same for d = 32 / 64 (d / 16 waves per head group; ttc_lqr_hamw.cuh)
+int launch_ham32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                      const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
+                      const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
+                      float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0,
+                      float* gBg, float* gQg, float limit, int32_t* fail_list, int32_t* fail_count,
+                      int32_t* status, hipStream_t s);
+int launch_ham64_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                      const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
+                      const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
+                      float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0,
+                      float* gBg, float* gQg, float limit, int32_t* fail_list, int32_t* fail_count,
+                      int32_t* status, hipStream_t s);
 // Low-rank front-end (ttc_lqr_factored.hip): expansion of coefficient x basis sums and
 // their chain rule.  Rows of E = d * du floats; ranks R <= 64; E in {256, 1024, 4096}.
 int launch_expand(const float* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s);

@@ -28,12 +28,12 @@ Differences from the reference, by design:
   barely discounted horizons the value matrix reaches ~1e17 and fp32 rounding
   corrupts the gains (the reference's own fp32 solvers lose the gradients
   entirely there).  Everything else (rollouts, costates, gradients) is fp32.
-  The fp32 sweep runs on the matrix cores (MFMA): for d = 16 as the symplectic
-  sweep (three matrix products per step, one certified solve at the end; the
-  problems the certificate rejects are recomputed by the row-layout kernel), for
-  d = 32 / 64 as blocked-Cholesky Riccati steps.  ``"fp32-riccati"`` selects per-step
-  Riccati on the matrix cores for d = 16 too, ``"fp32-row"`` the vector-ALU row-layout
-  kernel.
+  The fp32 sweep runs on the matrix cores (MFMA) as the symplectic sweep (three
+  matrix products per step, one certified solve at the end; the problems the
+  certificate rejects are recomputed with Riccati steps, then by the row-layout
+  kernel).  ``"fp32-riccati"`` selects per-step Riccati on the matrix cores,
+  ``"fp32-row"`` the vector-ALU row-layout kernels (forward sweep and backward
+  rollout).
 
 Environment knobs:
 ``TTC_LQR_STASH`` = ``auto`` (default: keep the stash from the forward when it fits
@@ -104,10 +104,10 @@ def _pad_inputs(ins, d, du, Dp):
 def riccati_flags(precision: str, T: int, Dp: int) -> int:
     """Kernel flags for the requested Riccati arithmetic (fp64 kernels exist for d <= 32).
 
-    ``"fp32"``: the fastest fp32 kernel (matrix cores; symplectic sweep for d = 16);
-    ``"fp32-riccati"``: per-step Riccati on the matrix cores (d = 16; the same kernels
-    as ``"fp32"`` for d = 32 / 64); ``"fp32-row"``: the row-layout fp32 kernel (vector
-    ALU only) -- an independent cross-check of the matrix-core kernels; ``"fp64"``:
+    ``"fp32"``: the fastest fp32 kernels (matrix cores; symplectic sweep);
+    ``"fp32-riccati"``: per-step Riccati on the matrix cores; ``"fp32-row"``: the
+    row-layout fp32 kernels (vector ALU only, forward and the backward's rollout) -- an
+    independent cross-check of the matrix-core kernels; ``"fp64"``:
     fp64 sweep; ``"auto"``: fp64 for T >= FP64_HORIZON where available, else fp32.
     """
     assert precision in ("fp32", "fp32-riccati", "fp32-row", "fp64", "auto"), f"unknown precision {precision}"
