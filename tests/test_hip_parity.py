@@ -174,6 +174,28 @@ def test_wide_head_groups_on_stress_inputs(d, H, T):
     assert out["_fallback"] % 8 == 0
 
 
+@pytest.mark.parametrize("d,T", [(32, 128), (64, 96)])
+def test_wide_head_groups_with_rejected_groups(d, T):
+    """Stress inputs on the second head group of every token only (heads 8..15: barely
+    discounted, log-normal scalings of Q_f and R_inv): its groups fail the certificate and
+    take the stable path as whole groups while the first groups stay on the matrix cores,
+    and the head sums of grad_B / grad_Q combine both kinds of group of the same token."""
+    H = 16
+    ins = bench_solver_inputs(3, H, d, seed=T + d + 3)
+    A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0 = [t.clone() for t in ins]
+    g = torch.Generator().manual_seed(T + 5)
+    hi = slice(8, 16)
+    Qf[:, hi] *= torch.exp(1.5 * torch.randn(3, 1, 1, 1, generator=g))
+    R_inv[:, hi] *= torch.exp(torch.randn(3, 8, 1, generator=g))
+    lgA[:, hi] *= 0.05
+    lgB[:, hi] *= 0.05
+    lgQ[:, hi] *= 0.05
+    out = check_case(f"groups{d}-mixed-T{T}", [A_diag, B, Q, R_inv, Qf, lgA, lgB, lgQ, h0], T,
+                     grad_limit=math.inf)
+    P = 3 * H
+    assert 0 < out["_fallback"] < P and out["_fallback"] % 8 == 0
+
+
 def test_config3_layer_slice():
     c = CONFIGS[3]
     x = make_x(3, n_tokens=2, seed=2)
