@@ -9,9 +9,15 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
   using G = MB<16, 4, 1, true>;
+  using GT = MB<16, 4, 1, true, true>;
   const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
-  hipLaunchKernelGGL((lqr_fwd_blk_kernel<16, 4, 1, SM, WU, true>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf, lA,
-                     lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+  // H % 4 == 0: the four problems of a wave are heads of one token and share its B and Q
+  if (H % 4 == 0)
+    hipLaunchKernelGGL((lqr_fwd_blk_kernel<16, 4, 1, SM, WU, true, false, true>), grid, block, GT::LDS_BYTES, s, A, B,
+                       Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+  else
+    hipLaunchKernelGGL((lqr_fwd_blk_kernel<16, 4, 1, SM, WU, true>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf,
+                       lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
   // rescue: the per-step Riccati kernel on the marked problems (its own breakdown guard
   // finishes on the pivoted row-layout sweep)
   const int64_t groups = (P + 3) / 4;

@@ -145,6 +145,11 @@ __device__ __forceinline__ unsigned mag_key(double x) {
   return (unsigned)(__double_as_longlong(fabs(x)) >> 32);
 }
 
+// Reciprocal of a pivot: the hardware reciprocal (1 ulp) in fp32, a division in fp64
+// (used for d = 16; the wider eliminations keep the division).
+__device__ __forceinline__ float pivot_recip(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ double pivot_recip(double x) { return 1.0 / x; }
+
 // In-place Gauss-Jordan elimination with partial pivoting on the D x D left block
 // of the augmented rows `aug` (lane li owns row li, width W >= D).  On return the
 // lane with pivot position `pos` holds row `pos` of (left^{-1} * right) scaled by
@@ -177,7 +182,7 @@ __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& my
 #pragma unroll
     for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::ld(prow + c, pr + c);
     (void)cs;
-    const R inv = R(1) / pr[k];
+    const R inv = D == 16 ? pivot_recip(pr[k]) : R(1) / pr[k];  // (wider: register pressure)
     const R f = me ? R(0) : aug[k] * inv;
 #pragma unroll
     for (int c = k + 1; c < W; ++c) aug[c] = fma(-f, pr[c], aug[c]);

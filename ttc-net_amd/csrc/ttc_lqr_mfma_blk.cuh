@@ -38,13 +38,16 @@
 #ifndef TTC_SYM_WAVES
 #define TTC_SYM_WAVES 3   // waves per SIMD of the symplectic kernel (144 VGPRs, no spills)
 #endif
+#ifndef TTC_SYM_WAVES_TOK
+#define TTC_SYM_WAVES_TOK 4  // the same with one register copy of B / Q per wave
+#endif
 #ifndef TTC_SYM_RENORM
 #define TTC_SYM_RENORM 8  // steps between power-of-2 renormalisations of the symplectic sweep
 #endif
 
 namespace ttc {
 
-template <int D, int PPW_, int WPB_, bool SYM_ = false>
+template <int D, int PPW_, int WPB_, bool SYM_ = false, bool TOK_ = false>
 struct MB {
   static constexpr bool SYM = SYM_;                 // symplectic sweep (d = 16) instead of Riccati steps
   static constexpr int NB = D / 16;                 // tiles per dimension
@@ -90,7 +93,11 @@ struct MB {
   static constexpr int THREADS = 64 * WPB;
   // two waves per SIMD, except with four problems per wave that keep B and Q in registers;
   // the symplectic sweep's small state leaves room for four
-  static constexpr int MINW = SYMW ? 2 : SYM ? TTC_SYM_WAVES : (PPW == 4 && !BQ_LDS) ? 1 : 2;
+  // the problems of a wave belong to one token (H % PPW == 0): one register copy of B, B' and
+  // -sym(Q) for all of them
+  static constexpr bool TOK = TOK_ && !BQ_LDS;
+  static constexpr int NBQ = (BQ_LDS || TOK) ? 1 : PPW;
+  static constexpr int MINW = SYMW ? 2 : SYM ? (TOK ? TTC_SYM_WAVES_TOK : TTC_SYM_WAVES) : (PPW == 4 && !BQ_LDS) ? 1 : 2;
   static constexpr int MAXW = MINW;
   static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)SH + (size_t)WPB * PER_WAVE);
 };
@@ -121,16 +128,18 @@ __host__ __device__ constexpr int utile(int I, int J) {
 
 // RESC_: rescue pass after the symplectic sweep (Riccati steps only): a workgroup runs only when
 // one of its problems carries the NaN marker, and stores the marked problems only.
-template <int D, int PPW_, int WPB_, int SM, bool WRITE_U, bool SYM_ = false, bool RESC_ = false>
-__global__ __launch_bounds__(64 * WPB_) __attribute__((amdgpu_waves_per_eu(MB<D, PPW_, WPB_, SYM_>::MINW,
-                                                                           MB<D, PPW_, WPB_, SYM_>::MAXW))) void
+template <int D, int PPW_, int WPB_, int SM, bool WRITE_U, bool SYM_ = false, bool RESC_ = false, bool TOK_ = false>
+__global__ __launch_bounds__(64 * WPB_) __attribute__((amdgpu_waves_per_eu(MB<D, PPW_, WPB_, SYM_, TOK_>::MINW,
+                                                                           MB<D, PPW_, WPB_, SYM_, TOK_>::MAXW))) void
 lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
                    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
                    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
                    int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
                    float* __restrict__ q0stash, int* __restrict__ status) {
-  using G = MB<D, PPW_, WPB_, SYM_>;
+  using G = MB<D, PPW_, WPB_, SYM_, TOK_>;
   constexpr int NB = G::NB, PPW = G::PPW, NT = G::NT, LDX = G::LDX, LDG = G::LDG;
+  constexpr int NBQ = G::NBQ;
+  auto bqi = [](int q) { return NBQ == 1 ? 0 : q; };  // register copy of B / Q of problem q
   constexpr int RPP = G::RPP, NPASS = G::NPASS;
   constexpr bool BQL = G::BQ_LDS;
   extern __shared__ __align__(16) float sm[];
@@ -184,12 +193,12 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
 
   // C-layout state: N = -V (all tiles); B and -sym(Q) (registers, or shared LDS for d = 64)
   v4f NV[PPW][NB][NB];
-  float Bm[BQL ? 1 : PPW][NB][NB][4];
-  v4f Qn[BQL ? 1 : PPW][NT];
+  float Bm[NBQ][NB][NB][4];
+  v4f Qn[NBQ][NT];
   float rr[PPW][NB];  // 1 / R_inv[16I + c]
   // symplectic sweep: B in the transposed operand layout, Bt[q][I][K][s] = B[16I + c][16K + 4g + s],
   // and Y1' (the sweep keeps Y-hat = Y' in the C layout; Y2' is -N)
-  float Bt[(G::SYM && !G::SYMW) ? PPW : 1][NB][NB][4];
+  float Bt[(G::SYM && !G::SYMW) ? NBQ : 1][NB][NB][4];
   v4f Y1[G::SYM ? PPW : 1][NB][NB];
   if constexpr (BQL) {
     // the workgroup's token: B column-major, -sym(Q) as per-lane C-layout fragments
@@ -236,12 +245,12 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * I + 4 * g + r, j = 16 * J + c;
           NV[q][I][J][r] = -0.5f * (fq[i * D + j] + fq[j * D + i]);
-          if constexpr (!BQL) {
-            Bm[q][I][J][r] = bq[i * D + j];
-            if (I <= J) Qn[q][utile<NB>(I, J)][r] = -0.5f * (qq[i * D + j] + qq[j * D + i]);
+          if (!BQL && q < NBQ) {
+            Bm[bqi(q)][I][J][r] = bq[i * D + j];
+            if (I <= J) Qn[bqi(q)][utile<NB>(I, J)][r] = -0.5f * (qq[i * D + j] + qq[j * D + i]);
           }
           if constexpr (G::SYM) {
-            if constexpr (!G::SYMW) Bt[q][I][J][r] = bq[(16 * I + c) * D + 16 * J + 4 * g + r];
+            if (!G::SYMW && q < NBQ) Bt[bqi(q)][I][J][r] = bq[(16 * I + c) * D + 16 * J + 4 * g + r];
             Y1[q][I][J][r] = (i == j) ? 1.0f : 0.0f;
           }
         }
@@ -272,7 +281,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
         for (int s = 0; s < 4; ++s) Bk[J][s] = b4[s] * bj;
       } else {
 #pragma unroll
-        for (int s = 0; s < 4; ++s) Bk[J][s] = Bm[q][K][J][s] * bj;
+        for (int s = 0; s < 4; ++s) Bk[J][s] = Bm[bqi(q)][K][J][s] * bj;
       }
     }
   };
@@ -448,7 +457,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
           const float qcol = v[D + 16 * J + c];
           v4f qn;
           if constexpr (BQL) qn = ld4(shq + (utile<NB>(I, J) * 64 + lane) * 4);
-          else qn = Qn[q][utile<NB>(I, J)];
+          else qn = Qn[bqi(q)][utile<NB>(I, J)];
 #pragma unroll
           for (int r = 0; r < 4; ++r) NV[q][I][J][r] = fmaf(arow[r] * acol, NV[q][I][J][r], (qrw[r] * qcol) * qn[r]);
         }
@@ -502,13 +511,13 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       // M = (B' N) diag-row(-beta^2 R^{-1}) = R^{-1} B_k' Y2'
       v4f M = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) M = mfma16x16x4(Bm[q][0][0][s], NV[q][0][0][s], M);
+      for (int s = 0; s < 4; ++s) M = mfma16x16x4(Bm[bqi(q)][0][0][s], NV[q][0][0][s], M);
       const v4f nf = ld4(v + 3 * D + 4 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) M[r] *= nf[r];
       // Y1' <- A^{-1} (Y1' + B M)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Y1[q][0][0] = mfma16x16x4(Bt[q][0][0][s], M[s], Y1[q][0][0]);
+      for (int s = 0; s < 4; ++s) Y1[q][0][0] = mfma16x16x4(Bt[bqi(q)][0][0][s], M[s], Y1[q][0][0]);
       const v4f ia = ld4(v + 4 * D + 4 * g);
       const v4f al = ld4(v + 4 * g);
 #pragma unroll
@@ -521,7 +530,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       const v4f qrw = ld4(v + D + 4 * g);
       float op[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) op[s] = Qn[q][0][s] * (qc * qrw[s]);
+      for (int s = 0; s < 4; ++s) op[s] = Qn[bqi(q)][0][s] * (qc * qrw[s]);
 #pragma unroll
       for (int s = 0; s < 4; ++s) NV[q][0][0] = mfma16x16x4(op[s], Y1[q][0][0][s], NV[q][0][0]);
       if (renorm) {
