@@ -39,7 +39,8 @@
 #define TTC_SYM_WAVES 3   // waves per SIMD of the symplectic kernel (144 VGPRs, no spills)
 #endif
 #ifndef TTC_SYM_WAVES_TOK
-#define TTC_SYM_WAVES_TOK 4  // the same with one register copy of B / Q per wave
+#define TTC_SYM_WAVES_TOK 5  // the same with one register copy of B / Q per wave (96 VGPRs; spills
+                             // only outside the time loop)
 #endif
 #ifndef TTC_SYM_RENORM
 #define TTC_SYM_RENORM 8  // steps between power-of-2 renormalisations of the symplectic sweep
@@ -75,16 +76,16 @@ struct MB {
   // buffer and the step-0 row buffer
   static constexpr int CH = SYMW ? 1 : (BQ_LDS ? NB / 2 : NB);
   static constexpr int XROWS = CH * 16;
-  static constexpr int LDS2 = 2 * D + 4;            // symplectic: rows of [Y1 | -Y2]
   static constexpr int REG0 = XROWS * LDX;
-  // SYMW stages 16 rows of D at a time through it (the final solve's input and output)
-  static constexpr int REG = (SYM && !SYMW && D * LDS2 > REG0) ? D * LDS2
-                                                             : ((SYMW && 16 * LDX > REG0) ? 16 * LDX : REG0);
+  // the symplectic final solve stages 16 rows of D at a time through it (Y1, then -Y2, then
+  // the solution)
+  static constexpr int REG = (SYMW && 16 * LDX > REG0) ? 16 * LDX : REG0;
   // the final solve of the symplectic sweep works on [Y1 | -Y2 | I] (Y1^{-1} for the condition
   // number) up to d = 32; at d = 64 on [Y1 | -Y2], with the pivots' spread as the estimate
   static constexpr bool SYM_INV = D < 64;
   static constexpr int AUGW = SYM_INV ? 3 * D : 2 * D;
-  static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4 && (!SYMW || REG >= AUGW + 4),
+  static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4 && (!SYMW || REG >= AUGW + 4) &&
+                    (!SYM || SYMW || REG >= 3 * D),
                 "per-problem LDS region");
   static_assert(!SYM || (D == 16 && !BQ_LDS) || (D >= 32 && BQ_LDS), "symplectic sweep: d = 16, or d = 32 / 64 from LDS");
   // per-problem vectors: alpha, q (step 0: alpha*h0), beta (step 0: rhs), -beta^2 R^{-1}, 1/alpha
@@ -747,60 +748,59 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     wave_sync();
     return bits;
     } else {
-    constexpr int L2 = G::LDS2;
+    // d = 16: one pass (16 lanes per problem); Y1, then -Y2, go through each problem's region
+    // (row c of Y1 = column c of Y1'), which then holds the pivot row and the solution
+    static_assert(NPASS == 1, "d = 16 final solve: one row-layout pass");
+    constexpr int L2 = LDX;
+    float* buf = region(qr[0]);
+    float aug[3 * D];
 #pragma unroll
-    for (int q = 0; q < PPW; ++q) {
-      float* buf = region(q);
-      st4(buf + c * L2 + 4 * g, Y1[q][0][0]);      // row c of Y1 = column c of Y1'
-      st4(buf + c * L2 + D + 4 * g, NV[q][0][0]);  // row c of -Y2
-    }
-    wave_sync();
-    bool ok = true;
+    for (int mtx = 0; mtx < 2; ++mtx) {
+      wave_sync();  // the previous rows have been read
 #pragma unroll
-    for (int pa = 0; pa < NPASS; ++pa) {
-      float* buf = region(qr[pa]);
-      float aug[3 * D];
-      ld_row<2 * D>(buf + li * L2, *reinterpret_cast<float(*)[2 * D]>(aug));
-#pragma unroll
-      for (int k = 0; k < D; ++k) aug[2 * D + k] = (k == li) ? 1.0f : 0.0f;
-      float rs = 0.f;
-#pragma unroll
-      for (int k = 0; k < D; ++k) rs += fabsf(aug[k]);
-      const float n1 = dgroup_max<D>(rs);  // ||Y1||_inf
-      wave_sync();  // every row read before the pivot-row buffer (aliasing them) is written
-      float piv;
-      int pos;
-      gauss_jordan<D, 3 * D>(aug, li, buf, piv, pos);
-      const float ip = 1.0f / piv;
-      float ri = 0.f, pn[D];
-#pragma unroll
-      for (int k = 0; k < D; ++k) {
-        ri += fabsf(aug[2 * D + k]);
-        pn[k] = aug[D + k] * ip;
-      }
-      const float n2 = dgroup_max<D>(ri * fabsf(ip));  // ||Y1^{-1}||_inf
-      st_row<D>(buf + pos * L2, pn);
+      for (int q = 0; q < PPW; ++q) st4(region(q) + c * L2 + 4 * g, mtx == 0 ? Y1[q][0][0] : NV[q][0][0]);
       wave_sync();
-      float da = 0.f, mx = 0.f;
-#pragma unroll
-      for (int k = 0; k < D; ++k) {
-        da = fmaxf(da, fabsf(pn[k] - buf[k * L2 + pos]));
-        mx = fmaxf(mx, fabsf(pn[k]));
-      }
-      da = dgroup_max<D>(da);
-      mx = dgroup_max<D>(mx);
-      ok = (n1 * n2 <= kSymCondMax) && (da <= kSymAsymMax * mx);  // false on NaN
+      ld_row<D>(buf + li * L2, *reinterpret_cast<float(*)[D]>(aug + mtx * D));
     }
+#pragma unroll
+    for (int k = 0; k < D; ++k) aug[2 * D + k] = (k == li) ? 1.0f : 0.0f;
+    float rs = 0.f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) rs += fabsf(aug[k]);
+    const float n1 = dgroup_max<D>(rs);  // ||Y1||_inf
+    wave_sync();  // every row read before the pivot-row buffer (aliasing them) is written
+    float piv;
+    int pos;
+    gauss_jordan<D, 3 * D>(aug, li, buf, piv, pos);
+    const float ip = 1.0f / piv;
+    float ri = 0.f, pn[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      ri += fabsf(aug[2 * D + k]);
+      pn[k] = aug[D + k] * ip;
+    }
+    const float n2 = dgroup_max<D>(ri * fabsf(ip));  // ||Y1^{-1}||_inf
+    st_row<D>(buf + pos * L2, pn);
+    wave_sync();
+    float da = 0.f, mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      da = fmaxf(da, fabsf(pn[k] - buf[k * L2 + pos]));
+      mx = fmaxf(mx, fabsf(pn[k]));
+    }
+    da = dgroup_max<D>(da);
+    mx = dgroup_max<D>(mx);
+    const bool ok = (n1 * n2 <= kSymCondMax) && (da <= kSymAsymMax * mx);  // false on NaN
     const unsigned long long bal = __ballot(ok);
     unsigned bits = 0u;
 #pragma unroll
     for (int q = 0; q < PPW; ++q) bits |= (unsigned)((bal >> (q * D)) & 1ull) << q;
 #pragma unroll
     for (int q = 0; q < PPW; ++q) {
-      const float* buf = region(q);
+      const float* b = region(q);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        NV[q][0][0][r] = 0.5f * (buf[(4 * g + r) * L2 + c] + buf[c * L2 + 4 * g + r]);
+        NV[q][0][0][r] = 0.5f * (b[(4 * g + r) * L2 + c] + b[c * L2 + 4 * g + r]);
     }
     wave_sync();
     return bits;
