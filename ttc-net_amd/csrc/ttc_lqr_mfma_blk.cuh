@@ -146,7 +146,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   extern __shared__ __align__(16) float sm[];
   constexpr float kLog2e = 1.4426950408889634f;
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;  // wave of the workgroup
+  const int wv = G::WPB == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave of the workgroup (uniform)
   const int g = lane >> 4;          // lane group: MFMA row block
   const int c = lane & 15;          // MFMA column; row of the 16x16 elimination
   const int qe = g / G::GPP;        // my problem in the 16x16 elimination
@@ -239,7 +239,6 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     const float* fq = Qf + pid[q] * D * D;
 #pragma unroll
     for (int I = 0; I < NB; ++I) {
-      rr[q][I] = 1.0f / Rinv[pid[q] * D + 16 * I + c];
 #pragma unroll
       for (int J = 0; J < NB; ++J) {
 #pragma unroll
@@ -258,16 +257,24 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       }
     }
   }
-  // pivot floor of my elimination problem: half of min_j 1 / R_inv_j
+  // R = 1 / R_inv per problem, and the pivot floor of my elimination problem: half of
+  // min_j 1 / R_inv_j (the symplectic sweep needs them only from step 0 on, after its loop)
   float piv_floor = 0.f;
+  auto load_r = [&]() {
 #pragma unroll
-  for (int q = 0; q < PPW; ++q) {
-    float m = rr[q][0];
+    for (int q = 0; q < PPW; ++q)
 #pragma unroll
-    for (int I = 1; I < NB; ++I) m = fminf(m, rr[q][I]);
-    m = 0.5f * row16_min(m);
-    if (q == qe) piv_floor = m;
-  }
+      for (int I = 0; I < NB; ++I) rr[q][I] = 1.0f / Rinv[pid[q] * D + 16 * I + c];
+#pragma unroll
+    for (int q = 0; q < PPW; ++q) {
+      float m = rr[q][0];
+#pragma unroll
+      for (int I = 1; I < NB; ++I) m = fminf(m, rr[q][I]);
+      m = 0.5f * row16_min(m);
+      if (q == qe) piv_floor = m;
+    }
+  };
+  if constexpr (!G::SYM) load_r();
   if constexpr (BQL) __syncthreads();  // shared B / Q written (the only workgroup barrier)
 
   // B_k = B diag(beta), block-row K: Bk[J][s] = B[16K + 4g + s][16J + c] beta[16J + c]
@@ -905,6 +912,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   if constexpr (G::SYM) {
     for (int t = T - 1; t >= 1; --t) sym_step(t);
     okbits = sym_finish();
+    load_r();
     step0();
   } else {
     int t = T - 1;
