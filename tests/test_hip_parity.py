@@ -300,6 +300,35 @@ def test_padding_odd_dims_and_ragged_problem_count():
     check_case("pad", ins, T)
 
 
+def _random_case(seed):
+    """A seeded draw of (N, H, d, du, T, precision) and inputs of the bench distribution
+    with a rectangular B: every padded width (16 / 32 / 64), head counts that do and do not
+    form head groups of 8, T from 1 up, and each fp32 kernel family."""
+    rng = np.random.default_rng(seed)
+    d = int(rng.integers(3, 65))
+    du = int(rng.integers(2, 65))
+    H = int(rng.choice([1, 2, 3, 4, 5, 8, 16, 24]))
+    N = int(rng.integers(1, 4))
+    T = int(rng.integers(3, 65)) if rng.random() < 0.75 else int(rng.choice([1, 2]))
+    precision = str(rng.choice(["fp32", "fp32-riccati", "fp32-row"]))
+    g = torch.Generator().manual_seed(seed)
+    ins = bench_solver_inputs(N, H, max(d, du), seed=seed)
+    A, _, Q, _, Qf, lgA, _, lgQ, h0 = ins
+    B = torch.randn(N, d, du, generator=g) / math.sqrt(max(d, du))
+    R_inv = torch.nn.functional.softplus(torch.rand(N, H, du, generator=g))
+    lgB = -torch.nn.functional.softplus(torch.randn(N, H, du, generator=g)) - 1.328
+    ins = [A[..., :d], B, Q[:, :d, :d], R_inv, Qf[:, :, :d, :d], lgA, lgB, lgQ[..., :d], h0[..., :d]]
+    return [t.contiguous() for t in ins], T, precision
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_random_shapes(seed):
+    """Seeded random shapes and kernels against the fp64 oracle (u and all nine gradients)."""
+    ins, T, precision = _random_case(1000 + seed)
+    out = check_case(f"rand{seed}", ins, T, precision=precision, grad_limit=math.inf)
+    assert np.isfinite(out["u"]).all()
+
+
 def _indefinite_terminal_inputs(s, seed=2):
     """Problem 1 of 8 gets Q_f = -s I with a strong, barely discounted B: Quu turns
     indefinite (nonsingular), so the matrix-core kernel's Cholesky guard fires for the
