@@ -209,8 +209,8 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     cR += swap8(cR);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      sP[k] = -cR[k];
-      sPt[k] = cLB[k] * (-0.5f / rinv[k]);
+      sP[k] = rinv[k] * cR[k];
+      sPt[k] = 0.5f * cLB[k];
     }
   }
   // grad_B += Lambda Pi (beta o U)'
@@ -225,11 +225,13 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   }
   S = S1;
 
-  // Steps t >= 1 need no u_t of their own: with u_t = -R^{-1} beta_t B' lambda_{t+1} and
-  // P_t = (B' lambda_{t+1}) o (B' lambda~_{t+1}) (equal on primal and adjoint lanes),
-  //   grad lgB:   (t+1) beta (u B'lambda~ + w B'lambda) = -2 R_inv (t+1) beta^2 P,
-  //   grad R_inv: -u w / R_inv^2                          = -beta^2 P,
-  // so the loop sums beta^2 P and (t+1) beta^2 P and forms beta o U = -R_inv beta^2 B'Lambda.
+  // Steps t >= 1 need no u_t of their own: with u_t = -R^{-1} beta_t B' lambda_{t+1},
+  // beta o U = -R_inv beta^2 B'Lambda, and W_t = (beta o U) o (B' Lambda~) = -R_inv beta^2 P_t,
+  // P_t = (B' lambda_{t+1}) o (B' lambda~_{t+1}) (the same on primal and adjoint lanes up to
+  // rounding),
+  //   grad lgB:   (t+1) beta (u B'lambda~ + w B'lambda) = 2 (t+1) W,
+  //   grad R_inv: -u w / R_inv^2                          = W / R_inv,
+  // so the loop sums W and (t+1) W (sP, sPt; one lane of each pair suffices).
   v4f lb4;
 #pragma unroll
   for (int k = 0; k < 4; ++k) lb4[k] = 2.0f * lb2[k];
@@ -250,17 +252,16 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     v4f QX = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) QX = mfma16x16x4(Qa[s], X1[s], QX);
-    const v4f Qh = q * QX;
     st_tile_rowmajor(Z, g, c, X1);
     const float eA = __builtin_amdgcn_exp2f(la2 * tp1);
     v4f al, b2;
     {
-      const v4f Qhx = swap8(Qh);
+      const v4f QXx = swap8(QX);  // Qc h = q o QX; q is the same on primal and adjoint lanes
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        accLQ[k] = fmaf(tf * S[k], Qhx[k], accLQ[k]);  // t (h Qc h~ | h~ Qc h)
+        accLQ[k] = fmaf(tf * X1[k], QXx[k], accLQ[k]);  // t (h Qc h~ | h~ Qc h)
         al[k] = fmaf(a4[k], eA, 1.0f);
-        L[k] = (L[k] - Qh[k]) * __builtin_amdgcn_rcpf(al[k]);
+        L[k] = fmaf(-q[k], QX[k], L[k]) * __builtin_amdgcn_rcpf(al[k]);
         b2[k] = __builtin_amdgcn_exp2f(lb4[k] * tp1);  // beta_t^2
       }
     }
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
         const float gAt = S[k] * Lx[k];                // h_t lambda~_{t+1} | h~_t lambda_{t+1}
         accA[k] = fmaf(gAt, eA, accA[k]);
         accLA[k] = fmaf(gAt, tea, accLA[k]);
-        const float w = b2[k] * (BtL[k] * BtLx[k]);
+        const float w = BU[k] * BtLx[k];
         sP[k] += w;
         sPt[k] = fmaf(tp1, w, sPt[k]);
       }
@@ -333,8 +334,8 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   v4f fLB, fR;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    fLB[k] = -2.0f * rinv[k] * sPt[k];
-    fR[k] = -sP[k];
+    fLB[k] = 2.0f * sPt[k];
+    fR[k] = sP[k] / rinv[k];
   }
   const v4f fLQ = accLQ + swap8(accLQ), fH0 = accH0 + swap8(accH0);
   float la_sum = accLA[0] * a4[0] + accLA[1] * a4[1] + accLA[2] * a4[2] + accLA[3] * a4[3];
