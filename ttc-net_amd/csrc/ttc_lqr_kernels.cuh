@@ -154,7 +154,10 @@ __device__ __forceinline__ double pivot_recip(double x) { return 1.0 / x; }
 // of the augmented rows `aug` (lane li owns row li, width W >= D).  On return the
 // lane with pivot position `pos` holds row `pos` of (left^{-1} * right) scaled by
 // `mypiv` (divide by it).  `prow` is W elements of this problem's LDS.
-template <int D, int W, typename R>
+// CHUNK > 0 reads the pivot row CHUNK elements at a time, each chunk's loads followed by its
+// updates (a scheduling barrier keeps the loads from being hoisted): fewer live registers
+// for kernels whose peak is this elimination, one LDS latency per chunk instead of one per row.
+template <int D, int W, int CHUNK = 0, typename R>
 __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& mypiv, int& pos) {
   constexpr unsigned kIdxBits = (D == 16) ? 4u : (D == 32 ? 5u : 6u);
   constexpr unsigned kIdxMask = (1u << kIdxBits) - 1u;
@@ -178,15 +181,34 @@ __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& my
       for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::st(prow + c, aug + c);
     }
     wave_sync();
-    R pr[W];
-#pragma unroll
-    for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::ld(prow + c, pr + c);
     (void)cs;
-    const R inv = D == 16 ? pivot_recip(pr[k]) : R(1) / pr[k];  // (wider: register pressure)
-    const R f = me ? R(0) : aug[k] * inv;
+    R pkv;  // the pivot
+    if constexpr (CHUNK == 0) {
+      R pr[W];
 #pragma unroll
-    for (int c = k + 1; c < W; ++c) aug[c] = fma(-f, pr[c], aug[c]);
-    if (me) { mypiv = pr[k]; pos = k; done = true; }
+      for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::ld(prow + c, pr + c);
+      pkv = pr[k];
+      const R inv = D == 16 ? pivot_recip(pkv) : R(1) / pkv;  // (wider: register pressure)
+      const R f = me ? R(0) : aug[k] * inv;
+#pragma unroll
+      for (int c = k + 1; c < W; ++c) aug[c] = fma(-f, pr[c], aug[c]);
+    } else {
+      static_assert(CHUNK % VN == 0 && W % CHUNK == 0, "pivot-row chunks");
+      pkv = prow[k];
+      const R inv = D == 16 ? pivot_recip(pkv) : R(1) / pkv;
+      const R f = me ? R(0) : aug[k] * inv;
+#pragma unroll
+      for (int c0 = k & ~(CHUNK - 1); c0 < W; c0 += CHUNK) {
+        R pr[CHUNK];
+#pragma unroll
+        for (int c = 0; c < CHUNK; c += VN) V16<R>::ld(prow + c0 + c, pr + c);
+#pragma unroll
+        for (int c = 0; c < CHUNK; ++c)
+          if (c0 + c > k) aug[c0 + c] = fma(-f, pr[c], aug[c0 + c]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (me) { mypiv = pkv; pos = k; done = true; }
     wave_sync();  // next pivot row may overwrite prow
   }
 }

@@ -778,7 +778,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     wave_sync();  // every row read before the pivot-row buffer (aliasing them) is written
     float piv;
     int pos;
-    gauss_jordan<D, 3 * D>(aug, li, buf, piv, pos);
+    gauss_jordan<D, 3 * D, 8>(aug, li, buf, piv, pos);
     const float ip = 1.0f / piv;
     float ri = 0.f, pn[D];
 #pragma unroll
