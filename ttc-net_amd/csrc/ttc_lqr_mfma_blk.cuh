@@ -39,8 +39,8 @@
 #define TTC_SYM_WAVES 3   // waves per SIMD of the symplectic kernel (144 VGPRs, no spills)
 #endif
 #ifndef TTC_SYM_WAVES_TOK
-#define TTC_SYM_WAVES_TOK 5  // the same with one register copy of B / Q per wave (96 VGPRs; spills
-                             // only outside the time loop)
+#define TTC_SYM_WAVES_TOK 6  // the same with one register copy of B / Q per wave (80 VGPRs; a few
+                             // spills, none in the time loop)
 #endif
 #ifndef TTC_SYM_RENORM
 #define TTC_SYM_RENORM 8  // steps between power-of-2 renormalisations of the symplectic sweep
@@ -818,12 +818,27 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
 
   // Step 0: stash V_1, form W_0 and Quu_0, u0 = -Quu_0^{-1} W_0' (alpha_0 * h0).
   auto step0 = [&]() {
+    // the row-layout problem indices once more, from an opaque copy of the lane index: after
+    // the symplectic sweep's loop, which needs every register, they are cheaper to recompute
+    // than to keep across it
+    int64_t po0[NPASS];
+    bool own0[NPASS];
+    {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+#pragma unroll
+      for (int pa = 0; pa < NPASS; ++pa) {
+        const int q = pa * RPP + ln / D;
+        own0[pa] = pbase + q < P;
+        po0[pa] = own0[pa] ? (pbase + q) : (P - 1);
+      }
+    }
 #pragma unroll
     for (int pa = 0; pa < NPASS; ++pa) {
       float* v = vecs + qr[pa] * G::VEC;
       const float alpha = fmaf(a_l[pa], __builtin_amdgcn_exp2f(la2_o[pa]), 1.0f);
       v[li] = alpha;
-      v[D + li] = alpha * h0[po[pa] * D + li];            // (A_0 h0)_li
+      v[D + li] = alpha * h0[po0[pa] * D + li];            // (A_0 h0)_li
       v[2 * D + li] = __builtin_amdgcn_exp2f(lb2_l[pa]);  // beta_0
     }
     wave_sync();
@@ -894,16 +909,16 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
           ld_row<D>(region(qr[pa]) + (li - h) * LDX, *reinterpret_cast<float(*)[D]>(aug));
       }
       aug[D] = vecs[qr[pa] * G::VEC + 2 * D + li];
-      const bool store = own_valid[pa] && ((okbits >> qr[pa]) & 1u);
+      const bool store = own0[pa] && ((okbits >> qr[pa]) & 1u);
       if (SM == STASH_V1 && store)
-        st_global_row<D>(q0stash + (po[pa] * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
+        st_global_row<D>(q0stash + (po0[pa] * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
       wave_sync();  // all rows read before the pivot-row buffer (aliasing them) is written
       float piv;
       int pos;
-      gauss_jordan<D, D + 4>(aug, li, region(qr[pa]), piv, pos);
+      gauss_jordan<D, D + 4, (D + 4) % 8 == 0 ? 8 : 4>(aug, li, region(qr[pa]), piv, pos);
       const float u0 = -aug[D] / piv;
       if (store) {
-        if (WRITE_U) u_out[po[pa] * D + pos] = u0;
+        if (WRITE_U) u_out[po0[pa] * D + pos] = u0;
         if (status != nullptr && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
       }
     }
