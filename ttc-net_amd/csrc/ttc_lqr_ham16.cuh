@@ -29,6 +29,10 @@
 // with the stable path.
 #include "ttc_lqr_mfma16.cuh"
 
+#ifndef TTC_HAM16_WAVES
+#define TTC_HAM16_WAVES 4  // waves per SIMD the registers must allow (119 VGPRs, no spills)
+#endif
+
 namespace ttc {
 
 struct Ham16 {
@@ -69,7 +73,7 @@ __device__ __forceinline__ v4f mfma_cross(const float* X, const float* Y, int g,
 }
 
 template <bool DIRECT>
-__global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(3, 4))) void lqr_ham16_mfma_kernel(
+__global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(TTC_HAM16_WAVES))) void lqr_ham16_mfma_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
@@ -137,7 +141,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     aug[17] = aug[18] = aug[19] = 0.f;
     float piv;
     int pos;
-    gauss_jordan<16, 20>(aug, c, prow, piv, pos);
+    gauss_jordan<16, 20, 4>(aug, c, prow, piv, pos);
     TS[(8 + 4 * pa + g) * Ham16::LD + pos] = -aug[16] / piv;  // adjoint column of problem 4pa+g
   }
   wave_sync();
