@@ -26,7 +26,11 @@ static void launch_b32(const float* A, const float* B, const float* Q, const flo
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool sym) {
   if (sym && H % 2 == 0) {
-    launch_b32_w<SM, WU, 2, 1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    // H % 8 == 0: 4-wave workgroups of one token share its B, B' and Q in LDS
+    if (H % 8 == 0)
+      launch_b32_w<SM, WU, 2, 4, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    else
+      launch_b32_w<SM, WU, 2, 1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
     // problems the certificate rejected: Riccati steps on the matrix cores first (only the
     // workgroups that hold one run), the row layout for what still breaks down
     if (H % 16 == 0)

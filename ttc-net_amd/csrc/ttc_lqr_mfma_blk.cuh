@@ -42,6 +42,9 @@
 #define TTC_SYM_WAVES_TOK 6  // the same with one register copy of B / Q per wave (80 VGPRs; a few
                              // spills, none in the time loop)
 #endif
+#ifndef TTC_SYMW32_WAVES
+#define TTC_SYMW32_WAVES 3  // the d = 32 symplectic sweep in 4-wave workgroups sharing B / Q (145 VGPRs)
+#endif
 #ifndef TTC_SYM_RENORM
 #define TTC_SYM_RENORM 8  // steps between power-of-2 renormalisations of the symplectic sweep
 #endif
@@ -98,7 +101,8 @@ struct MB {
   // -sym(Q) for all of them
   static constexpr bool TOK = TOK_ && !BQ_LDS;
   static constexpr int NBQ = (BQ_LDS || TOK) ? 1 : PPW;
-  static constexpr int MINW = SYMW ? 2 : SYM ? (TOK ? TTC_SYM_WAVES_TOK : TTC_SYM_WAVES) : (PPW == 4 && !BQ_LDS) ? 1 : 2;
+  static constexpr int MINW = SYMW ? (D == 32 && WPB > 1 ? TTC_SYMW32_WAVES : 2)
+                                  : SYM ? (TOK ? TTC_SYM_WAVES_TOK : TTC_SYM_WAVES) : (PPW == 4 && !BQ_LDS) ? 1 : 2;
   static constexpr int MAXW = MINW;
   static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)SH + (size_t)WPB * PER_WAVE);
 };
@@ -695,7 +699,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       float* buf = region(qr[pa]);
       float piv;
       int pos;
-      gauss_jordan<D, W>(aug, li, buf, piv, pos);
+      gauss_jordan<D, W, 8>(aug, li, buf, piv, pos);
       const float ip = 1.0f / piv;
       float pn[D];
 #pragma unroll
