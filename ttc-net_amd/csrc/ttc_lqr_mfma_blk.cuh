@@ -125,6 +125,10 @@ __device__ __forceinline__ float dgroup_max(float v) {
   return v;
 }
 
+// |x| as its bit pattern: non-negative floats order like their bits, so a maximum of |x| is
+// an integer maximum (no NaN canonicalisation; a NaN sorts above infinity)
+__device__ __forceinline__ unsigned absbits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+
 // upper tile (I, J), I <= J, in row-major order of the upper triangle
 template <int NB>
 __host__ __device__ constexpr int utile(int I, int J) {
@@ -546,12 +550,12 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
 #pragma unroll
       for (int s = 0; s < 4; ++s) NV[q][0][0] = mfma16x16x4(op[s], Y1[q][0][0][s], NV[q][0][0]);
       if (renorm) {
-        float m = 0.f;
+        unsigned mk = 0u;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(fabsf(Y1[q][0][0][r]), fabsf(NV[q][0][0][r])));
-        m = fmaxf(m, __shfl_xor(m, 16, 64));
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
-        const int e = 1 - __builtin_amdgcn_frexp_expf(m);  // m * 2^e in [1, 2)
+        for (int r = 0; r < 4; ++r) mk = max(mk, max(absbits(Y1[q][0][0][r]), absbits(NV[q][0][0][r])));
+        mk = max(mk, (unsigned)__shfl_xor((int)mk, 16, 64));
+        mk = max(mk, (unsigned)__shfl_xor((int)mk, 32, 64));
+        const int e = 1 - __builtin_amdgcn_frexp_expf(__uint_as_float(mk));  // m * 2^e in [1, 2)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           Y1[q][0][0][r] = __builtin_amdgcn_ldexpf(Y1[q][0][0][r], e);
@@ -629,14 +633,14 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       if (renorm) {  // per column 16J + c of Y-hat
 #pragma unroll
         for (int J = 0; J < NB; ++J) {
-          float m = 0.f;
+          unsigned mk = 0u;
 #pragma unroll
           for (int I = 0; I < NB; ++I)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) m = fmaxf(m, fmaxf(fabsf(Y1[q][I][J][r]), fabsf(NV[q][I][J][r])));
-          m = fmaxf(m, __shfl_xor(m, 16, 64));
-          m = fmaxf(m, __shfl_xor(m, 32, 64));
-          const int e = 1 - __builtin_amdgcn_frexp_expf(m);
+            for (int r = 0; r < 4; ++r) mk = max(mk, max(absbits(Y1[q][I][J][r]), absbits(NV[q][I][J][r])));
+          mk = max(mk, (unsigned)__shfl_xor((int)mk, 16, 64));
+          mk = max(mk, (unsigned)__shfl_xor((int)mk, 32, 64));
+          const int e = 1 - __builtin_amdgcn_frexp_expf(__uint_as_float(mk));
 #pragma unroll
           for (int I = 0; I < NB; ++I)
 #pragma unroll
