@@ -266,7 +266,8 @@ def main():
     PROGRESS = args.progress
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the LQR problems shard over tokens with no "
-                                   "exchange, so a multi-GPU figure is not produced here (see DESIGN.md)",
+                                   "exchange (each rank would run these kernels on its N/G tokens), so a "
+                                   "multi-GPU figure is not produced here",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import torch
