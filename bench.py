@@ -34,6 +34,7 @@ for _p in (ROOT, os.path.join(ROOT, "ttc-net_amd")):
 
 METRIC = "LQR solves/sec fwd & fwd+bwd (h=16,T=64) + % HBM/MFMA roofline, 1×MI355X"
 PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix peak (published)
+PEAK_FP64 = 78.6e12         # MI355X fp64 peak (published; vector and matrix)
 PEAK_HBM = 8.0e12
 
 CONFIGS = {
@@ -313,6 +314,11 @@ def main():
     fwd_bytes = 4 * (3 * d + 2 * d + d * d + 1 + d) + 4 * (d * d + d * d) / H
     traffic = traffic_from_profiles(f"lqr_fwd_cfg{args.config}")
     kern = f"lqr_fwd_blk_kernel<{d}>" + (" (symplectic sweep)" if d == 16 else " (blocked Riccati)")
+    # the solver's precision="auto" runs the fp64 Riccati sweep for T >= 512 where d <= 32
+    fp64 = T >= 512 and d <= 32
+    peak = PEAK_FP64 if fp64 else PEAK_FP32_MFMA
+    if fp64:
+        kern = f"lqr_fwd_kernel<{d}, double> (fp64 Riccati, row layout)"
     out = {
         "metric": METRIC,
         "value": P / step_s,
@@ -324,7 +330,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f64" if fp64 else "f32",
         "data": "synthetic (seeded N(0,1) x, random-init layer weights)",
         "config": {"workload": f"cfg{args.config}: TTCLayer(in={c['in_dim']},out={c['out_dim']},h={d},heads={H},"
                                f"b_rank={c['b_rank']},q_rank={c['q_rank']}) T={T}, x{xshape} -> "
@@ -338,8 +344,8 @@ def main():
         "bwd_fallback_problems": r["bwd_fallback_problems"],
         "tokens_per_s_fwd_bwd": N / step_s,
         "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
-        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
+        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": traffic,
                      "kernel": kern, "flops_per_problem": F_fwd,
                      "algorithmic_bytes_per_problem": fwd_bytes},
     }

@@ -149,12 +149,12 @@ static StableLayout stable_layout(int64_t chunk_tokens, int H, int d, int T) {
   const size_t Pc = (size_t)chunk_tokens * (size_t)H;
   StableLayout L{};
   size_t off = 0;
-  L.kst = off;
-  off += align256(Pc * (size_t)T * d * d * sizeof(float));
+  L.kst = off;  // gains K_t, fp64 where the fp64 sweeps run (d <= 32)
+  off += align256(Pc * (size_t)T * d * d * (d <= 32 ? sizeof(double) : sizeof(float)));
   L.q0s = off;
   off += align256(Pc * (size_t)d * d * sizeof(float));
-  L.traj = off;
-  off += align256(Pc * (size_t)T * d * 4 * sizeof(float));
+  L.traj = off;  // (h, h~, u, w) per step, fp64 where the fp64 sweeps run (d <= 32)
+  off += align256(Pc * (size_t)T * d * 4 * (d <= 32 ? sizeof(double) : sizeof(float)));
   L.gBp = off;
   off += align256(Pc * (size_t)d * d * sizeof(float));
   L.gQp = off;
@@ -198,13 +198,14 @@ static int stable_backward(const float* A, const float* B, const float* Q, const
     float* q0s = reinterpret_cast<float*>(ws + L.q0s);
     int rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, Pc, H, T, nullptr, kst, q0s, kStashGains, nullptr, s, flags);
     if (rc != TTC_LQR_OK) return rc;
-    float4* traj = reinterpret_cast<float4*>(ws + L.traj);
+    void* traj = ws + L.traj;
+    const bool fp64 = (flags & TTC_LQR_FLAG_FP64_RICCATI) && d <= 32;
     float* gBp = reinterpret_cast<float*>(ws + L.gBp);
     float* gQp = reinterpret_cast<float*>(ws + L.gQp);
     switch (d) {
-      case 16: rc = launch_bwd_d16(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
-      case 32: rc = launch_bwd_d32(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
-      case 64: rc = launch_bwd_d64(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
+      case 16: rc = launch_bwd_d16(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, fp64, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
+      case 32: rc = launch_bwd_d32(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, fp64, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
+      case 64: rc = launch_bwd_d64(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, fp64, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
       default: return TTC_LQR_EUNSUPPORTED;
     }
     if (rc != TTC_LQR_OK) return rc;

@@ -17,11 +17,12 @@ int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* 
 
 int launch_bwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
-                  const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
+                  const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s) {
-  return launch_bwd<64>(A, B, Q, R, Qf, lA, lB, lQ, h0, dU, kst, q0s, P, H, T, traj, gA, gR, gQf, glA, glB, glQ,
-                       gh0, gBp, gQp, limit, status, s);
+  if (fp64) return TTC_LQR_EUNSUPPORTED;  // the fp64 sweeps cover d <= 32
+  return launch_bwd<64>(A, B, Q, R, Qf, lA, lB, lQ, h0, dU, kst, q0s, P, H, T, static_cast<float4*>(traj), gA, gR,
+                       gQf, glA, glB, glQ, gh0, gBp, gQp, limit, status, s);
 }
 
 int launch_ham_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,

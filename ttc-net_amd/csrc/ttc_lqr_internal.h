@@ -26,7 +26,7 @@ int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* 
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
 int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
-                  const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
+                  const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s);
 int launch_ham_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
@@ -40,7 +40,7 @@ int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* 
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
 int launch_bwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
-                  const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
+                  const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s);
 int launch_ham_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
@@ -54,7 +54,7 @@ int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* 
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
 int launch_bwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
-                  const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
+                  const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s);
 int launch_ham_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,

@@ -28,6 +28,7 @@
 // which is stable where the open-loop one amplifies rounding by prod(A_k).
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include "ttc_lqr.h"
@@ -109,6 +110,37 @@ __device__ __forceinline__ void st_global_row(float* __restrict__ g, const float
     *reinterpret_cast<float4*>(g + c) = make_float4(in[c], in[c + 1], in[c + 2], in[c + 3]);
 }
 
+template <int N>
+__device__ __forceinline__ void ld_global_row(const float* __restrict__ g, double (&out)[N]) {
+#pragma unroll
+  for (int c = 0; c < N; c += 4) {
+    const float4 v = *reinterpret_cast<const float4*>(g + c);
+    out[c] = v.x; out[c + 1] = v.y; out[c + 2] = v.z; out[c + 3] = v.w;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void st_global_row(float* __restrict__ g, const double (&in)[N]) {
+#pragma unroll
+  for (int c = 0; c < N; c += 4)
+    *reinterpret_cast<float4*>(g + c) = make_float4((float)in[c], (float)in[c + 1], (float)in[c + 2], (float)in[c + 3]);
+}
+
+template <int N>
+__device__ __forceinline__ void ld_global_row(const double* __restrict__ g, double (&out)[N]) {
+#pragma unroll
+  for (int c = 0; c < N; c += 2) {
+    const double2 v = *reinterpret_cast<const double2*>(g + c);
+    out[c] = v.x; out[c + 1] = v.y;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void st_global_row(double* __restrict__ g, const double (&in)[N]) {
+#pragma unroll
+  for (int c = 0; c < N; c += 2) *reinterpret_cast<double2*>(g + c) = make_double2(in[c], in[c + 1]);
+}
+
 // Max of a 32-bit key over the D lanes of a problem (all lanes get the result).
 template <int N>
 __device__ __forceinline__ unsigned ror16(unsigned v) {
@@ -125,15 +157,15 @@ __device__ __forceinline__ unsigned group_max_u32(unsigned k) {
   return k;
 }
 
-template <int D>
-__device__ __forceinline__ float group_sum(float v, float* scratch, int li) {
+template <int D, typename R = float>
+__device__ __forceinline__ R group_sum(R v, R* scratch, int li) {
   // via LDS: every lane writes, everyone reads the D values
   wave_sync();
   scratch[li] = v;
   wave_sync();
-  float vals[D];
+  R vals[D];
   ld_row<D>(scratch, vals);
-  float s = 0.f;
+  R s = 0;
 #pragma unroll
   for (int c = 0; c < D; ++c) s += vals[c];
   return s;
@@ -318,10 +350,15 @@ __device__ __forceinline__ void rpl_sweep(
 #pragma unroll
     for (int c = 0; c < D; ++c) x[c] = aug[D + c] * ipiv;
     if (SM == STASH_GAINS && valid) {
-      float krow[D];
+      // gains in the sweep's arithmetic: on long horizons with expensive control |K|
+      // reaches 1e19, and fp32-rounded gains make the closed-loop rollouts diverge
+      R krow[D];
 #pragma unroll
-      for (int c = 0; c < D; ++c) krow[c] = (float)(-x[c]);
-      st_global_row<D>(kstash + (((int64_t)p * T + t) * D + pos) * D, krow);
+      for (int c = 0; c < D; ++c) krow[c] = -x[c];
+      if constexpr (std::is_same<R, double>::value)
+        st_global_row<D>(reinterpret_cast<double*>(kstash) + (((int64_t)p * T + t) * D + pos) * D, krow);
+      else
+        st_global_row<D>(kstash + (((int64_t)p * T + t) * D + pos) * D, krow);
     }
     if (t == 0) {
       // u0[pos] = K_0[pos,:] . h0
@@ -420,24 +457,37 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_fwd_kernel(
 // sweep with all gradient accumulations.  grad_B / grad_Q are written per problem
 // into gBp / gQp and summed over heads by headsum_kernel.
 // ---------------------------------------------------------------------------
+template <typename R> struct Traj4 { using type = float4; };
+template <> struct Traj4<double> { using type = double4; };
+template <typename R> __device__ __forceinline__ typename Traj4<R>::type mk4(R x, R y, R z, R w) {
+  if constexpr (std::is_same<R, double>::value) return make_double4(x, y, z, w);
+  else return make_float4(x, y, z, w);
+}
+
 template <int D>
 __device__ __forceinline__ void flag_value(float v, float limit, int& flags) {
   if (!isfinite(v)) flags |= TTC_LQR_STATUS_NONFINITE;
   else if (fabsf(v) >= limit) flags |= TTC_LQR_STATUS_LARGE;
 }
-
 template <int D>
+__device__ __forceinline__ void flag_value(double v, float limit, int& flags) {
+  flag_value<D>((float)v, limit, flags);
+}
+
+template <int D, typename R = float>
 __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
     const float* __restrict__ dU, const float* __restrict__ kstash, const float* __restrict__ q0stash,
-    int64_t P, int H, int T, int ntok_lds, float4* __restrict__ traj, float* __restrict__ gA,
+    int64_t P, int H, int T, int ntok_lds, typename Traj4<R>::type* __restrict__ traj, float* __restrict__ gA,
     float* __restrict__ gRinv, float* __restrict__ gQf, float* __restrict__ glgA,
     float* __restrict__ glgB, float* __restrict__ glgQ, float* __restrict__ gh0,
     float* __restrict__ gBp, float* __restrict__ gQp, float grad_limit, int* __restrict__ status) {
   using G = Geo<D>;
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem_f[];
+  R* const smem = reinterpret_cast<R*>(smem_f);
+  const R* const kst = reinterpret_cast<const R*>(kstash);  // gains K_t in the forward sweep's type
   const int li = threadIdx.x % D;
   const int pb = threadIdx.x / D;
   const int64_t p0 = (int64_t)blockIdx.x * G::PPB;
@@ -455,42 +505,42 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     }
   }
   __syncthreads();
-  const float* Bs = smem + (int)(n - n0) * G::MAT;
-  float* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
-  float* v0 = S + G::MAT;     // 8 vectors of D floats
-  float* v1 = v0 + D;
-  float* v2 = v1 + D;
-  float* v3 = v2 + D;
-  float* v4 = v3 + D;
-  float* v5 = v4 + D;
-  float* v6 = v5 + D;
-  float* v7 = v6 + D;
-  float* prow = v7 + D;       // D + 4 floats
+  const R* Bs = smem + (int)(n - n0) * G::MAT;
+  R* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
+  R* v0 = S + G::MAT;     // 8 vectors of D floats
+  R* v1 = v0 + D;
+  R* v2 = v1 + D;
+  R* v3 = v2 + D;
+  R* v4 = v3 + D;
+  R* v5 = v4 + D;
+  R* v6 = v5 + D;
+  R* v7 = v6 + D;
+  R* prow = v7 + D;       // D + 4 floats
 
-  const float a_i = A_diag[p * D + li];
-  const float rr_i = 1.0f / Rinv[p * D + li];
-  const float lgB_i = lgB[p * D + li];
-  const float lgQ_i = lgQ[p * D + li];
-  const float lgA_p = lgA[p];
-  float Brow[D], Bcol[D], Qrow[D];
+  const R a_i = A_diag[p * D + li];
+  const R rr_i = R(1) / Rinv[p * D + li];
+  const R lgB_i = lgB[p * D + li];
+  const R lgQ_i = lgQ[p * D + li];
+  const R lgA_p = lgA[p];
+  R Brow[D], Bcol[D], Qrow[D];
   {
     const float* qg = Qg + n * D * D;
 #pragma unroll
     for (int c = 0; c < D; ++c) {
       Brow[c] = Bs[li * G::LDM + c];
       Bcol[c] = Bs[c * G::LDM + li];
-      Qrow[c] = 0.5f * (qg[li * D + c] + qg[c * D + li]);
+      Qrow[c] = R(0.5) * (qg[li * D + c] + qg[c * D + li]);
     }
   }
 
   // adjoint feed-forward at t = 0: w0 = -Quu_0^{-1} d_u
-  float w0_i;
+  R w0_i;
   {
-    float aug[D + 4];
-    ld_global_row<D>(q0stash + (p * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
+    R aug[D + 4];
+    ld_global_row<D>(q0stash + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
     aug[D] = dU[p * D + li];
-    aug[D + 1] = aug[D + 2] = aug[D + 3] = 0.f;
-    float piv;
+    aug[D + 1] = aug[D + 2] = aug[D + 3] = R(0);
+    R piv;
     int pos;
     gauss_jordan<D, D + 4>(aug, li, prow, piv, pos);
     v0[pos] = -aug[D] / piv;
@@ -500,38 +550,38 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   }
 
   // phase 1: rollouts, t = 0..T-1
-  float h_i = h0[p * D + li];
-  float hb_i = 0.f;
+  R h_i = h0[p * D + li];
+  R hb_i = R(0);
   for (int t = 0; t < T; ++t) {
-    const float tp1 = (float)(t + 1);
-    const float alpha_i = fmaf(a_i, expf(lgA_p * tp1), 1.0f);
-    const float beta_i = expf(lgB_i * tp1);
+    const R tp1 = (R)(t + 1);
+    const R alpha_i = fma(a_i, exp(lgA_p * tp1), R(1));
+    const R beta_i = exp(lgB_i * tp1);
     v0[li] = h_i;
     v1[li] = hb_i;
     wave_sync();
-    float hv[D], hbv[D], krow[D];
+    R hv[D], hbv[D], krow[D];
     ld_row<D>(v0, hv);
     ld_row<D>(v1, hbv);
-    ld_global_row<D>(kstash + (((int64_t)p * T + t) * D + li) * D, krow);
-    float u_i = 0.f, w_i = (t == 0) ? w0_i : 0.f;
+    ld_global_row<D>(kst + (((int64_t)p * T + t) * D + li) * D, krow);
+    R u_i = R(0), w_i = (t == 0) ? w0_i : R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      u_i = fmaf(krow[c], hv[c], u_i);
-      w_i = fmaf(krow[c], hbv[c], w_i);
+      u_i = fma(krow[c], hv[c], u_i);
+      w_i = fma(krow[c], hbv[c], w_i);
     }
     v2[li] = beta_i * u_i;
     v3[li] = beta_i * w_i;
     wave_sync();
-    float bu[D], bw[D];
+    R bu[D], bw[D];
     ld_row<D>(v2, bu);
     ld_row<D>(v3, bw);
-    float hn = alpha_i * h_i, hbn = alpha_i * hb_i;
+    R hn = alpha_i * h_i, hbn = alpha_i * hb_i;
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      hn = fmaf(Brow[j], bu[j], hn);
-      hbn = fmaf(Brow[j], bw[j], hbn);
+      hn = fma(Brow[j], bu[j], hn);
+      hbn = fma(Brow[j], bw[j], hbn);
     }
-    if (valid) traj[((int64_t)p * T + t) * D + li] = make_float4(h_i, hb_i, u_i, w_i);
+    if (valid) traj[((int64_t)p * T + t) * D + li] = mk4<R>(h_i, hb_i, u_i, w_i);
     h_i = hn;
     hb_i = hbn;
     wave_sync();
@@ -539,101 +589,101 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
 
   // phase 2: costates lambda_{t+1}, gradients, t = T-1..0
   int flags = 0;
-  float lam_i, lamb_i;
+  R lam_i, lamb_i;
   {
     v0[li] = h_i;
     v1[li] = hb_i;
     wave_sync();
-    float hv[D], hbv[D], qf[D], gq[D];
+    R hv[D], hbv[D], qf[D], gq[D];
     ld_row<D>(v0, hv);
     ld_row<D>(v1, hbv);
     const float* qfp = Qf + p * D * D;
-    lam_i = 0.f;
-    lamb_i = 0.f;
+    lam_i = R(0);
+    lamb_i = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      qf[c] = 0.5f * (qfp[li * D + c] + qfp[c * D + li]);
-      lam_i = fmaf(qf[c], hv[c], lam_i);
-      lamb_i = fmaf(qf[c], hbv[c], lamb_i);
-      gq[c] = 0.5f * (h_i * hbv[c] + hb_i * hv[c]);
+      qf[c] = R(0.5) * (qfp[li * D + c] + qfp[c * D + li]);
+      lam_i = fma(qf[c], hv[c], lam_i);
+      lamb_i = fma(qf[c], hbv[c], lamb_i);
+      gq[c] = R(0.5) * (h_i * hbv[c] + hb_i * hv[c]);
       flag_value<D>(gq[c], grad_limit, flags);
     }
     if (valid) st_global_row<D>(gQf + (p * D + li) * D, gq);
     wave_sync();
   }
-  float gA_i = 0.f, glgA_part = 0.f, glgB_i = 0.f, gr_i = 0.f, glgQ_i = 0.f, gh0_i = 0.f;
-  float gBrow[D], gQrow[D];
+  R gA_i = R(0), glgA_part = R(0), glgB_i = R(0), gr_i = R(0), glgQ_i = R(0), gh0_i = R(0);
+  R gBrow[D], gQrow[D];
 #pragma unroll
-  for (int c = 0; c < D; ++c) { gBrow[c] = 0.f; gQrow[c] = 0.f; }
+  for (int c = 0; c < D; ++c) { gBrow[c] = R(0); gQrow[c] = R(0); }
 
   for (int t = T - 1; t >= 0; --t) {
-    const float4 tr = traj[((int64_t)p * T + t) * D + li];
-    const float h_t = tr.x, hb_t = tr.y, u_i = tr.z, w_i = tr.w;
-    const float tp1 = (float)(t + 1);
-    const float eA = expf(lgA_p * tp1);
-    const float alpha_i = fmaf(a_i, eA, 1.0f);
-    const float beta_i = expf(lgB_i * tp1);
+    const auto tr = traj[((int64_t)p * T + t) * D + li];
+    const R h_t = tr.x, hb_t = tr.y, u_i = tr.z, w_i = tr.w;
+    const R tp1 = (R)(t + 1);
+    const R eA = exp(lgA_p * tp1);
+    const R alpha_i = fma(a_i, eA, R(1));
+    const R beta_i = exp(lgB_i * tp1);
     // A: d/dA_t,i = h_t,i lamb_{t+1},i + hb_t,i lam_{t+1},i   (torch_lqr.py:51)
-    const float gAt = fmaf(h_t, lamb_i, hb_t * lam_i);
-    gA_i = fmaf(gAt, eA, gA_i);
-    glgA_part = fmaf(gAt * a_i, tp1 * eA, glgA_part);
+    const R gAt = fma(h_t, lamb_i, hb_t * lam_i);
+    gA_i = fma(gAt, eA, gA_i);
+    glgA_part = fma(gAt * a_i, tp1 * eA, glgA_part);
     v0[li] = lam_i;
     v1[li] = lamb_i;
     v2[li] = beta_i * u_i;
     v3[li] = beta_i * w_i;
     wave_sync();
-    float lv[D], lbv[D], bu[D], bw[D];
+    R lv[D], lbv[D], bu[D], bw[D];
     ld_row<D>(v0, lv);
     ld_row<D>(v1, lbv);
     ld_row<D>(v2, bu);
     ld_row<D>(v3, bw);
     // B: lamb u' + lam w' (torch_lqr.py:53), chained through B_t = B diag(beta_t)
-    float btl = 0.f, btlb = 0.f;
+    R btl = R(0), btlb = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      gBrow[c] = fmaf(lamb_i, bu[c], fmaf(lam_i, bw[c], gBrow[c]));
-      btl = fmaf(Bcol[c], lv[c], btl);
-      btlb = fmaf(Bcol[c], lbv[c], btlb);
+      gBrow[c] = fma(lamb_i, bu[c], fma(lam_i, bw[c], gBrow[c]));
+      btl = fma(Bcol[c], lv[c], btl);
+      btlb = fma(Bcol[c], lbv[c], btlb);
     }
-    glgB_i = fmaf(tp1 * beta_i, fmaf(u_i, btlb, w_i * btl), glgB_i);
+    glgB_i = fma(tp1 * beta_i, fma(u_i, btlb, w_i * btl), glgB_i);
     // R = 1/R_inv:  d/dR_inv = -(u w) / R_inv^2   (torch_lqr.py:59)
-    gr_i = fmaf(-u_i * w_i, rr_i * rr_i, gr_i);
+    gr_i = fma(-u_i * w_i, rr_i * rr_i, gr_i);
     if (t >= 1) {
-      const float q_i = expf(lgQ_i * (float)t);
+      const R q_i = exp(lgQ_i * (R)t);
       // closed-loop correction c = R u + B_t' lambda_{t+1}
       v4[li] = q_i * h_t;
       v5[li] = q_i * hb_t;
-      v6[li] = fmaf(u_i, rr_i, beta_i * btl);
-      v7[li] = fmaf(w_i, rr_i, beta_i * btlb);
+      v6[li] = fma(u_i, rr_i, beta_i * btl);
+      v7[li] = fma(w_i, rr_i, beta_i * btlb);
       wave_sync();
-      float qh[D], qhb[D], cu[D], cw[D];
+      R qh[D], qhb[D], cu[D], cw[D];
       ld_row<D>(v4, qh);
       ld_row<D>(v5, qhb);
       ld_row<D>(v6, cu);
       ld_row<D>(v7, cw);
-      float Qh = 0.f, Qhb = 0.f, kcu = 0.f, kcw = 0.f;
-      const float* kp = kstash + (((int64_t)p * T + t) * D) * D + li;
+      R Qh = R(0), Qhb = R(0), kcu = R(0), kcw = R(0);
+      const R* kp = kst + (((int64_t)p * T + t) * D) * D + li;
 #pragma unroll
       for (int c = 0; c < D; ++c) {
-        Qh = fmaf(Qrow[c], qh[c], Qh);
-        Qhb = fmaf(Qrow[c], qhb[c], Qhb);
+        Qh = fma(Qrow[c], qh[c], Qh);
+        Qhb = fma(Qrow[c], qhb[c], Qhb);
         // Q_t = D_t Q D_t:  gradient D_t sym(h hb') D_t  (torch_lqr.py:55)
-        gQrow[c] = fmaf(0.5f * q_i, fmaf(h_t, qhb[c], hb_t * qh[c]), gQrow[c]);
-        const float kji = kp[c * D];  // K_t[c, li]
-        kcu = fmaf(kji, cu[c], kcu);
-        kcw = fmaf(kji, cw[c], kcw);
+        gQrow[c] = fma(R(0.5) * q_i, fma(h_t, qhb[c], hb_t * qh[c]), gQrow[c]);
+        const R kji = kp[c * D];  // K_t[c, li]
+        kcu = fma(kji, cu[c], kcu);
+        kcw = fma(kji, cw[c], kcw);
       }
       Qh *= q_i;
       Qhb *= q_i;
-      glgQ_i = fmaf((float)t, fmaf(h_t, Qhb, hb_t * Qh), glgQ_i);
-      lam_i = Qh + fmaf(alpha_i, lam_i, kcu);
-      lamb_i = Qhb + fmaf(alpha_i, lamb_i, kcw);
+      glgQ_i = fma((R)t, fma(h_t, Qhb, hb_t * Qh), glgQ_i);
+      lam_i = Qh + fma(alpha_i, lam_i, kcu);
+      lamb_i = Qhb + fma(alpha_i, lamb_i, kcw);
     } else {
       gh0_i = alpha_i * lamb_i;  // torch_lqr.py:61 (lambda_0 = A_0' lambda_1)
     }
     wave_sync();
   }
-  const float glgA_p = group_sum<D>(glgA_part, v0, li);
+  const R glgA_p = group_sum<D>(glgA_part, v0, li);
   flag_value<D>(gA_i, grad_limit, flags);
   flag_value<D>(glgB_i, grad_limit, flags);
   flag_value<D>(gr_i, grad_limit, flags);
@@ -1101,15 +1151,17 @@ inline int launch_ham(const float* A, const float* B, const float* Q, const floa
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
-template <int D>
+template <int D, typename RT = float>
 inline int launch_bwd(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                       const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
-                      const float* kst, const float* q0s, int64_t P, int H, int T, float4* traj, float* gA,
+                      const float* kst, const float* q0s, int64_t P, int H, int T,
+                      typename Traj4<RT>::type* traj, float* gA,
                       float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                       float* gQp, float limit, int32_t* status, hipStream_t s) {
   if (P <= 0) return TTC_LQR_OK;
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
-  hipLaunchKernelGGL((lqr_bwd_kernel<D>), grid, block, lds_bytes<D>(H), s, A, B, Q, R, Qf, lA, lB, lQ, h0, dU,
+  hipLaunchKernelGGL((lqr_bwd_kernel<D, RT>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf, lA, lB,
+                     lQ, h0, dU,
                      kst, q0s, P, H, T, ntok_lds_for<D>(H), traj, gA, gR, gQf, glA, glB, glQ, gh0, gBp, gQp,
                      limit, status);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
