@@ -226,7 +226,9 @@ static size_t compact_floats(int d, int du) {  // inputs + gradients of one prob
 
 static int64_t fallback_capacity(int64_t Pc, int d, int du, int T) {
   const size_t per = compact_floats(d, du) * sizeof(float) + 19 * 256 + stable_layout(1, 1, d, T).total;
-  int64_t cap = (int64_t)((size_t)256 << 20) / (int64_t)per;
+  // up to 1 GiB: at long horizons a rejected problem needs MBs of gain stash, and each
+  // chunk of rejected problems costs one serial T-step sweep
+  int64_t cap = (int64_t)((size_t)1024 << 20) / (int64_t)per;
   if (cap < 8) cap = 8;  // at least one head group of 8 (the d = 16 matrix-core backward's unit)
   return Pc < cap ? Pc : cap;
 }
