@@ -56,7 +56,10 @@ extern "C" {
 /* `flags` bits.  TTC_LQR_FLAG_FP64_RICCATI runs the backward-in-time Riccati sweep
  * (the gains) in fp64 arithmetic; inputs, outputs and the stash stay fp32.  Needed
  * for long, barely-discounted horizons (e.g. T = 1024 with log-normal inputs),
- * where fp32 rounding of V ~ 1e17 corrupts the gains. */
+ * where fp32 rounding of V ~ 1e17 corrupts the gains.  The backward's stable path
+ * (problems the certificate rejects, or TTC_LQR_FLAG_STABLE_BWD) then also runs in
+ * fp64: gains |K| up to ~1e19 stored in fp64 in the workspace, rollouts and costates in
+ * fp64, gradients written as fp32. */
 #define TTC_LQR_FLAG_FP64_RICCATI 1
 /* TTC_LQR_FLAG_ROW_KERNEL selects the row-layout (vector-ALU only) fp32 kernels -- the
  * forward sweep and the backward's Hamiltonian rollout, one problem per d lanes -- instead
