@@ -255,6 +255,31 @@ int ttc_lqr_backward_factored_bf16(const uint16_t* A_diag, const uint16_t* coeff
                                    size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
                                    void* stream);
 
+/* ---- Host (CPU) solver: the same problems on CPU tensors ----
+ * Replace the reference's device-agnostic pure-PyTorch solvers for CPU tensors:
+ *   ttc_lqr_forward_host   <- direct_lqr_solve / kkt_lqr_solve forward (ttc/solvers/torch_lqr.py:93-140,
+ *                             the Riccati sweep of lin_solver_lqr.py:113-212)
+ *   ttc_lqr_backward_host  <- KKTLQRSolveFunc.backward (torch_lqr.py:34-63) chained through the
+ *                             discount expansion (torch_lqr.py:65-91)
+ * so that TTCLayer(..., solver_impl="riccati" | "kkt") runs without a GPU.  Host pointers
+ * (fp32, contiguous, the shapes above), any d, du >= 1; arithmetic in fp64; no GPU call.
+ * `status` (host, may be NULL) receives the status bits as above (the backward's magnitude
+ * guard covers the gradients of A_diag, B, Q, R_inv, Q_f and h0, as fused_lqr.py:243-246).
+ * n_threads: worker threads (<= 0: all hardware threads); tokens are split over them, and
+ * the head sums of grad_B / grad_Q are formed in head order (deterministic). */
+int ttc_lqr_forward_host(const float* A_diag, const float* B, const float* Q, const float* R_inv,
+                         const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
+                         const float* log_gamma_Q, const float* h0, int64_t n_tokens, int32_t heads, int32_t d,
+                         int32_t du, int32_t T, float* u, int32_t* status, int32_t n_threads);
+
+int ttc_lqr_backward_host(const float* A_diag, const float* B, const float* Q, const float* R_inv,
+                          const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
+                          const float* log_gamma_Q, const float* h0, const float* d_u, int64_t n_tokens,
+                          int32_t heads, int32_t d, int32_t du, int32_t T, float* grad_A_diag, float* grad_B,
+                          float* grad_Q, float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A,
+                          float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0, float grad_limit,
+                          int32_t* status, int32_t n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,7 +33,7 @@ def test_header_declares_expected_entry_points():
         "ttc_lqr_compact_stash_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
-        "ttc_lqr_rescale_backward"])
+        "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host"])
 
 
 def test_library_exports_every_declared_symbol(L):

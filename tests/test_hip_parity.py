@@ -282,10 +282,106 @@ def test_wide_symplectic_stress(d, H, T):
                precision="fp32")
 
 
-@pytest.mark.parametrize("cfg,T", [(5, 64), (5, 1024), ("5b", 1024)])
-def test_config5_stress(cfg, T):
-    x = make_x(cfg, n_tokens=4, seed=5)
+@pytest.mark.parametrize("cfg,T,seed", [(5, 64, 5), (5, 1024, 5), ("5b", 1024, 55)])
+def test_config5_stress(cfg, T, seed):
+    """Config 5 / 5b share the layer and the log-normal token scales; 5b draws its own tokens
+    (another seed), so the two cases cover different problems."""
+    x = make_x(cfg, n_tokens=4, seed=seed)
     check_case(f"cfg{cfg}", layer_solver_inputs(cfg, x), T, grad_limit=math.inf)
+
+
+@pytest.mark.parametrize("cfg,n_tok,d_pad", [(4, 1, None), (4, 1, 24)])
+def test_fp64_stable_backward_d32(cfg, n_tok, d_pad):
+    """The fp64 stable path at d = 32 (lqr_bwd_kernel<32, double>): a config-4 slice, and the
+    same problems cut to d = du = 24 (padded to 32 inside), both against the fp64 oracle."""
+    x = make_x(cfg, n_tokens=n_tok, seed=9)
+    ins = layer_solver_inputs(cfg, x)
+    if d_pad is not None:
+        k = d_pad
+        A, B, Q, R, Qf, lA, lB, lQ, h0 = ins
+        ins = [t.contiguous() for t in (A[..., :k], B[:, :k, :k], Q[:, :k, :k], R[..., :k], Qf[:, :, :k, :k], lA,
+                                        lB[..., :k], lQ[..., :k], h0[..., :k])]
+    out = check_case(f"cfg{cfg}-fp64-stable-d{d_pad or 32}", ins, CONFIGS[cfg]["T"], precision="fp64", stable=True)
+    assert out["_fallback"] == out["u"].shape[0] * out["u"].shape[1]
+
+
+def _guard_inputs(H, T):
+    """Long, barely discounted horizons with a small A_diag: the log-discount gradients (with
+    their (t+1) factor) exceed every gradient the reference's guard covers."""
+    ins = bench_solver_inputs(2, H, 16, seed=5)
+    ins[0] = ins[0] * 0.1
+    ins[5], ins[6], ins[7] = ins[5] * 0.005, ins[6] * 0.005, ins[7] * 0.005
+    return ins
+
+
+@pytest.mark.parametrize("H,precision,stable", [(8, "fp32", False), (16, "fp32", False), (2, "fp32", False),
+                                                (8, "fp32", True), (8, "fp32-row", False)])
+def test_grad_guard_covers_the_reference_six(H, precision, stable):
+    """The backward's magnitude guard (fused_lqr.py:243-246) covers the gradients of A_diag, B,
+    Q, R_inv, Q_f and h0: with a limit between their largest entry and the largest log-discount
+    gradient nothing is raised; at half their largest entry the RuntimeError is.  H = 8: head
+    group = token (sums stored directly); H = 16: group sums then head sums; H = 2: row-layout
+    rollout; stable path; row-layout kernels."""
+    T = 256
+    ins = _guard_inputs(H, T)
+    dU = np.ones((2, H, 16))
+    g = run_hip(ins, T, dU, grad_limit=math.inf, precision=precision, stable=stable)
+    guarded = max(np.abs(g[k]).max() for k in ("A_diag", "B", "Q", "R_inv", "Q_f", "h0"))
+    lg = max(np.abs(g[k]).max() for k in ("lgA", "lgB", "lgQ"))
+    print(f"H={H} {precision} stable={stable}: guarded max {guarded:.3e}, log-discount max {lg:.3e}", flush=True)
+    assert lg > 1.2 * guarded
+    run_hip(ins, T, dU, grad_limit=math.sqrt(lg * guarded), precision=precision, stable=stable)
+    with pytest.raises(RuntimeError, match="backward"):
+        run_hip(ins, T, dU, grad_limit=0.5 * guarded, precision=precision, stable=stable)
+
+
+def _A0_zero_inputs(H, d=16, seed=3):
+    """a_i = -exp(-lgA) for every state of the first problem: A_0 = diag(1 + a exp(lgA)) = 0."""
+    ins = [t.clone() for t in bench_solver_inputs(2, H, d, seed=seed)]
+    ins[0][0, 0] = -torch.exp(-ins[5][0, 0])
+    return ins
+
+
+@pytest.mark.parametrize("d,H,precision,stable", [(16, 8, "fp32", False), (16, 8, "fp32-riccati", False),
+                                                  (16, 8, "fp32-row", False), (16, 8, "fp64", False),
+                                                  (16, 8, "fp32", True), (16, 2, "fp32", False),
+                                                  (32, 8, "fp32", False), (64, 8, "fp32", False)])
+def test_A0_zero(d, H, precision, stable):
+    """A_0 = 0 (SURVEY's host-forcible case; the reference's fused kernels divide by A_k):
+    symplectic, per-step Riccati, row-layout and fp64 forwards, the head-group backward (whose
+    Hamiltonian rollout divides by A_t from t = 1 on, so A_0 = 0 is reachable) and the stable
+    path, against the fp64 oracle."""
+    check_case(f"A0=0 d{d} H{H}", _A0_zero_inputs(H, d), 24, precision=precision, stable=stable)
+
+
+def test_fused_lqr_solve_reference_signature():
+    """fused_lqr_solve(..., h0, T, inv_guard) as the reference calls it (fused_lqr.py:294-304):
+    inv_guard=True is accepted and changes nothing (the reference routes it into an unused slot)."""
+    from ttc.solvers import fused_lqr_solve
+    ins = [t.cuda() for t in bench_solver_inputs(2, 8, 16, seed=2)]
+    a = fused_lqr_solve(*ins, 16, True)
+    b = fused_lqr_solve(*ins, 16)
+    assert torch.equal(a, b)
+
+
+def test_layer_parameter_gradients_match_oracle():
+    """TTCLayer(solver_impl="hip") (factored solve, fused rescale) on the GPU: gradients of
+    in_proj, out_proj, Bs and Qs against fp64 autograd of the oracle layer around the fp64
+    oracle solve, T = 16."""
+    from ttc import TTCLayer
+    from _layer_oracle import oracle_layer_grads
+    torch.manual_seed(1)
+    layer = TTCLayer(32, 32, 16, 8, 16, 16, solver_impl="hip").cuda()
+    x = torch.randn(3, 5, 32, generator=torch.Generator().manual_seed(2))
+    dy = torch.randn(3, 5, 32, generator=torch.Generator().manual_seed(3))
+    y = layer(x.cuda(), T=16)
+    (y * dy.cuda()).sum().backward()
+    ref = oracle_layer_grads(layer, x, dy, 16)
+    for name, p in (("in_proj", layer.in_proj.weight), ("out_proj", layer.out_proj.weight), ("Bs", layer.Bs),
+                    ("Qs", layer.Qs)):
+        e = _relerr(p.grad.cpu().numpy(), ref[name])
+        print(f"layer grad {name}: {e:.1e}", flush=True)
+        assert e <= TOL, name
 
 
 def test_padding_odd_dims_and_ragged_problem_count():
@@ -448,12 +544,12 @@ def test_against_committed_golden(name):
     print(f"[golden {name}] {z['meta']}", flush=True)
     out = run_hip(ins, T, z["dU"], grad_limit=math.inf)
     errs = {k: _relerr(out[k], z[f"out_{k}"]) for k in ["u"] + NAMES}
-    print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
-    # per-output tolerances where the fixture records the problem as ill-conditioned
-    # for that output (inf: the output must be finite)
-    tol = {k: float(z[f"tol_{k}"]) if f"tol_{k}" in z.files else TOL for k in errs}
+    print("   achieved rel err " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+    # one bar for every output of every fixture (north_star: 1e-4); a fixture may only
+    # tighten it, never lift it
+    tol = {k: min(float(z[f"tol_{k}"]), TOL) if f"tol_{k}" in z.files else TOL for k in errs}
     assert all(np.isfinite(out[k]).all() for k in errs), f"{name}: non-finite output"
-    bad = {k: v for k, v in errs.items() if not (v <= tol[k]) and np.isfinite(tol[k])}
+    bad = {k: v for k, v in errs.items() if not (v <= tol[k])}
     assert not bad, f"{name}: rel err above {TOL}: {bad}"
 
 

@@ -17,10 +17,12 @@ SOURCES = ["ttc_lqr_capi.hip", "ttc_lqr_d16.hip", "ttc_lqr_d16_mfma.hip", "ttc_l
            "ttc_lqr_d32_mfma.hip", "ttc_lqr_d64_mfma.hip", "ttc_lqr_d16_sym.hip",
            "ttc_lqr_factored.hip", "ttc_lqr_d16_ham.hip", "ttc_lqr_d32_ham.hip", "ttc_lqr_d64_ham.hip",
            "ttc_lqr_epilogue.hip", "ttc_lqr_stash.hip"]
+HOST_SOURCES = ["ttc_lqr_host.cpp"]  # CPU code (no GPU kernels): compiled by the host compiler
 ARCH = os.environ.get("TTC_LQR_ARCH", "gfx950")
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (some of their forms have given wrong results
 # on the GPUs this builds for; the compiler emits them from ordinary float code otherwise)
+CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-I", os.path.join(ROOT, "include")]
 HIPCC_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                "-I", os.path.join(ROOT, "include")]
@@ -47,11 +49,14 @@ def build(verbose: bool = True) -> str:
     hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
     out = os.path.join(OUT_DIR, "libttc_lqr.so")
     tmp = out + ".tmp"
-    objs = [os.path.join(obj_dir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    objs = [os.path.join(obj_dir, os.path.splitext(s)[0] + ".o") for s in SOURCES + HOST_SOURCES]
+    cxx = os.environ.get("CXX", "g++")
     cmds = [[hipcc, *HIPCC_FLAGS, "-c", os.path.join(HERE, s), "-o", o] for s, o in zip(SOURCES, objs)]
+    cmds += [[cxx, *CXX_FLAGS, "-c", os.path.join(HERE, s), "-o", o]
+             for s, o in zip(HOST_SOURCES, objs[len(SOURCES):])]
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         list(ex.map(lambda c: _run(c, verbose), cmds))
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", *objs, "-o", tmp], verbose)
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", *objs, "-lpthread", "-o", tmp], verbose)
     os.replace(tmp, out)
     return out
 

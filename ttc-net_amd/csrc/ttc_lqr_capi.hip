@@ -151,8 +151,8 @@ static StableLayout stable_layout(int64_t chunk_tokens, int H, int d, int T) {
   size_t off = 0;
   L.kst = off;  // gains K_t, fp64 where the fp64 sweeps run (d <= 32)
   off += align256(Pc * (size_t)T * d * d * (d <= 32 ? sizeof(double) : sizeof(float)));
-  L.q0s = off;
-  off += align256(Pc * (size_t)d * d * sizeof(float));
+  L.q0s = off;  // Quu_0, fp64 where the fp64 sweeps run
+  off += align256(Pc * (size_t)d * d * (d <= 32 ? sizeof(double) : sizeof(float)));
   L.traj = off;  // (h, h~, u, w) per step, fp64 where the fp64 sweeps run (d <= 32)
   off += align256(Pc * (size_t)T * d * 4 * (d <= 32 ? sizeof(double) : sizeof(float)));
   L.gBp = off;
@@ -175,11 +175,13 @@ static int fwd_d(int d, const float* a, const float* b, const float* q, const fl
 }
 
 // Gradients of every problem by the stable path, token chunk by token chunk inside ws.
+// limit: the magnitude guard of the per-problem gradients; sum_limit: that of the head sums
+// of grad_B / grad_Q (INFINITY where they are partial sums that a later head sum completes).
 static int stable_backward(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                            const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                            int64_t n_tokens, int H, int d, int T, int flags, float* gA, float* gB, float* gQ,
                            float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, char* ws,
-                           size_t ws_bytes, float limit, int32_t* status, hipStream_t s) {
+                           size_t ws_bytes, float limit, float sum_limit, int32_t* status, hipStream_t s) {
   if (ws_bytes < stable_layout(1, H, d, T).total) return TTC_LQR_EINVAL;
   int64_t chunk = 1, hi = n_tokens;  // largest token chunk whose layout fits
   while (chunk < hi) {
@@ -209,9 +211,9 @@ static int stable_backward(const float* A, const float* B, const float* Q, const
       default: return TTC_LQR_EUNSUPPORTED;
     }
     if (rc != TTC_LQR_OK) return rc;
-    rc = launch_headsum(gBp, nc, H, (int)dd, gB + n0 * dd, limit, status, s);
+    rc = launch_headsum(gBp, nc, H, (int)dd, gB + n0 * dd, sum_limit, status, s);
     if (rc != TTC_LQR_OK) return rc;
-    rc = launch_headsum(gQp, nc, H, (int)dd, gQ + n0 * dd, limit, status, s);
+    rc = launch_headsum(gQp, nc, H, (int)dd, gQ + n0 * dd, sum_limit, status, s);
     if (rc != TTC_LQR_OK) return rc;
   }
   return TTC_LQR_OK;
@@ -301,7 +303,8 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     if (n_fallback) *n_fallback = n_tokens * H;
     return stable_backward(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, d_u, n_tokens, H, d,
                            T, flags, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f, grad_log_gamma_A,
-                           grad_log_gamma_B, grad_log_gamma_Q, grad_h0, ws, workspace_bytes, grad_limit, status, s);
+                           grad_log_gamma_B, grad_log_gamma_Q, grad_h0, ws, workspace_bytes, grad_limit, grad_limit,
+                           status, s);
   }
   const bool with_stash = v1s != nullptr;
   // largest token chunk whose layout fits the workspace (the layout grows with the chunk)
@@ -365,9 +368,10 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
         hipLaunchKernelGGL(gather_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q,
                            r, qf, la, lb, lq, hz, dz, c);
         if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+        // a group's sums are the token's head sums only when H == 8
         rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 8, d, T, flags, c.gA, c.gB,
                              c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable, L.total - L.fb_stable,
-                             grad_limit, status, s);
+                             grad_limit, direct ? grad_limit : INFINITY, status, s);
         if (rc != TTC_LQR_OK) return rc;
         hipLaunchKernelGGL(scatter_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, c, gA, gR,
                            gQf, glA, glB, glQ, gh, gBg, gQg);
@@ -402,7 +406,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
       if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
       rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags, c.gA, c.gB,
                            c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable,
-                           L.total - L.fb_stable, grad_limit, status, s);
+                           L.total - L.fb_stable, grad_limit, INFINITY, status, s);  // per-problem partials
       if (rc != TTC_LQR_OK) return rc;
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
                          glB, glQ, gh, gBp, gQp);

@@ -361,10 +361,9 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   if (!adj) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
+      // the reference's guard covers A_diag, B, Q, R_inv, Q_f and h0, not the log-discounts
       flag_value<16>(fA[k], grad_limit, flags);
-      flag_value<16>(fLB[k], grad_limit, flags);
       flag_value<16>(fR[k], grad_limit, flags);
-      flag_value<16>(fLQ[k], grad_limit, flags);
       flag_value<16>(fH0[k], grad_limit, flags);
     }
     st4(gA + p * 16 + 4 * g, fA);
@@ -372,10 +371,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     st4(gRinv + p * 16 + 4 * g, fR);
     st4(glgQ + p * 16 + 4 * g, fLQ);
     st4(gh0 + p * 16 + 4 * g, fH0);
-    if (g == 0) {
-      flag_value<16>(la_sum, grad_limit, flags);
-      glgA[p] = la_sum;
-    }
+    if (g == 0) glgA[p] = la_sum;
   }
 #pragma unroll
   for (int pa = 0; pa < 2; ++pa) {
@@ -396,8 +392,10 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   float* oq = gQg + (DIRECT ? n : G) * 256;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    flag_value<16>(gB[r], grad_limit, flags);
-    flag_value<16>(gQ[r], grad_limit, flags);
+    if (DIRECT) {  // the token's head sums; otherwise headsum_kernel checks the completed sums
+      flag_value<16>(gB[r], grad_limit, flags);
+      flag_value<16>(gQ[r], grad_limit, flags);
+    }
     ob[(4 * g + r) * 16 + c] = gB[r];
     oq[(4 * g + r) * 16 + c] = gQ[r];
   }

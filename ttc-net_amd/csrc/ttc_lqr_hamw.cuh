@@ -388,10 +388,9 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
   if (!adj) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
+      // the reference's guard covers A_diag, B, Q, R_inv, Q_f and h0, not the log-discounts
       flag_value<D>(fA[k], grad_limit, flags);
-      flag_value<D>(fLB[k], grad_limit, flags);
       flag_value<D>(fR[k], grad_limit, flags);
-      flag_value<D>(fLQ[k], grad_limit, flags);
       flag_value<D>(fH0[k], grad_limit, flags);
     }
     st4(gA + p * D + r0, fA);
@@ -399,10 +398,7 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
     st4(gRinv + p * D + r0, fR);
     st4(glgQ + p * D + r0, fLQ);
     st4(gh0 + p * D + r0, fH0);
-    if (I == 0 && g == 0) {
-      flag_value<D>(la_sum, grad_limit, flags);
-      glgA[p] = la_sum;
-    }
+    if (I == 0 && g == 0) glgA[p] = la_sum;
   }
 #pragma unroll 1
   for (int pa = 0; pa < 2; ++pa) {
@@ -431,8 +427,10 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
   for (int J = 0; J < NW; ++J)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      flag_value<D>(gB[J][r], grad_limit, flags);
-      flag_value<D>(gQ[J][r], grad_limit, flags);
+      if (DIRECT) {  // the token's head sums; otherwise headsum_kernel checks the completed sums
+        flag_value<D>(gB[J][r], grad_limit, flags);
+        flag_value<D>(gQ[J][r], grad_limit, flags);
+      }
       ob[(r0 + r) * D + 16 * J + c] = gB[J][r];
       oq[(r0 + r) * D + 16 * J + c] = gQ[J][r];
     }

@@ -1,5 +1,5 @@
 #pragma once
-// ttc_lqr.hip -- gfx950 kernels + C ABI for TTC-Net's batched receding-horizon LQR solve.
+// ttc_lqr_kernels.cuh -- row-layout gfx950 kernels of TTC-Net's batched receding-horizon LQR solve.
 //
 // Problem (one per token n and head h, P = N*H problems), restating
 // ttc/solvers/torch_lqr.py:65-91 and ttc/solvers/lin_solver_lqr.py:113-212:
@@ -335,11 +335,19 @@ __device__ __forceinline__ void rpl_sweep(
     for (int k = 0; k < D; ++k) aug[k] = aug[k] * beta_i + ((k == li) ? rr_i : R(0));
 #pragma unroll
     for (int c = 0; c < D; ++c) aug[D + c] = mat[c * G::LDM + li] * alpha[c];
-    if (SM != STASH_NONE && t == 0) {
-      float qrow[D];
+    if (SM != STASH_NONE && t == 0 && valid) {
+      if constexpr (SM == STASH_GAINS && std::is_same<R, double>::value) {
+        // the stable backward's adjoint solve w_0 = -Quu_0^{-1} d_u in the sweep's arithmetic
+        R qrow[D];
 #pragma unroll
-      for (int k = 0; k < D; ++k) qrow[k] = (float)aug[k];
-      if (valid) st_global_row<D>(q0stash + (p * D + li) * D, qrow);
+        for (int k = 0; k < D; ++k) qrow[k] = aug[k];
+        st_global_row<D>(reinterpret_cast<double*>(q0stash) + (p * D + li) * D, qrow);
+      } else {
+        float qrow[D];
+#pragma unroll
+        for (int k = 0; k < D; ++k) qrow[k] = (float)aug[k];
+        st_global_row<D>(q0stash + (p * D + li) * D, qrow);
+      }
     }
 
     R mypiv;
@@ -537,7 +545,8 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   R w0_i;
   {
     R aug[D + 4];
-    ld_global_row<D>(q0stash + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
+    // Quu_0 as the forward sweep stored it (fp64 when it ran in fp64)
+    ld_global_row<D>(reinterpret_cast<const R*>(q0stash) + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
     aug[D] = dU[p * D + li];
     aug[D + 1] = aug[D + 2] = aug[D + 3] = R(0);
     R piv;
@@ -684,12 +693,11 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     wave_sync();
   }
   const R glgA_p = group_sum<D>(glgA_part, v0, li);
+  // the reference's guard covers A_diag, B, Q, R_inv, Q_f and h0 (B and Q: the head sums,
+  // checked by headsum_kernel), not the log-discounts
   flag_value<D>(gA_i, grad_limit, flags);
-  flag_value<D>(glgB_i, grad_limit, flags);
   flag_value<D>(gr_i, grad_limit, flags);
-  flag_value<D>(glgQ_i, grad_limit, flags);
   flag_value<D>(gh0_i, grad_limit, flags);
-  flag_value<D>(glgA_p, grad_limit, flags);
   if (valid) {
     gA[p * D + li] = gA_i;
     gRinv[p * D + li] = gr_i;
@@ -973,19 +981,14 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
     if (li == 0) fail_list[atomicAdd(fail_count, 1)] = (int)p;
     return;
   }
+  // the reference's guard covers A_diag, B, Q, R_inv, Q_f and h0 (B and Q: the head sums,
+  // checked by headsum_kernel), not the log-discounts
   int flags = 0;
 #pragma unroll
-  for (int c = 0; c < D; ++c) {
-    flag_value<D>(gBrow[c], grad_limit, flags);
-    flag_value<D>(gQrow[c], grad_limit, flags);
-    flag_value<D>(gq[c], grad_limit, flags);
-  }
+  for (int c = 0; c < D; ++c) flag_value<D>(gq[c], grad_limit, flags);
   flag_value<D>(gA_i, grad_limit, flags);
-  flag_value<D>(glgB_i, grad_limit, flags);
   flag_value<D>(gr_i, grad_limit, flags);
-  flag_value<D>(glgQ_i, grad_limit, flags);
   flag_value<D>(gh0_i, grad_limit, flags);
-  flag_value<D>(glgA_p, grad_limit, flags);
   gA[p * D + li] = gA_i;
   gRinv[p * D + li] = gr_i;
   glgB[p * D + li] = glgB_i;

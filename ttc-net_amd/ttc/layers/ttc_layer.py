@@ -3,8 +3,9 @@
 Same constructor arguments and semantics as the reference
 (``ttc_layer.py:25-70``, init ``:72-96``, forward ``:98-153``); the solver call
 at ``:137`` dispatches through ``LQR_SOLVER_IMPL_MAP`` (``:18-22``), which here
-holds the gfx950 HIP solver under ``"hip"`` (and the alias ``"fused"``, the
-reference's default key).  The front-end (projections, ``l2norm``, softplus and
+holds the gfx950 HIP solver under ``"hip"`` and the reference's keys ``"fused"`` (the same
+HIP solver), ``"riccati"`` and ``"kkt"`` (HIP kernels on CUDA tensors, the library's native
+host solver on CPU tensors, so the layer runs without a GPU).  The front-end (projections, ``l2norm``, softplus and
 the low-rank ``B``/``Q``/``Q_f`` mixtures) and the back-end (rescale, ``out_proj``)
 are ordinary torch ops around that call.
 
@@ -36,13 +37,18 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ..solvers.fused_lqr import fused_lqr_solve
 from ..solvers.hip_lqr import hip_lqr_solve, hip_lqr_solve_factored
+from ..solvers.torch_lqr import direct_lqr_solve, kkt_lqr_solve
 
 __all__ = ["TTCLayer", "LQR_SOLVER_IMPL_MAP", "LQR_FACTORED_IMPL_MAP", "l2norm"]
 
+# the reference's keys (ttc_layer.py:18-22) plus "hip"; "riccati" / "kkt" run on CPU tensors too
 LQR_SOLVER_IMPL_MAP = {
+    "riccati": direct_lqr_solve,
+    "kkt": kkt_lqr_solve,
+    "fused": fused_lqr_solve,
     "hip": hip_lqr_solve,
-    "fused": hip_lqr_solve,
 }
 
 # solvers that can take (coeff_B, coeff_Q, coeff_Qf, B_basis, Q_basis) in place of B, Q, Q_f

@@ -74,6 +74,11 @@ def _load():
     L.ttc_lqr_rescale.argtypes = [f32p, f32p, i64, i32, i32, i32, i32, f32p, ctypes.c_void_p]
     L.ttc_lqr_rescale_backward.restype = ctypes.c_int
     L.ttc_lqr_rescale_backward.argtypes = [f32p, f32p, f32p, i64, i32, i32, i32, i32, f32p, ctypes.c_void_p]
+    L.ttc_lqr_forward_host.restype = ctypes.c_int
+    L.ttc_lqr_forward_host.argtypes = [f32p] * 9 + [i64, i32, i32, i32, i32] + [f32p, f32p, i32]
+    L.ttc_lqr_backward_host.restype = ctypes.c_int
+    L.ttc_lqr_backward_host.argtypes = ([f32p] * 10 + [i64, i32, i32, i32, i32] + [f32p] * 9
+                                        + [ctypes.c_float, f32p, i32])
     for suffix in ("", "_bf16"):
         getattr(L, "ttc_lqr_forward_factored" + suffix).restype = ctypes.c_int
         getattr(L, "ttc_lqr_forward_factored" + suffix).argtypes = L.ttc_lqr_forward_factored.argtypes

@@ -104,13 +104,17 @@ def _pad_inputs(ins, d, du, Dp):
 def riccati_flags(precision: str, T: int, Dp: int) -> int:
     """Kernel flags for the requested Riccati arithmetic (fp64 kernels exist for d <= 32).
 
-    ``"fp32"``: the fastest fp32 kernels (matrix cores; symplectic sweep);
+    ``"fp32"``: the fastest fp32 kernels (matrix cores; symplectic sweep); ``"riccati"``:
+    as ``"auto"``, with a Riccati step at every horizon step where the sweep runs in fp32;
     ``"fp32-riccati"``: per-step Riccati on the matrix cores; ``"fp32-row"``: the
     row-layout fp32 kernels (vector ALU only, forward and the backward's rollout) -- an
     independent cross-check of the matrix-core kernels; ``"fp64"``:
     fp64 sweep; ``"auto"``: fp64 for T >= FP64_HORIZON where available, else fp32.
     """
-    assert precision in ("fp32", "fp32-riccati", "fp32-row", "fp64", "auto"), f"unknown precision {precision}"
+    assert precision in ("fp32", "fp32-riccati", "fp32-row", "fp64", "auto", "riccati"), \
+        f"unknown precision {precision}"
+    if precision == "riccati":
+        return riccati_flags("auto", T, Dp) or FLAG_RICCATI_STEPS
     if precision == "fp32-row":
         return FLAG_ROW_KERNEL
     if precision == "fp32-riccati":
@@ -236,16 +240,23 @@ class HipLQRSolveFunc(torch.autograd.Function):
 
 def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_diag: torch.Tensor,
                   Q_f: torch.Tensor, log_gamma_A: torch.Tensor, log_gamma_B: torch.Tensor,
-                  log_gamma_Q: torch.Tensor, h0: torch.Tensor, T: int, grad_limit: float = 1e6,
-                  stash: str | None = None, precision: str = "auto", stable_backward: bool = False) -> torch.Tensor:
+                  log_gamma_Q: torch.Tensor, h0: torch.Tensor, T: int, inv_guard: bool = False, *,
+                  grad_limit: float = 1e6, stash: str | None = None, precision: str = "auto",
+                  stable_backward: bool = False) -> torch.Tensor:
     """First optimal action ``u [N,H,du]`` of every (token, head) LQR problem.
 
-    Drop-in for the reference ``fused_lqr_solve`` (``fused_lqr.py:294-304``).
-    ``grad_limit``: the backward raises when a gradient reaches it (the reference's
-    1e6 guard, ``fused_lqr.py:245``); ``math.inf`` disables the magnitude check.
+    Drop-in for the reference ``fused_lqr_solve`` (``fused_lqr.py:294-304``): the same ten
+    positional inputs and ``inv_guard`` in the eleventh slot.  ``inv_guard`` has no effect
+    (as in the reference, whose ``fused_lqr_solve`` passes it into the ``cache_level`` slot of
+    ``FusedLQRSolveFunc``, ``fused_lqr.py:268,304``); the keyword-only knobs below have no
+    reference counterpart.
+    ``grad_limit``: the backward raises when a gradient of ``A_diag``, ``B``, ``Q``, ``R_inv``,
+    ``Q_f`` or ``h0`` reaches it (the reference's 1e6 guard, ``fused_lqr.py:243-246``, which
+    does not cover the log-discount gradients); ``math.inf`` disables the magnitude check.
     ``stash``: ``"auto" | "always" | "never"`` overrides ``TTC_LQR_STASH``.
-    ``precision``: ``"auto" | "fp32" | "fp32-riccati" | "fp32-row" | "fp64"`` arithmetic
-    (and, for ``"fp32-riccati"`` / ``"fp32-row"``, kernel) of the sweep; see ``riccati_flags``.
+    ``precision``: ``"auto" | "riccati" | "fp32" | "fp32-riccati" | "fp32-row" | "fp64"``
+    arithmetic (and, for ``"riccati"`` / ``"fp32-riccati"`` / ``"fp32-row"``, kernel) of the
+    sweep; see ``riccati_flags``.
     ``stable_backward``: skip the certified Hamiltonian rollout and compute every
     problem's gradients with the stable path.
     """
