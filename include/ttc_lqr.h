@@ -85,6 +85,14 @@ extern "C" {
  * backward needs no forward sweep.  Pass the same flag to both calls.  Same results to
  * fp32 rounding. */
 #define TTC_LQR_FLAG_COMPACT_STASH 16
+/* TTC_LQR_FLAG_FP64_RESCUE (d <= 32): fp64 where long horizons need it, fp32 matrix cores
+ * elsewhere.  The forward runs the fp32 symplectic sweep and recomputes the problems its
+ * certificate rejects -- the ill-conditioned ones, whose value matrices grow to ~1e17 -- with
+ * the row-layout Riccati sweep in fp64 (instead of the fp32 rescue tiers); the backward's
+ * stable path runs in fp64 as under TTC_LQR_FLAG_FP64_RICCATI.  Combined with
+ * TTC_LQR_FLAG_ROW_KERNEL or TTC_LQR_FLAG_RICCATI_STEPS (no symplectic sweep to certify), or at
+ * d = 32 with an odd head count, it acts as TTC_LQR_FLAG_FP64_RICCATI. */
+#define TTC_LQR_FLAG_FP64_RESCUE 32
 
 /* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
  * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds
@@ -113,11 +121,19 @@ size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t d
 size_t ttc_lqr_compact_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du);
 
 /* Workspace bytes ttc_lqr_backward needs to process `chunk_tokens` tokens per pass
- * (it loops over the tokens in chunks of that size).  `with_stash` != 0 when the
- * forward's stash is passed to the backward (then V_1 / Quu_0 are not recomputed).
- * Includes a fixed-size region (<= 256 MiB) for problems the certificate rejects. */
+ * (it loops over the tokens in chunks of that size) with these `flags` (the stable path's
+ * arithmetic, fp32 or fp64, sets its size).  `with_stash` != 0 when the forward's stash is
+ * passed to the backward (then V_1 / Quu_0 are not recomputed).  Includes a region of up to
+ * 256 MiB for problems the certificate rejects; any workspace beyond the size returned here
+ * widens that region, so the rejected problems are recomputed in fewer, larger passes. */
 size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
-                               int32_t with_stash);
+                               int32_t with_stash, int32_t flags);
+
+/* Bytes of the fallback region that recomputes `problems` rejected problems in one pass
+ * (their gathered inputs and gradients and the stable path's per-step gains and
+ * trajectories; about 2.6 MB per problem at d = 16, T = 1024 in fp64).  A caller that
+ * expects many rejections (long, barely discounted horizons) adds this to the workspace. */
+size_t ttc_lqr_fallback_bytes(int64_t problems, int32_t d, int32_t du, int32_t T, int32_t flags);
 
 /* Forward: u = first optimal action [N,H,du] of every problem.
  * Replaces fused_lqr_layer_fwd (ttc/solvers/fused_lqr.py:18-146).
@@ -175,10 +191,11 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
  * backward = 0 for ttc_lqr_forward_factored (the expanded B, Q, Q_f of a chunk),
  * backward != 0 for ttc_lqr_backward_factored (plus the chunk's B / Q / Q_f gradients,
  * the reduction partials and ttc_lqr_backward's own workspace); bf16 != 0 for the _bf16
- * entry points (plus fp32 copies of the chunk's inputs, gradients and the bases). */
+ * entry points (plus fp32 copies of the chunk's inputs, gradients and the bases); flags as for
+ * ttc_lqr_workspace_bytes (the backward's beyond-layout workspace widens its fallback passes). */
 size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du,
                                         int32_t b_rank, int32_t q_rank, int32_t T, int32_t with_stash,
-                                        int32_t backward, int32_t bf16);
+                                        int32_t backward, int32_t bf16, int32_t flags);
 
 /* Forward on factored inputs; u, stash, status and flags as ttc_lqr_forward.
  * workspace_bytes >= ttc_lqr_factored_workspace_bytes(1, ..., backward = 0). */

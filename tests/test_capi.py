@@ -33,7 +33,7 @@ def test_header_declares_expected_entry_points():
         "ttc_lqr_compact_stash_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
-        "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host"])
+        "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host", "ttc_lqr_fallback_bytes"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -62,7 +62,7 @@ def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 8) == 1 and L.ttc_lqr_supported_flags(32, 32, 8 | 4) == 1
-    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 32) == 0
+    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 64) == 0
     assert _fwd(L, flags=16) == 2          # the compact stash needs the factored entry points
     assert _fwd(L, d=64, du=64, flags=1) == 2
 
@@ -76,17 +76,17 @@ def test_stash_bytes_formula(L):
 
 
 def test_workspace_bytes_monotone_and_stash_smaller(L):
-    a = L.ttc_lqr_workspace_bytes(1, 8, 16, 16, 64, 0)
-    b = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 0)
-    s = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 1)
+    a = L.ttc_lqr_workspace_bytes(1, 8, 16, 16, 64, 0, 0)
+    b = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 0, 0)
+    s = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 1, 0)
     assert 0 < a < b and 0 < s < b
     # per problem: two d^2 gradient partials + list entry, plus (no stash) V_1 and Quu_0
     assert s >= 4 * 800000 * (2 * 256 + 1)
     assert b - s >= 4 * 800000 * (2 * 256)
     # the fallback region is capped (256 MiB + alignment), so large chunks grow linearly
-    c = L.ttc_lqr_workspace_bytes(200000, 8, 16, 16, 64, 1)
+    c = L.ttc_lqr_workspace_bytes(200000, 8, 16, 16, 64, 1, 0)
     assert abs((c - s) - 4 * 800000 * (2 * 256 + 1)) < 4096
-    assert L.ttc_lqr_workspace_bytes(0, 8, 16, 16, 64, 0) == 0
+    assert L.ttc_lqr_workspace_bytes(0, 8, 16, 16, 64, 0, 0) == 0
 
 
 def _fwd(L, n=1, h=1, d=16, du=16, T=1, null_inputs=False, flags=0):
@@ -123,20 +123,20 @@ def test_backward_argument_validation(L):
 def test_factored_workspace_bytes(L):
     # forward: the expanded B, Q (per token) and Q_f (per problem) of one chunk
     N, H, d, T = 1000, 8, 16, 64
-    f = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0, 0)
+    f = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0, 0, 0)
     assert 4 * N * (2 * d * d + H * d * d) <= f < 4 * N * (2 * d * d + H * d * d) + 1024
     # backward: also the chunk's gradients of B, Q, Q_f and ttc_lqr_backward's own workspace
-    b = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1, 0)
-    assert b >= 2 * f + L.ttc_lqr_workspace_bytes(N, H, d, d, T, 1)
-    assert L.ttc_lqr_factored_workspace_bytes(2 * N, H, d, d, 16, 16, T, 1, 1, 0) > b
+    b = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1, 0, 0)
+    assert b >= 2 * f + L.ttc_lqr_workspace_bytes(N, H, d, d, T, 1, 0)
+    assert L.ttc_lqr_factored_workspace_bytes(2 * N, H, d, d, 16, 16, T, 1, 1, 0, 0) > b
     # bf16 storage: plus fp32 copies of the chunk's inputs (and d_u, gradients) and of the bases
     per_in = 3 * d + 2 * d + 1 + 16              # A, R, lgB, lgQ, h0, lgA, coeff_Qf per problem
-    fb = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0, 1)
+    fb = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 0, 0, 1, 0)
     assert fb - f >= 4 * (N * H * per_in + 2 * 16 * d * d)
-    bb = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1, 1)
+    bb = L.ttc_lqr_factored_workspace_bytes(N, H, d, d, 16, 16, T, 1, 1, 1, 0)
     assert bb - b >= 4 * (N * H * (2 * per_in + d) + 4 * 16 * d * d)
     for bad in [(N, H, d, d, 0, 16), (N, H, d, d, 16, 65), (0, H, d, d, 16, 16), (N, H, 16, 32, 16, 16)]:
-        assert L.ttc_lqr_factored_workspace_bytes(*bad, T, 0, 0, 0) == 0
+        assert L.ttc_lqr_factored_workspace_bytes(*bad, T, 0, 0, 0, 0) == 0
 
 
 def test_factored_argument_validation(L):
@@ -176,6 +176,33 @@ def test_compact_stash_bytes(L):
     assert L.ttc_lqr_compact_stash_bytes(1000, 16, 64, 64) == 4 * 16000 * 2080
     assert 4 * L.ttc_lqr_compact_stash_bytes(10, 8, 64, 64) < L.ttc_lqr_stash_bytes(10, 8, 64, 64, 1) * 1.02
     # the compact layout holds the chunk's full V_1 and Quu_0 besides
-    a = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 1, 1, 0)
-    b = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 2, 1, 0)
+    a = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 1, 1, 0, 0)
+    b = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 2, 1, 0, 0)
     assert b - a >= 4 * 800 * 2 * 256
+
+
+def test_fallback_and_precision_sizing(L):
+    """The stable path's region is sized by its arithmetic: fp64 (either fp64 flag, d <= 32)
+    stores gains, Quu_0 and trajectories in doubles; fp32 runs need half of that."""
+    FP64, RESCUE, STABLE = 1, 32, 4
+    d, T = 16, 1024
+    f32 = L.ttc_lqr_fallback_bytes(100, d, d, T, 0)
+    f64 = L.ttc_lqr_fallback_bytes(100, d, d, T, FP64)
+    assert f64 == L.ttc_lqr_fallback_bytes(100, d, d, T, RESCUE)
+    # per problem and step: gains d*d, trajectory 4*d (fp64 doubles them)
+    assert 8 * 100 * T * (d * d + 4 * d) <= f64 < 8 * 100 * T * (d * d + 4 * d) + 100 * 20000
+    assert f32 < 0.6 * f64
+    assert L.ttc_lqr_fallback_bytes(200, d, d, T, FP64) > f64 > 0
+    assert L.ttc_lqr_fallback_bytes(0, d, d, T, FP64) == 0
+    # d = 64 has no fp64 kernels: the flags do not change its size
+    assert L.ttc_lqr_fallback_bytes(10, 64, 64, 128, FP64) == L.ttc_lqr_fallback_bytes(10, 64, 64, 128, 0)
+    # the backward's workspace: the main layout (with the stash: two d x d partials and a list
+    # entry per problem) plus a fallback reserve of at most 256 MiB, fp32 or fp64
+    P = 8000
+    for flags in (0, RESCUE):
+        w = L.ttc_lqr_workspace_bytes(1000, 8, d, d, 64, 1, flags)
+        assert 4 * P * (2 * d * d + 1) <= w <= 4 * P * (2 * d * d + 1) + (256 << 20) + (1 << 16)
+    # stable-path-only workspace: the stable layout for the chunk
+    ws = L.ttc_lqr_workspace_bytes(10, 8, d, d, 64, 0, STABLE | FP64)
+    assert ws >= 8 * 80 * 64 * (d * d + 4 * d)
+    assert L.ttc_lqr_supported_flags(16, 16, RESCUE) == 1 and L.ttc_lqr_supported_flags(64, 64, RESCUE) == 0

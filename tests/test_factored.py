@@ -135,7 +135,7 @@ def test_factored_token_chunks_match_single_pass(monkeypatch):
     T = 16
     dU = torch.randn(37, 8, 16, generator=torch.Generator().manual_seed(9)).double().numpy()
     one = run_factored(ins, T, dU, stash="never")
-    ws = lib.ttc_lqr_factored_workspace_bytes(5, 8, 16, 16, 16, 16, T, 0, 1, 0)
+    ws = lib.ttc_lqr_factored_workspace_bytes(5, 8, 16, 16, 16, 16, T, 0, 1, 0, 0)
     monkeypatch.setenv("TTC_LQR_WORKSPACE_BYTES", str(ws))
     many = run_factored(ins, T, dU, stash="never")
     assert np.array_equal(one["u"], many["u"])
@@ -235,7 +235,7 @@ def test_factored_bf16_token_chunks(monkeypatch):
     dU = torch.randn(30, 8, 16, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
     one = _run_grads(ins, T, dU, torch.bfloat16, stash="never")
     monkeypatch.setenv("TTC_LQR_WORKSPACE_BYTES", str(lib.ttc_lqr_factored_workspace_bytes(4, 8, 16, 16, 16, 16,
-                                                                                        T, 0, 1, 1)))
+                                                                                        T, 0, 1, 1, 0)))
     many = _run_grads(ins, T, dU, torch.bfloat16, stash="never")
     assert torch.equal(one[0], many[0])
     for k in range(1, 12):
@@ -326,7 +326,7 @@ def test_compact_stash_matches_full_stash(cfg, n_tok, monkeypatch):
     assert np.array_equal(full["u"], comp["u"])
     for k in NAMES11:
         assert _relerr(comp[k], full[k]) <= 2e-5, k
-    ws = lib.ttc_lqr_factored_workspace_bytes(1, H, d, d, ins[1].shape[1], ins[2].shape[1], T, 2, 1, 0)
+    ws = lib.ttc_lqr_factored_workspace_bytes(1, H, d, d, ins[1].shape[1], ins[2].shape[1], T, 2, 1, 0, 0)
     monkeypatch.setenv("TTC_LQR_WORKSPACE_BYTES", str(ws))
     chunked = run_factored(ins, T, dU, stash="compact")
     assert np.array_equal(full["u"], chunked["u"])

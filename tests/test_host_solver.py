@@ -190,7 +190,8 @@ def test_grad_guard_covers_the_reference_six():
     limit, and not when only a log-discount gradient does (fused_lqr.py:243-246 checks those six)."""
     from ttc.solvers.host_lqr import host_lqr_solve
     ins = guard_inputs()
-    dU = np.ones((2, 2, 16))
+    dU = np.zeros((2, 2, 16))
+    dU[:, 0] = 1.0  # head 0 only: head 1's adjoint, hence its gradient contribution, is zero
     g = _run(host_lqr_solve, ins, GUARD_T, dU, grad_limit=math.inf)
     guarded = max(np.abs(g[k]).max() for k in GUARDED)
     lg = max(np.abs(g[k]).max() for k in ("lgA", "lgB", "lgQ"))

@@ -141,20 +141,26 @@ static int launch_headsum(const float* part, int64_t N, int H, int DD, float* ou
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // ---- stable path: gains recomputed (or stashed), closed-loop costates ----------------
+// The stable path runs in fp64 under either fp64 flag (kernels for d <= 32).
+static bool fp64_stable(int flags, int d) {
+  return (flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE)) != 0 && d <= 32;
+}
+
 struct StableLayout {
   size_t kst, q0s, traj, gBp, gQp, total;
 };
 
-static StableLayout stable_layout(int64_t chunk_tokens, int H, int d, int T) {
+static StableLayout stable_layout(int64_t chunk_tokens, int H, int d, int T, bool fp64) {
   const size_t Pc = (size_t)chunk_tokens * (size_t)H;
+  const size_t e = fp64 ? sizeof(double) : sizeof(float);  // the sweep's arithmetic
   StableLayout L{};
   size_t off = 0;
-  L.kst = off;  // gains K_t, fp64 where the fp64 sweeps run (d <= 32)
-  off += align256(Pc * (size_t)T * d * d * (d <= 32 ? sizeof(double) : sizeof(float)));
-  L.q0s = off;  // Quu_0, fp64 where the fp64 sweeps run
-  off += align256(Pc * (size_t)d * d * (d <= 32 ? sizeof(double) : sizeof(float)));
-  L.traj = off;  // (h, h~, u, w) per step, fp64 where the fp64 sweeps run (d <= 32)
-  off += align256(Pc * (size_t)T * d * 4 * (d <= 32 ? sizeof(double) : sizeof(float)));
+  L.kst = off;  // gains K_t
+  off += align256(Pc * (size_t)T * d * d * e);
+  L.q0s = off;  // Quu_0
+  off += align256(Pc * (size_t)d * d * e);
+  L.traj = off;  // (h, h~, u, w) per step
+  off += align256(Pc * (size_t)T * d * 4 * e);
   L.gBp = off;
   off += align256(Pc * (size_t)d * d * sizeof(float));
   L.gQp = off;
@@ -182,18 +188,19 @@ static int stable_backward(const float* A, const float* B, const float* Q, const
                            int64_t n_tokens, int H, int d, int T, int flags, float* gA, float* gB, float* gQ,
                            float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, char* ws,
                            size_t ws_bytes, float limit, float sum_limit, int32_t* status, hipStream_t s) {
-  if (ws_bytes < stable_layout(1, H, d, T).total) return TTC_LQR_EINVAL;
+  const bool fp64 = fp64_stable(flags, d);
+  if (ws_bytes < stable_layout(1, H, d, T, fp64).total) return TTC_LQR_EINVAL;
   int64_t chunk = 1, hi = n_tokens;  // largest token chunk whose layout fits
   while (chunk < hi) {
     const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (stable_layout(mid, H, d, T).total <= ws_bytes) chunk = mid;
+    if (stable_layout(mid, H, d, T, fp64).total <= ws_bytes) chunk = mid;
     else hi = mid - 1;
   }
   const int64_t dd = (int64_t)d * d;
   for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H, Pc = nc * H;
-    const StableLayout L = stable_layout(nc, H, d, T);
+    const StableLayout L = stable_layout(nc, H, d, T, fp64);
     const float *a = A + p0 * d, *b = B + n0 * dd, *q = Q + n0 * dd, *r = R + p0 * d, *qf = Qf + p0 * dd;
     const float *la = lA + p0, *lb = lB + p0 * d, *lq = lQ + p0 * d, *hz = h0 + p0 * d, *dz = dU + p0 * d;
     float* kst = reinterpret_cast<float*>(ws + L.kst);
@@ -201,7 +208,6 @@ static int stable_backward(const float* A, const float* B, const float* Q, const
     int rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, Pc, H, T, nullptr, kst, q0s, kStashGains, nullptr, s, flags);
     if (rc != TTC_LQR_OK) return rc;
     void* traj = ws + L.traj;
-    const bool fp64 = (flags & TTC_LQR_FLAG_FP64_RICCATI) && d <= 32;
     float* gBp = reinterpret_cast<float*>(ws + L.gBp);
     float* gQp = reinterpret_cast<float*>(ws + L.gQp);
     switch (d) {
@@ -226,21 +232,52 @@ static size_t compact_floats(int d, int du) {  // inputs + gradients of one prob
   return in + out;
 }
 
-static int64_t fallback_capacity(int64_t Pc, int d, int du, int T) {
-  const size_t per = compact_floats(d, du) * sizeof(float) + 19 * 256 + stable_layout(1, 1, d, T).total;
-  // up to 1 GiB: at long horizons a rejected problem needs MBs of gain stash, and each
-  // chunk of rejected problems costs one serial T-step sweep
-  int64_t cap = (int64_t)((size_t)1024 << 20) / (int64_t)per;
-  if (cap < 8) cap = 8;  // at least one head group of 8 (the d = 16 matrix-core backward's unit)
-  return Pc < cap ? Pc : cap;
+// The 19 compact arrays (inputs and gradients) of F gathered problems.
+static size_t compact_sizes(int64_t F64, int d, int du, size_t (&sizes)[19]) {
+  const size_t F = (size_t)F64;
+  const size_t v[19] = {F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d, F * du,
+                        F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d};
+  size_t total = 0;
+  for (int k = 0; k < 19; ++k) {
+    sizes[k] = v[k];
+    total += align256(v[k] * sizeof(float));
+  }
+  return total;
 }
 
+// Bytes of the fallback region for F rejected problems: their compact inputs and gradients,
+// then the stable path's layout for all of them in one pass.
+static size_t fallback_bytes(int64_t F, int d, int du, int T, bool fp64) {
+  size_t sizes[19];
+  return compact_sizes(F, d, du, sizes) + stable_layout(F, 1, d, T, fp64).total;
+}
+
+// Rejected problems one fallback pass can take within `bytes`: a multiple of 8 (the head
+// group of the matrix-core backward), at least 8.
+static int64_t fallback_capacity(size_t bytes, int d, int du, int T, bool fp64) {
+  if (bytes > ((size_t)1 << 50)) bytes = (size_t)1 << 50;  // keeps the products below in range
+  if (fallback_bytes(8, d, du, T, fp64) > bytes) return 8;
+  int64_t fit = 1;  // in units of 8 problems: 8 * fit fits, 16 * fit does not
+  while (fallback_bytes(16 * fit, d, du, T, fp64) <= bytes) fit *= 2;
+  int64_t lo = fit, hi = 2 * fit - 1;
+  while (lo < hi) {
+    const int64_t mid = lo + (hi - lo + 1) / 2;
+    if (fallback_bytes(8 * mid, d, du, T, fp64) <= bytes) lo = mid;
+    else hi = mid - 1;
+  }
+  return 8 * lo;
+}
+
+// Fallback region reserved by the workspace size queries; a larger workspace gives the
+// fallback larger passes (backward_core uses whatever the main chunk leaves).
+constexpr size_t kFallbackReserve = (size_t)256 << 20;
+
 struct FastLayout {
-  size_t v1, q0, gBp, gQp, list, cnt, fb, fb_stable, total;
-  int64_t F;
+  size_t v1, q0, gBp, gQp, list, cnt, fb, total;
+  int64_t F;  // fallback capacity within the reserve
 };
 
-static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash) {
+static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash, bool fp64) {
   const size_t Pc = (size_t)chunk_tokens * (size_t)H;
   FastLayout L{};
   size_t off = 0;
@@ -256,23 +293,16 @@ static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T,
   off += align256(Pc * sizeof(int32_t));
   L.cnt = off;
   off += 256;
-  L.F = fallback_capacity((int64_t)Pc, d, du, T);
   L.fb = off;
-  // 19 compact arrays, each rounded up to 256 bytes
-  const size_t F = (size_t)L.F;
-  const size_t sizes[19] = {F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d, F * du,
-                            F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d};
-  for (size_t k = 0; k < 19; ++k) off += align256(sizes[k] * sizeof(float));
-  L.fb_stable = off;
-  off += stable_layout(L.F, 1, d, T).total;
-  L.total = off;
+  const int64_t cap = fallback_capacity(kFallbackReserve, d, du, T, fp64);
+  L.F = (int64_t)Pc < cap ? (int64_t)Pc : cap;
+  L.total = off + fallback_bytes(L.F, d, du, T, fp64);
   return L;
 }
 
 static Compact compact_at(char* base, int64_t F64, int d, int du) {
-  const size_t F = (size_t)F64;
-  const size_t sizes[19] = {F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d, F * du,
-                            F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d};
+  size_t sizes[19];
+  compact_sizes(F64, d, du, sizes);
   float* ptr[19];
   size_t off = 0;
   for (int k = 0; k < 19; ++k) {
@@ -299,6 +329,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
                          float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0, char* ws,
                          size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
                          hipStream_t s) {
+  const bool fp64 = fp64_stable(flags, d);
   if (flags & TTC_LQR_FLAG_STABLE_BWD) {
     if (n_fallback) *n_fallback = n_tokens * H;
     return stable_backward(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, d_u, n_tokens, H, d,
@@ -308,11 +339,11 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
   }
   const bool with_stash = v1s != nullptr;
   // largest token chunk whose layout fits the workspace (the layout grows with the chunk)
-  if (workspace_bytes < fast_layout(1, H, d, du, T, with_stash).total) return TTC_LQR_EINVAL;
+  if (workspace_bytes < fast_layout(1, H, d, du, T, with_stash, fp64).total) return TTC_LQR_EINVAL;
   int64_t chunk = 1, hi = n_tokens;
   while (chunk < hi) {
     const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (fast_layout(mid, H, d, du, T, with_stash).total <= workspace_bytes) chunk = mid;
+    if (fast_layout(mid, H, d, du, T, with_stash, fp64).total <= workspace_bytes) chunk = mid;
     else hi = mid - 1;
   }
   const int64_t dd = (int64_t)d * d;
@@ -321,7 +352,13 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
   for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H, Pc = nc * H;
-    const FastLayout L = fast_layout(nc, H, d, du, T, with_stash);
+    const FastLayout L = fast_layout(nc, H, d, du, T, with_stash, fp64);
+    // rejected problems per fallback pass: whatever the workspace holds beyond the main layout
+    int64_t Frun = fallback_capacity(workspace_bytes - L.fb, d, du, T, fp64);
+    if (Frun < L.F) Frun = L.F;
+    if (Frun > Pc) Frun = Pc;
+    size_t csz[19];
+    const size_t fb_stable = L.fb + compact_sizes(Frun, d, du, csz);
     const float *a = A_diag + p0 * d, *b = B + n0 * dd, *q = Q + n0 * dd, *r = R_inv + p0 * du;
     const float *qf = Q_f + p0 * dd, *la = log_gamma_A + p0, *lb = log_gamma_B + p0 * du;
     const float *lq = log_gamma_Q + p0 * d, *hz = h0 + p0 * d, *dz = d_u + p0 * du, *uz = u + p0 * du;
@@ -346,7 +383,10 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
     hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
-    if (H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL)) {
+    // long horizons in fp64 (fp64 flags): the rollout per problem in fp64 on the row layout, which
+    // accepts far more of their problems than the fp32 head-group rollout (a rejected group is
+    // recomputed whole by the stable path, each pass of which is a serial T-step sweep)
+    if (H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL) && !fp64) {
       // head groups of 8 on the matrix cores: grad_B / grad_Q summed inside the kernel
       // (straight into the outputs when a group is a token, H == 8)
       const bool direct = H == 8;
@@ -361,8 +401,8 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
       if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
       if (nfail < 0 || nfail > Pc / 8) return TTC_LQR_ELAUNCH;
       total_fb += 8 * (int64_t)nfail;
-      const Compact c = compact_at(ws + L.fb, L.F, d, du);
-      const int64_t Fg = L.F / 8;  // groups per fallback batch
+      const Compact c = compact_at(ws + L.fb, Frun, d, du);
+      const int64_t Fg = Frun / 8;  // groups per fallback batch
       for (int64_t f0 = 0; f0 < nfail; f0 += Fg) {
         const int64_t fc = (f0 + Fg <= nfail) ? Fg : (nfail - f0);
         hipLaunchKernelGGL(gather_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q,
@@ -370,7 +410,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
         if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
         // a group's sums are the token's head sums only when H == 8
         rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 8, d, T, flags, c.gA, c.gB,
-                             c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable, L.total - L.fb_stable,
+                             c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable, workspace_bytes - fb_stable,
                              grad_limit, direct ? grad_limit : INFINITY, status, s);
         if (rc != TTC_LQR_OK) return rc;
         hipLaunchKernelGGL(scatter_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, c, gA, gR,
@@ -386,9 +426,9 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
       continue;
     }
     switch (d) {
-      case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
-      case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
-      case 64: rc = launch_ham_d64(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s); break;
+      case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64); break;
+      case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64); break;
+      case 64: rc = launch_ham_d64(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64); break;
       default: return TTC_LQR_EUNSUPPORTED;
     }
     if (rc != TTC_LQR_OK) return rc;
@@ -398,15 +438,15 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
     if (nfail < 0 || nfail > Pc) return TTC_LQR_ELAUNCH;
     total_fb += nfail;
-    const Compact c = compact_at(ws + L.fb, L.F, d, du);
-    for (int64_t f0 = 0; f0 < nfail; f0 += L.F) {
-      const int64_t fc = (f0 + L.F <= nfail) ? L.F : (nfail - f0);
+    const Compact c = compact_at(ws + L.fb, Frun, d, du);
+    for (int64_t f0 = 0; f0 < nfail; f0 += Frun) {
+      const int64_t fc = (f0 + Frun <= nfail) ? Frun : (nfail - f0);
       hipLaunchKernelGGL(gather_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q, r, qf, la,
                          lb, lq, hz, dz, c);
       if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
       rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags, c.gA, c.gB,
-                           c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + L.fb_stable,
-                           L.total - L.fb_stable, grad_limit, INFINITY, status, s);  // per-problem partials
+                           c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable,
+                           workspace_bytes - fb_stable, grad_limit, INFINITY, status, s);  // per-problem partials
       if (rc != TTC_LQR_OK) return rc;
       hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
                          glB, glQ, gh, gBp, gQp);
@@ -445,7 +485,7 @@ static void io_counts(int64_t nc, int H, int d, int du, int rb, int rq, size_t (
 // full V_1 and Quu_0 the chunk then holds in v1t / q0t, in the forward before packing and in
 // the backward after unpacking).
 static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                              bool backward, bool bf16, bool compact = false) {
+                              bool backward, bool bf16, bool compact, bool fp64) {
   const size_t N = (size_t)nc, P = (size_t)nc * (size_t)H, Eb = (size_t)d * du, Eq = (size_t)d * d;
   const size_t nbas = (size_t)rb * Eb + (size_t)rq * Eq;
   FactLayout L{};
@@ -498,7 +538,8 @@ static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, 
     L.inner = off;
     // ttc_lqr_backward's workspace for this chunk in one pass; the stable path (flag
     // TTC_LQR_FLAG_STABLE_BWD) splits the chunk further inside it (one token at least)
-    const size_t fast = fast_layout(nc, H, d, du, T, with_stash).total, stab = stable_layout(1, H, d, T).total;
+    const size_t fast = fast_layout(nc, H, d, du, T, with_stash, fp64).total;
+    const size_t stab = stable_layout(1, H, d, T, fp64).total;
     off += fast > stab ? fast : stab;
   }
   L.total = off;
@@ -513,12 +554,13 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Largest token chunk whose factored layout fits ws_bytes (0 when not even one token fits).
 static int64_t fact_chunk(int64_t n_tokens, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                          bool backward, bool bf16, bool compact, size_t ws_bytes) {
-  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward, bf16, compact).total > ws_bytes) return 0;
+                          bool backward, bool bf16, bool compact, bool fp64, size_t ws_bytes) {
+  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward, bf16, compact, fp64).total > ws_bytes) return 0;
   int64_t chunk = 1, hi = n_tokens;
   while (chunk < hi) {
     const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward, bf16, compact).total <= ws_bytes) chunk = mid;
+    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward, bf16, compact, fp64).total <= ws_bytes)
+      chunk = mid;
     else hi = mid - 1;
   }
   return chunk;
@@ -575,12 +617,13 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
                             size_t ws_bytes, int32_t* status, hipStream_t s) {
   using St = Store<TS>;
   const bool compact = stash != nullptr && (flags & TTC_LQR_FLAG_COMPACT_STASH);
-  const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact,
+  const bool fp64 = fp64_stable(flags, d);
+  const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, fp64,
                                    ws_bytes);
   if (chunk == 0) return TTC_LQR_EINVAL;
   const int64_t P = n_tokens * H, dd = (int64_t)d * d;
   const size_t nb = (size_t)rb * d * du, nq = (size_t)rq * d * d;
-  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact);
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, fp64);
   int rc = TTC_LQR_OK;
   float* bas = reinterpret_cast<float*>(ws + L0.bas);
   const float* Bs = St::in(B_basis, 0, nb, bas, s, rc);
@@ -588,7 +631,7 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
   for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H;
-    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact);
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, fp64);
     size_t n[10];
     io_counts(nc, H, d, du, rb, rq, n);
     auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
@@ -634,13 +677,14 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
   const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
   const bool with_stash = stash != nullptr && !stable;
   const bool compact = with_stash && (flags & TTC_LQR_FLAG_COMPACT_STASH);
+  const bool fp64 = fp64_stable(flags, d);
   flags &= ~TTC_LQR_FLAG_COMPACT_STASH;
   const int Eb = d * du, Eq = d * d;
   const size_t nb = (size_t)rb * Eb, nq = (size_t)rq * Eq;
   const int64_t chunk = fact_chunk(n_tokens > 0 ? n_tokens : 1, H, d, du, rb, rq, T, with_stash, true, St::BF16,
-                                   compact, ws_bytes);
+                                   compact, fp64, ws_bytes);
   if (chunk == 0) return TTC_LQR_EINVAL;
-  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact);
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact, fp64);
   int rc = TTC_LQR_OK;
   float* bas = reinterpret_cast<float*>(ws + L0.bas);
   float* gbas = reinterpret_cast<float*>(ws + L0.gbas);
@@ -660,7 +704,7 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
   for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H, Pc = nc * H;
-    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact);
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact, fp64);
     size_t n[10];
     io_counts(nc, H, d, du, rb, rq, n);
     auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
@@ -706,8 +750,8 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
     }
     int64_t nfb = 0;
     rc = backward_core(a, Bx, Qx, r, Qfx, la, lb, lq, hz, u ? u + p0 * du : nullptr, dz, nc, H, d, du, T, flags, v1,
-                       q0, gA, gB, gQ, gR, gQf, glA, glB, glQ, gh, ws + L.inner, L.total - L.inner, grad_limit, status,
-                       &nfb, s);
+                       q0, gA, gB, gQ, gR, gQf, glA, glB, glQ, gh, ws + L.inner, ws_bytes - L.inner, grad_limit, status,
+                       &nfb, s);  // the workspace beyond the chunk's layout widens the fallback passes
     if (rc != TTC_LQR_OK) return rc;
     total_fb += nfb;
     // chain rule of the expansion: coefficient gradients, then the basis sums
@@ -800,9 +844,9 @@ int ttc_lqr_supported(int32_t d, int32_t du) { return (d == du && (d == 16 || d 
 
 int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if (!ttc_lqr_supported(d, du)) return 0;
-  if ((flags & TTC_LQR_FLAG_FP64_RICCATI) && d > 32) return 0;
+  if ((flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE)) && d > 32) return 0;
   const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD |
-                        TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH;
+                        TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH | TTC_LQR_FLAG_FP64_RESCUE;
   return (flags & ~known) ? 0 : 1;
 }
 
@@ -818,9 +862,16 @@ size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t d
 }
 
 size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
-                               int32_t with_stash) {
+                               int32_t with_stash, int32_t flags) {
   if (chunk_tokens <= 0 || heads <= 0 || d <= 0 || du != d || T <= 0) return 0;
-  return fast_layout(chunk_tokens, heads, d, du, T, with_stash != 0).total;
+  if (flags & TTC_LQR_FLAG_STABLE_BWD)
+    return stable_layout(chunk_tokens, heads, d, T, fp64_stable(flags, d)).total;
+  return fast_layout(chunk_tokens, heads, d, du, T, with_stash != 0, fp64_stable(flags, d)).total;
+}
+
+size_t ttc_lqr_fallback_bytes(int64_t problems, int32_t d, int32_t du, int32_t T, int32_t flags) {
+  if (problems <= 0 || d <= 0 || du != d || T <= 0) return 0;
+  return fallback_bytes(problems, d, du, T, fp64_stable(flags, d));
 }
 
 int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
@@ -870,10 +921,10 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
 
 size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t b_rank,
                                         int32_t q_rank, int32_t T, int32_t with_stash, int32_t backward,
-                                        int32_t bf16) {
+                                        int32_t bf16, int32_t flags) {
   if (chunk_tokens <= 0 || !fact_args_ok(chunk_tokens, heads, d, du, b_rank, q_rank, T) || du != d) return 0;
   return fact_layout(chunk_tokens, heads, d, du, b_rank, q_rank, T, with_stash != 0, backward != 0, bf16 != 0,
-                     with_stash == 2)
+                     with_stash == 2, fp64_stable(flags, d))
       .total;
 }
 

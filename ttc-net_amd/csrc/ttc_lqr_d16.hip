@@ -6,12 +6,18 @@ namespace ttc {
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
+  // fp64 rescue of a symplectic sweep: without a symplectic sweep to certify (the stable
+  // backward's gains, row-layout or Riccati-step kernels asked for) the sweep is fp64 throughout
+  if ((flags & TTC_LQR_FLAG_FP64_RESCUE) &&
+      (sm == STASH_GAINS || (flags & (TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_RICCATI_STEPS))))
+    flags |= TTC_LQR_FLAG_FP64_RICCATI;
   // fp32 sweeps run on the matrix cores unless the row-layout kernel is asked for: the
   // symplectic sweep by default, per-step Riccati when asked for or when every gain is
   // stored (the stable backward)
   if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL))) {
     if (sm != STASH_GAINS && !(flags & TTC_LQR_FLAG_RICCATI_STEPS))
-      return launch_fwd_d16_sym(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
+      return launch_fwd_d16_sym(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s,
+                                (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0);
     return launch_fwd_d16_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
   }
   return launch_fwd<16, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);
@@ -34,7 +40,10 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s) {
+                  hipStream_t s, bool fp64) {
+  if (fp64)
+    return launch_ham<16, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
   return launch_ham<16>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
                        glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
 }

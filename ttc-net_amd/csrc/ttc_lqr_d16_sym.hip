@@ -1,5 +1,6 @@
 // ttc_lqr_d16_sym.hip -- launcher of the d = du = 16 symplectic matrix-core forward kernel
-// and its rescue pass (the per-step Riccati kernel on the problems the certificate rejects).
+// and its rescue pass (the per-step Riccati kernel on the problems the certificate rejects, or
+// the fp64 row-layout sweep under TTC_LQR_FLAG_FP64_RESCUE).
 #include "ttc_lqr_mfma_blk.cuh"
 
 namespace ttc {
@@ -7,7 +8,7 @@ namespace ttc {
 template <int SM, bool WU>
 static void launch_s16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                       float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
+                       float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool fp64_rescue) {
   using G = MB<16, 4, 1, true>;
   using GT = MB<16, 4, 1, true, true>;
   const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
@@ -18,6 +19,12 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
   else
     hipLaunchKernelGGL((lqr_fwd_blk_kernel<16, 4, 1, SM, WU, true>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf,
                        lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+  if (fp64_rescue) {
+    // long horizons: the rejected problems are the ill-conditioned ones, recomputed by the
+    // pivoted row-layout sweep in fp64
+    launch_rescue_k<16, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    return;
+  }
   // rescue: the per-step Riccati kernel on the marked problems (its own breakdown guard
   // finishes on the pivoted row-layout sweep)
   const int64_t groups = (P + 3) / 4;
@@ -30,17 +37,18 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
 // Riccati kernels.
 int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                       int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s) {
+                       int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
+                       bool fp64_rescue) {
   if (P <= 0) return TTC_LQR_OK;
   switch (sm) {
     case STASH_NONE:
-      launch_s16<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+      launch_s16<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue);
       break;
     case STASH_V1:
       if (u != nullptr)
-        launch_s16<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+        launch_s16<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue);
       else
-        launch_s16<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+        launch_s16<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue);
       break;
     default:
       return TTC_LQR_EINVAL;

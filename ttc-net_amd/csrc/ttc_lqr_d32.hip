@@ -9,9 +9,13 @@ int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* 
   // fp32 sweeps without per-step gains run on the matrix cores unless the row-layout kernel
   // is asked for: the certified symplectic sweep by default (even head counts), per-step
   // Riccati when asked for
+  // fp64 rescue of a symplectic sweep (even head counts); otherwise fp64 throughout
+  if ((flags & TTC_LQR_FLAG_FP64_RESCUE) &&
+      (sm == STASH_GAINS || (flags & (TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_RICCATI_STEPS)) || H % 2 != 0))
+    flags |= TTC_LQR_FLAG_FP64_RICCATI;
   if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL)) && sm != STASH_GAINS)
     return launch_fwd_d32_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s,
-                               !(flags & TTC_LQR_FLAG_RICCATI_STEPS));
+                               !(flags & TTC_LQR_FLAG_RICCATI_STEPS), (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0);
   return launch_fwd<32, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);
 }
 
@@ -32,7 +36,10 @@ int launch_ham_d32(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s) {
+                  hipStream_t s, bool fp64) {
+  if (fp64)
+    return launch_ham<32, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
   return launch_ham<32>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
                        glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
 }

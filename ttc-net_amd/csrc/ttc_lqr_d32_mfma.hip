@@ -24,7 +24,18 @@ static void launch_b32_w(const float* A, const float* B, const float* Q, const f
 template <int SM, bool WU>
 static void launch_b32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                       float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool sym) {
+                       float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool sym,
+                       bool fp64_rescue) {
+  if (fp64_rescue) {
+    // long horizons (even head counts): the symplectic sweep, its rejected problems recomputed
+    // by the pivoted row-layout sweep in fp64
+    if (H % 8 == 0)
+      launch_b32_w<SM, WU, 2, 4, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    else
+      launch_b32_w<SM, WU, 2, 1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    launch_rescue_k<32, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    return;
+  }
   if (sym && H % 2 == 0) {
     // H % 8 == 0: 4-wave workgroups of one token share its B, B' and Q in LDS
     if (H % 8 == 0)
@@ -49,17 +60,20 @@ static void launch_b32(const float* A, const float* B, const float* Q, const flo
 int launch_fwd_d32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                        bool sym) {
+                        bool sym, bool fp64_rescue) {
   if (P <= 0) return TTC_LQR_OK;
+  if (fp64_rescue && H % 2 != 0) return TTC_LQR_EINVAL;  // the symplectic sweep pairs heads of one token
   switch (sm) {
     case STASH_NONE:
-      launch_b32<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym);
+      launch_b32<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym, fp64_rescue);
       break;
     case STASH_V1:
       if (u != nullptr)
-        launch_b32<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym);
+        launch_b32<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym,
+                                   fp64_rescue);
       else
-        launch_b32<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym);
+        launch_b32<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym,
+                                    fp64_rescue);
       break;
     default:
       return TTC_LQR_EINVAL;

@@ -10,13 +10,16 @@ namespace ttc {
 int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s);
+// fp64_rescue: the problems the symplectic sweep's certificate rejects are recomputed by the
+// fp64 row-layout sweep (TTC_LQR_FLAG_FP64_RESCUE) instead of the fp32 rescue tiers.
 int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                       int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s);
+                       int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
+                       bool fp64_rescue);
 int launch_fwd_d32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                        bool sym);
+                        bool sym, bool fp64_rescue);
 int launch_fwd_d64_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
@@ -29,12 +32,13 @@ int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* status, hipStream_t s);
+// fp64: the row-layout Hamiltonian rollout in fp64 (long horizons, TTC_LQR_FLAG_FP64_*)
 int launch_ham_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s);
+                  hipStream_t s, bool fp64);
 int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
@@ -48,7 +52,7 @@ int launch_ham_d32(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s);
+                  hipStream_t s, bool fp64);
 int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
@@ -62,7 +66,7 @@ int launch_ham_d64(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s);
+                  hipStream_t s, bool fp64);
 // d = 16 Hamiltonian backward on the matrix cores over head groups of 8 (H % 8 == 0):
 // writes the group sums of grad_B / grad_Q to gBg / gQg ([P/8, 16, 16]; when H == 8 a group
 // is a token and gBg / gQg may be the final outputs) and lists rejected groups.

@@ -245,6 +245,72 @@ __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& my
   }
 }
 
+// LU factorisation with partial pivoting of the D x D left block of the augmented rows,
+// then back substitution: the same contract as gauss_jordan (the lane with pivot position
+// `pos` ends with row `pos` of left^{-1} right in aug[D..W), times `mypiv`, here 1).
+// Gauss-Jordan eliminates above the pivot too; its solutions are as accurate, but its
+// residuals can be larger by a factor cond(left), and the Riccati update's Schur complement
+// V - W Quu^{-1} W' inherits the residual: on long, barely discounted horizons with expensive
+// control (cond(Quu) ~ 1e20) fp64 Gauss-Jordan lost two more digits of the gradients than
+// LU.  The fp64 sweeps use this one.
+template <int D, int W, typename R>
+__device__ __forceinline__ void lu_rows(R (&aug)[W], int li, R* prow, R& mypiv, int& pos) {
+  constexpr unsigned kIdxBits = (D == 16) ? 4u : (D == 32 ? 5u : 6u);
+  constexpr unsigned kIdxMask = (1u << kIdxBits) - 1u;
+  constexpr int VN = V16<R>::N;
+  bool done = false;
+  mypiv = R(1);
+  pos = 0;
+#pragma unroll
+  for (int k = 0; k < D; ++k) {
+    const unsigned key = done ? 0u : ((mag_key(aug[k]) & ~kIdxMask) | (unsigned)(D - 1 - li));
+    const unsigned best = group_max_u32<D>(key);
+    const bool me = (D - 1 - (int)(best & kIdxMask)) == li;
+    if (me) {
+#pragma unroll
+      for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::st(prow + c, aug + c);
+    }
+    wave_sync();
+    R pr[W];
+#pragma unroll
+    for (int c = (k & ~(VN - 1)); c < W; c += VN) V16<R>::ld(prow + c, pr + c);
+    // rows already used as pivots keep their U row: only the remaining rows are eliminated
+    const R f = (me || done) ? R(0) : aug[k] / pr[k];
+#pragma unroll
+    for (int c = k + 1; c < W; ++c) aug[c] = fma(-f, pr[c], aug[c]);
+    if (me) { pos = k; done = true; }
+    wave_sync();  // next pivot row may overwrite prow
+  }
+  // back substitution, last pivot first: x_k = (rhs_k - sum_{j>k} U_kj x_j) / U_kk
+#pragma unroll
+  for (int k = D - 1; k >= 0; --k) {
+    if (pos == k) {
+      const R iu = R(1) / aug[k];
+#pragma unroll
+      for (int c = D; c < W; ++c) aug[c] *= iu;
+#pragma unroll
+      for (int c = D; c < W; c += VN) V16<R>::st(prow + c, aug + c);
+    }
+    wave_sync();
+    if (pos < k) {
+      R x[W - D];
+#pragma unroll
+      for (int c = 0; c < W - D; c += VN) V16<R>::ld(prow + D + c, x + c);
+      const R u = aug[k];  // U[pos][k]
+#pragma unroll
+      for (int c = 0; c < W - D; ++c) aug[D + c] = fma(-u, x[c], aug[D + c]);
+    }
+    wave_sync();
+  }
+}
+
+// The pivoted solve of the row-layout kernels: LU in fp64, Gauss-Jordan in fp32.
+template <int D, int W, typename R>
+__device__ __forceinline__ void solve_rows(R (&aug)[W], int li, R* prow, R& mypiv, int& pos) {
+  if constexpr (std::is_same<R, double>::value) lu_rows<D, W>(aug, li, prow, mypiv, pos);
+  else gauss_jordan<D, W>(aug, li, prow, mypiv, pos);
+}
+
 // ---------------------------------------------------------------------------
 // Row-layout Riccati sweep from step t_start down to 0: u0 and the stash of mode SM
 // (STASH_NONE; STASH_GAINS: all gains K_t [P,T,du,d] into `kstash` and Quu_0; STASH_V1:
@@ -352,7 +418,7 @@ __device__ __forceinline__ void rpl_sweep(
 
     R mypiv;
     int pos;
-    gauss_jordan<D, 2 * D>(aug, li, prow, mypiv, pos);
+    solve_rows<D, 2 * D>(aug, li, prow, mypiv, pos);
     R x[D];  // row `pos` of X = Quu^{-1} Qux  (K = -X)
     const R ipiv = R(1) / mypiv;
 #pragma unroll
@@ -551,7 +617,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     aug[D + 1] = aug[D + 2] = aug[D + 3] = R(0);
     R piv;
     int pos;
-    gauss_jordan<D, D + 4>(aug, li, prow, piv, pos);
+    solve_rows<D, D + 4>(aug, li, prow, piv, pos);
     v0[pos] = -aug[D] / piv;
     wave_sync();
     w0_i = v0[li];
@@ -711,6 +777,13 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   }
 }
 
+// exp2 and reciprocal in the rollout's arithmetic: the hardware instructions in fp32, the
+// library functions in fp64.
+__device__ __forceinline__ float exp2r(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ double exp2r(double x) { return exp2(x); }
+__device__ __forceinline__ float rcpr(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ double rcpr(double x) { return 1.0 / x; }
+
 // ---------------------------------------------------------------------------
 // Fast backward: forward Hamiltonian rollout with a terminal certificate.
 //
@@ -732,7 +805,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
 // stable path (stored gains, closed-loop costates).  grad_B / grad_Q partials go to
 // gBp / gQp for headsum_kernel, as in lqr_bwd_kernel.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, typename R = float>
 __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
@@ -743,7 +816,8 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
     float* __restrict__ glgQ, float* __restrict__ gh0, float* __restrict__ gBp, float* __restrict__ gQp,
     float grad_limit, int* __restrict__ fail_list, int* __restrict__ fail_count, int* __restrict__ status) {
   using G = Geo<D>;
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem_f[];
+  R* const smem = reinterpret_cast<R*>(smem_f);
   const int li = threadIdx.x % D;
   const int pb = threadIdx.x / D;
   const int64_t p0 = (int64_t)blockIdx.x * G::PPB;
@@ -761,103 +835,103 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
     }
   }
   __syncthreads();
-  const float* Bs = smem + (int)(n - n0) * G::MAT;
-  float* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
-  float* v0 = S + G::MAT;  // 6 vectors of D floats, then the pivot row
-  float* v1 = v0 + D;
-  float* v2 = v1 + D;
-  float* v3 = v2 + D;
-  float* v4 = v3 + D;
-  float* v5 = v4 + D;
-  float* prow = v5 + D;    // D + 4 floats
+  const R* Bs = smem + (int)(n - n0) * G::MAT;
+  R* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
+  R* v0 = S + G::MAT;  // 6 vectors of D floats, then the pivot row
+  R* v1 = v0 + D;
+  R* v2 = v1 + D;
+  R* v3 = v2 + D;
+  R* v4 = v3 + D;
+  R* v5 = v4 + D;
+  R* prow = v5 + D;    // D + 4 floats
 
-  const float a_i = A_diag[p * D + li];
-  const float r_i = Rinv[p * D + li];
-  const float rr_i = 1.0f / r_i;
-  constexpr float kLog2e = 1.4426950408889634f;
-  const float lgB_i = lgB[p * D + li];
-  const float lgQ_i = lgQ[p * D + li];
-  const float lgA_p = lgA[p];
+  const R a_i = A_diag[p * D + li];
+  const R r_i = Rinv[p * D + li];
+  const R rr_i = R(1) / r_i;
+  constexpr R kLog2e = R(1.4426950408889634);
+  const R lgB_i = lgB[p * D + li];
+  const R lgQ_i = lgQ[p * D + li];
+  const R lgA_p = lgA[p];
   // discounts as exp2 of base-2 exponents, the arithmetic of the forward kernels
-  const float lb2_i = lgB_i * kLog2e, lq2_i = lgQ_i * kLog2e, la2_p = lgA_p * kLog2e;
-  float Brow[D], Bcol[D], Qrow[D];
+  const R lb2_i = lgB_i * kLog2e, lq2_i = lgQ_i * kLog2e, la2_p = lgA_p * kLog2e;
+  R Brow[D], Bcol[D], Qrow[D];
   {
     const float* qg = Qg + n * D * D;
 #pragma unroll
     for (int c = 0; c < D; ++c) {
       Brow[c] = Bs[li * G::LDM + c];
       Bcol[c] = Bs[c * G::LDM + li];
-      Qrow[c] = 0.5f * (qg[li * D + c] + qg[c * D + li]);
+      Qrow[c] = R(0.5) * (qg[li * D + c] + qg[c * D + li]);
     }
   }
 
   // t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (pivoted elimination)
-  float w_i;
+  R w_i;
   {
-    float aug[D + 4];
-    ld_global_row<D>(q0s + (p * D + li) * D, *reinterpret_cast<float(*)[D]>(aug));
+    R aug[D + 4];
+    ld_global_row<D>(q0s + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
     aug[D] = dU[p * D + li];
-    aug[D + 1] = aug[D + 2] = aug[D + 3] = 0.f;
-    float piv;
+    aug[D + 1] = aug[D + 2] = aug[D + 3] = R(0);
+    R piv;
     int pos;
-    gauss_jordan<D, D + 4>(aug, li, prow, piv, pos);
+    solve_rows<D, D + 4>(aug, li, prow, piv, pos);
     v0[pos] = -aug[D] / piv;
     wave_sync();
     w_i = v0[li];
     wave_sync();
   }
 
-  float h_i = h0[p * D + li], hb_i = 0.f, lam_i, lamb_i;
-  float gA_i, glgA_part, glgB_i, gr_i, gh0_i, glgQ_i = 0.f;
-  float gBrow[D], gQrow[D];
+  R h_i = h0[p * D + li], hb_i = R(0), lam_i, lamb_i;
+  R gA_i, glgA_part, glgB_i, gr_i, gh0_i, glgQ_i = R(0);
+  R gBrow[D], gQrow[D];
   {
-    const float u_i = u0g[p * D + li];
-    const float eA = __builtin_amdgcn_exp2f(la2_p);
-    const float alpha_i = fmaf(a_i, eA, 1.0f);
-    const float beta_i = __builtin_amdgcn_exp2f(lb2_i);
+    const R u_i = u0g[p * D + li];
+    const R eA = exp2r(la2_p);
+    const R alpha_i = fma(a_i, eA, R(1));
+    const R beta_i = exp2r(lb2_i);
     v2[li] = beta_i * u_i;
     v3[li] = beta_i * w_i;
     wave_sync();
-    float bu[D], bw[D];
+    R bu[D], bw[D];
     ld_row<D>(v2, bu);
     ld_row<D>(v3, bw);
-    float hn = alpha_i * h_i, hbn = 0.f;
+    R hn = alpha_i * h_i, hbn = R(0);
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      hn = fmaf(Brow[j], bu[j], hn);
-      hbn = fmaf(Brow[j], bw[j], hbn);
+      hn = fma(Brow[j], bu[j], hn);
+      hbn = fma(Brow[j], bw[j], hbn);
     }
     v0[li] = hn;
     v1[li] = hbn;
     wave_sync();
-    float hv[D], hbv[D], vrow[D];
+    R hv[D], hbv[D], vrow[D];
     ld_row<D>(v0, hv);
     ld_row<D>(v1, hbv);
     ld_global_row<D>(v1s + (p * D + li) * D, vrow);
-    float lam = 0.f, lamb = 0.f;
+    R lam = R(0), lamb = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      lam = fmaf(vrow[c], hv[c], lam);
-      lamb = fmaf(vrow[c], hbv[c], lamb);
+      lam = fma(vrow[c], hv[c], lam);
+      lamb = fma(vrow[c], hbv[c], lamb);
     }
     v4[li] = lam;
     v5[li] = lamb;
     wave_sync();
-    float lv[D], lbv[D];
+    R lv[D], lbv[D];
     ld_row<D>(v4, lv);
     ld_row<D>(v5, lbv);
-    float btl = 0.f, btlb = 0.f;
+    R btl = R(0), btlb = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      gBrow[c] = fmaf(lamb, bu[c], lam * bw[c]);  // torch_lqr.py:53 chained through B_0 = B diag(beta_0)
-      gQrow[c] = 0.f;
-      btl = fmaf(Bcol[c], lv[c], btl);
-      btlb = fmaf(Bcol[c], lbv[c], btlb);
+      gBrow[c] = fma(lamb, bu[c], lam * bw[c]);  // torch_lqr.py:53 chained through B_0 = B diag(beta_0)
+      gQrow[c] = R(0);
+      btl = fma(Bcol[c], lv[c], btl);
+      btlb = fma(Bcol[c], lbv[c], btlb);
     }
-    const float gAt = h_i * lamb;  // h~_0 = 0   (torch_lqr.py:51)
+    const R gAt = h_i * lamb;  // h~_0 = 0   (torch_lqr.py:51)
     gA_i = gAt * eA;
     glgA_part = gAt * a_i * eA;
-    glgB_i = beta_i * fmaf(u_i, btlb, w_i * btl);
+    glgB_i = beta_i * fma(u_i, btlb, w_i * btl);
     gr_i = -u_i * w_i * rr_i * rr_i;  // d(1/R_inv)/dR_inv  (torch_lqr.py:59)
     gh0_i = alpha_i * lamb;           // torch_lqr.py:61
     h_i = hn;
@@ -868,67 +942,67 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
   }
 
   for (int t = 1; t < T; ++t) {
-    const float tf = (float)t;
+    const R tf = (R)t;
     // state cost on h_t:  Qc_t = D_t Q D_t,  D_t = diag(exp(lgQ t))   (torch_lqr.py:55 + chain rule)
-    const float q_i = __builtin_amdgcn_exp2f(lq2_i * tf);
-    const float qh_i = q_i * h_i, qhb_i = q_i * hb_i;
+    const R q_i = exp2r(lq2_i * tf);
+    const R qh_i = q_i * h_i, qhb_i = q_i * hb_i;
     v0[li] = qh_i;
     v1[li] = qhb_i;
     wave_sync();
-    float qh[D], qhb[D];
+    R qh[D], qhb[D];
     ld_row<D>(v0, qh);
     ld_row<D>(v1, qhb);
-    float Qh = 0.f, Qhb = 0.f;
+    R Qh = R(0), Qhb = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      Qh = fmaf(Qrow[c], qh[c], Qh);
-      Qhb = fmaf(Qrow[c], qhb[c], Qhb);
+      Qh = fma(Qrow[c], qh[c], Qh);
+      Qhb = fma(Qrow[c], qhb[c], Qhb);
       // twice the symmetric gradient of Qc_t (halved after the loop)
-      gQrow[c] = fmaf(qh_i, qhb[c], fmaf(qhb_i, qh[c], gQrow[c]));
+      gQrow[c] = fma(qh_i, qhb[c], fma(qhb_i, qh[c], gQrow[c]));
     }
     Qh *= q_i;
     Qhb *= q_i;
-    glgQ_i = fmaf(tf, fmaf(h_i, Qhb, hb_i * Qh), glgQ_i);
+    glgQ_i = fma(tf, fma(h_i, Qhb, hb_i * Qh), glgQ_i);
     // step t dynamics
-    const float tp1 = tf + 1.0f;
-    const float eA = __builtin_amdgcn_exp2f(la2_p * tp1);
-    const float alpha_i = fmaf(a_i, eA, 1.0f);
-    const float beta_i = __builtin_amdgcn_exp2f(lb2_i * tp1);
-    const float ia = __builtin_amdgcn_rcpf(alpha_i);
-    const float lam_n = (lam_i - Qh) * ia;
-    const float lamb_n = (lamb_i - Qhb) * ia;
+    const R tp1 = tf + R(1);
+    const R eA = exp2r(la2_p * tp1);
+    const R alpha_i = fma(a_i, eA, R(1));
+    const R beta_i = exp2r(lb2_i * tp1);
+    const R ia = rcpr(alpha_i);
+    const R lam_n = (lam_i - Qh) * ia;
+    const R lamb_n = (lamb_i - Qhb) * ia;
     v2[li] = lam_n;
     v3[li] = lamb_n;
     wave_sync();
-    float lv[D], lbv[D];
+    R lv[D], lbv[D];
     ld_row<D>(v2, lv);
     ld_row<D>(v3, lbv);
-    float btl = 0.f, btlb = 0.f;
+    R btl = R(0), btlb = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      btl = fmaf(Bcol[c], lv[c], btl);
-      btlb = fmaf(Bcol[c], lbv[c], btlb);
+      btl = fma(Bcol[c], lv[c], btl);
+      btlb = fma(Bcol[c], lbv[c], btlb);
     }
-    const float u_i = -r_i * beta_i * btl;
-    const float w_i2 = -r_i * beta_i * btlb;
+    const R u_i = -r_i * beta_i * btl;
+    const R w_i2 = -r_i * beta_i * btlb;
     v4[li] = beta_i * u_i;
     v5[li] = beta_i * w_i2;
     wave_sync();
-    float bu[D], bw[D];
+    R bu[D], bw[D];
     ld_row<D>(v4, bu);
     ld_row<D>(v5, bw);
-    float hn = alpha_i * h_i, hbn = alpha_i * hb_i;
+    R hn = alpha_i * h_i, hbn = alpha_i * hb_i;
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      hn = fmaf(Brow[j], bu[j], hn);
-      hbn = fmaf(Brow[j], bw[j], hbn);
-      gBrow[j] = fmaf(lamb_n, bu[j], fmaf(lam_n, bw[j], gBrow[j]));
+      hn = fma(Brow[j], bu[j], hn);
+      hbn = fma(Brow[j], bw[j], hbn);
+      gBrow[j] = fma(lamb_n, bu[j], fma(lam_n, bw[j], gBrow[j]));
     }
-    const float gAt = fmaf(h_i, lamb_n, hb_i * lam_n);
-    gA_i = fmaf(gAt, eA, gA_i);
-    glgA_part = fmaf(gAt * a_i, tp1 * eA, glgA_part);
-    glgB_i = fmaf(tp1 * beta_i, fmaf(u_i, btlb, w_i2 * btl), glgB_i);
-    gr_i = fmaf(-u_i * w_i2, rr_i * rr_i, gr_i);
+    const R gAt = fma(h_i, lamb_n, hb_i * lam_n);
+    gA_i = fma(gAt, eA, gA_i);
+    glgA_part = fma(gAt * a_i, tp1 * eA, glgA_part);
+    glgB_i = fma(tp1 * beta_i, fma(u_i, btlb, w_i2 * btl), glgB_i);
+    gr_i = fma(-u_i * w_i2, rr_i * rr_i, gr_i);
     h_i = hn;
     hb_i = hbn;
     lam_i = lam_n;
@@ -937,44 +1011,45 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
   }
 
 #pragma unroll
-  for (int c = 0; c < D; ++c) gQrow[c] *= 0.5f;
+  for (int c = 0; c < D; ++c) gQrow[c] *= R(0.5);
 
   // terminal cost: grad Q_f = sym(h_T h~_T'); certificate lambda_T = Q_f h_T
-  float gq[D];
-  float e1, e2, m1, m2, m3, m4;
+  R gq[D];
+  R e1, e2, m1, m2, m3, m4;
   {
     v0[li] = h_i;
     v1[li] = hb_i;
     wave_sync();
-    float hv[D], hbv[D];
+    R hv[D], hbv[D];
     ld_row<D>(v0, hv);
     ld_row<D>(v1, hbv);
     const float* qfp = Qf + p * D * D;
-    float fh = 0.f, fhb = 0.f;
+    R fh = R(0), fhb = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
-      const float qf = 0.5f * (qfp[li * D + c] + qfp[c * D + li]);
-      fh = fmaf(qf, hv[c], fh);
-      fhb = fmaf(qf, hbv[c], fhb);
-      gq[c] = 0.5f * fmaf(h_i, hbv[c], hb_i * hv[c]);
+      const R qf = R(0.5) * (qfp[li * D + c] + qfp[c * D + li]);
+      fh = fma(qf, hv[c], fh);
+      fhb = fma(qf, hbv[c], fhb);
+      gq[c] = R(0.5) * fma(h_i, hbv[c], hb_i * hv[c]);
     }
-    e1 = fabsf(lam_i - fh);
-    e2 = fabsf(lamb_i - fhb);
-    m1 = fabsf(fh) + fabsf(lam_i);
-    m2 = fabsf(fhb) + fabsf(lamb_i);
+    e1 = fabs(lam_i - fh);
+    e2 = fabs(lamb_i - fhb);
+    m1 = fabs(fh) + fabs(lam_i);
+    m2 = fabs(fhb) + fabs(lamb_i);
     wave_sync();
   }
-  const float glgA_p = group_sum<D>(glgA_part, v0, li);
+  const R glgA_p = group_sum<D>(glgA_part, v0, li);
   // every accumulator finite <=> this sum is (a sum of finite values overflows only near 1e38)
-  float fin = fabsf(gA_i) + fabsf(gr_i) + fabsf(glgB_i) + fabsf(glgQ_i) + fabsf(gh0_i) + fabsf(glgA_p);
+  R fin = fabs(gA_i) + fabs(gr_i) + fabs(glgB_i) + fabs(glgQ_i) + fabs(gh0_i) + fabs(glgA_p);
 #pragma unroll
-  for (int c = 0; c < D; ++c) fin += fabsf(gBrow[c]) + fabsf(gQrow[c]) + fabsf(gq[c]);
+  for (int c = 0; c < D; ++c) fin += fabs(gBrow[c]) + fabs(gQrow[c]) + fabs(gq[c]);
   // group maxima of non-negative floats via their bit patterns (NaN sorts above +inf)
-  const float E1 = __uint_as_float(group_max_u32<D>(__float_as_uint(e1)));
-  const float E2 = __uint_as_float(group_max_u32<D>(__float_as_uint(e2)));
-  m3 = __uint_as_float(group_max_u32<D>(__float_as_uint(m1)));
-  m4 = __uint_as_float(group_max_u32<D>(__float_as_uint(m2)));
-  const unsigned bad_lane = isfinite(fin) ? 0u : 1u;
+  const float E1 = __uint_as_float(group_max_u32<D>(__float_as_uint((float)e1)));
+  const float E2 = __uint_as_float(group_max_u32<D>(__float_as_uint((float)e2)));
+  m3 = __uint_as_float(group_max_u32<D>(__float_as_uint((float)m1)));
+  m4 = __uint_as_float(group_max_u32<D>(__float_as_uint((float)m2)));
+  // finite as stored (fp32): an fp64 rollout can leave the fp32 range while staying finite
+  const unsigned bad_lane = isfinite((float)fin) ? 0u : 1u;
   const bool ok = group_max_u32<D>(bad_lane) == 0u && E1 <= tau * m3 && E2 <= tau * m4;
   if (!valid) return;
   if (!ok) {
@@ -1012,27 +1087,51 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
 // marked problems at a time (lane li of group qo owns row li of problem qo).  With a status
 // word, the scan runs only when the forward set TTC_LQR_STATUS_RESCUED in it.
 // ---------------------------------------------------------------------------
-template <int D>
+// One rescued problem per group of D lanes: stage its B, V_T = sym(Q_f), sweep from scratch.
+template <int D, int SM, bool WRITE_U, typename R>
+__device__ __forceinline__ void rescue_one(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0, int H, int T,
+    float* __restrict__ u_out, float* __restrict__ kstash, float* __restrict__ q0stash, int* __restrict__ status,
+    R* Bs, R* S, int li, int64_t p, bool valid) {
+  const int64_t n = p / H;
+  wave_sync();
+#pragma unroll
+  for (int c = 0; c < D; ++c) Bs[li * Geo<D>::LDM + c] = (R)Bg[n * D * D + li * D + c];
+  R V[D];
+  const float* qf = Qf + p * D * D;
+#pragma unroll
+  for (int c = 0; c < D; ++c) V[c] = R(0.5) * ((R)qf[li * D + c] + (R)qf[c * D + li]);
+  wave_sync();
+  rpl_sweep<D, R, SM, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, Bs, S, li, p, valid, n, T, T - 1, V, u_out,
+                                kstash, q0stash, status);
+}
+
+template <int D, typename R = float>
 struct Rescue {
   static constexpr int PPW = 64 / D;
   static constexpr int PER = Geo<D>::MAT + Geo<D>::PER_PROB;  // B rows + rpl_sweep scratch
-  static constexpr size_t LDS_BYTES = sizeof(float) * (size_t)PPW * PER;
+  static constexpr size_t LDS_BYTES = sizeof(R) * (size_t)PPW * PER;
 };
 
-template <int D, int SM, bool WRITE_U>
+// R: the sweep's arithmetic (double after a long-horizon fp32 symplectic sweep, whose rejected
+// problems are the ill-conditioned ones that need fp64)
+template <int D, int SM, bool WRITE_U, typename R = float>
 __global__ __launch_bounds__(64) void lqr_rescue_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
     int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
     float* __restrict__ q0stash, int* __restrict__ status) {
-  constexpr int PPW = Rescue<D>::PPW;
-  extern __shared__ __align__(16) float smem[];
+  constexpr int PPW = Rescue<D, R>::PPW;
+  extern __shared__ __align__(16) float smem_rf[];
+  R* const smem = reinterpret_cast<R*>(smem_rf);
   const int lane = threadIdx.x;
   const int qo = lane / D;
   const int li = lane % D;
-  float* Bs = smem + qo * Rescue<D>::PER;
-  float* S = Bs + Geo<D>::MAT;
+  R* Bs = smem + qo * Rescue<D, R>::PER;
+  R* S = Bs + Geo<D>::MAT;
   // nothing was marked (the forward sets the bit when it marks a problem)
   if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
   const float* mark = WRITE_U ? u_out : q0stash;
@@ -1047,29 +1146,56 @@ __global__ __launch_bounds__(64) void lqr_rescue_kernel(
       const bool valid = m != 0ull;
       const int64_t p = base + (valid ? (__ffsll((long long)m) - 1) : (__ffsll((long long)mask) - 1));
       for (int k = 0; k < PPW && mask != 0ull; ++k) mask &= mask - 1ull;
-      const int64_t n = p / H;
-      wave_sync();
-#pragma unroll
-      for (int c = 0; c < D; ++c) Bs[li * Geo<D>::LDM + c] = Bg[n * D * D + li * D + c];
-      float V[D];
-      const float* qf = Qf + p * D * D;
-#pragma unroll
-      for (int c = 0; c < D; ++c) V[c] = 0.5f * (qf[li * D + c] + qf[c * D + li]);
-      wave_sync();
-      rpl_sweep<D, float, SM, WRITE_U>(A_diag, Qg, Rinv, lgA, lgB, lgQ, h0, Bs, S, li, p, valid, n, T, T - 1, V,
-                                        u_out, kstash, q0stash, status);
+      rescue_one<D, SM, WRITE_U, R>(A_diag, Bg, Qg, Rinv, Qf, lgA, lgB, lgQ, h0, H, T, u_out, kstash, q0stash,
+                                    status, Bs, S, li, p, valid);
     }
   }
 }
 
-template <int D, int SM, bool WU>
+// The same rescue with one wave per group of PPW consecutive problems (a wave whose problems
+// carry no marker returns at once): every marked problem's sweep runs concurrently.  For the
+// fp64 sweeps after a long-horizon symplectic sweep, whose rejected problems cluster by token
+// (a window of 64 could hold many, each window's sweeps running back to back).
+template <int D, int SM, bool WRITE_U, typename R>
+__global__ __launch_bounds__(64) void lqr_rescue_fine_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    int64_t P, int H, int T, float* __restrict__ u_out, float* __restrict__ kstash,
+    float* __restrict__ q0stash, int* __restrict__ status) {
+  constexpr int PPW = Rescue<D, R>::PPW;
+  extern __shared__ __align__(16) float smem_rf[];
+  R* const smem = reinterpret_cast<R*>(smem_rf);
+  const int lane = threadIdx.x;
+  const int qo = lane / D;
+  const int li = lane % D;
+  R* Bs = smem + qo * Rescue<D, R>::PER;
+  R* S = Bs + Geo<D>::MAT;
+  if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
+  const float* mark = WRITE_U ? u_out : q0stash;
+  const int64_t mstride = WRITE_U ? D : (int64_t)D * D;
+  const int64_t base = (int64_t)blockIdx.x * PPW;
+  const int64_t pq = base + qo;
+  const bool valid = pq < P && isnan(mark[pq * mstride]);
+  if (__ballot(valid) == 0ull) return;
+  rescue_one<D, SM, WRITE_U, R>(A_diag, Bg, Qg, Rinv, Qf, lgA, lgB, lgQ, h0, H, T, u_out, kstash, q0stash, status,
+                                Bs, S, li, valid ? pq : base, valid);
+}
+
+template <int D, int SM, bool WU, typename RT = float>
 inline void launch_rescue_k(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                             const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                             int T, float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
+  if (std::is_same<RT, double>::value) {
+    const int64_t blocks = (P + Rescue<D, RT>::PPW - 1) / Rescue<D, RT>::PPW;
+    hipLaunchKernelGGL((lqr_rescue_fine_kernel<D, SM, WU, RT>), dim3((unsigned)blocks), dim3(64),
+                       (Rescue<D, RT>::LDS_BYTES), s, A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+    return;
+  }
   int64_t blocks = (P + 63) / 64;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL((lqr_rescue_kernel<D, SM, WU>), dim3((unsigned)blocks), dim3(64), Rescue<D>::LDS_BYTES, s, A, B,
-                     Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
+  hipLaunchKernelGGL((lqr_rescue_kernel<D, SM, WU, RT>), dim3((unsigned)blocks), dim3(64), (Rescue<D, RT>::LDS_BYTES),
+                     s, A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
 }
 
 // ---------------------------------------------------------------------------
@@ -1139,7 +1265,7 @@ inline int launch_fwd(const float* A, const float* B, const float* Q, const floa
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
-template <int D>
+template <int D, typename RT = float>
 inline int launch_ham(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                       const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
                       const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
@@ -1148,7 +1274,8 @@ inline int launch_ham(const float* A, const float* B, const float* Q, const floa
                       hipStream_t s) {
   if (P <= 0) return TTC_LQR_OK;
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
-  hipLaunchKernelGGL((lqr_ham_bwd_kernel<D>), grid, block, lds_bytes<D>(H), s, A, B, Q, R, Qf, lA, lB, lQ, h0, u0,
+  hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf, lA, lB,
+                     lQ, h0, u0,
                      dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB, glQ, gh0, gBp, gQp,
                      limit, fail_list, fail_count, status);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;

@@ -11,13 +11,14 @@ import ctypes
 import os
 
 __all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI", "FLAG_ROW_KERNEL",
-           "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS", "FLAG_COMPACT_STASH"]
+           "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS", "FLAG_COMPACT_STASH", "FLAG_FP64_RESCUE"]
 
 FLAG_FP64_RICCATI = 1  # TTC_LQR_FLAG_FP64_RICCATI
 FLAG_ROW_KERNEL = 2    # TTC_LQR_FLAG_ROW_KERNEL
 FLAG_STABLE_BWD = 4    # TTC_LQR_FLAG_STABLE_BWD
 FLAG_RICCATI_STEPS = 8  # TTC_LQR_FLAG_RICCATI_STEPS
 FLAG_COMPACT_STASH = 16  # TTC_LQR_FLAG_COMPACT_STASH
+FLAG_FP64_RESCUE = 32  # TTC_LQR_FLAG_FP64_RESCUE
 
 LIB_NAME = "libttc_lqr.so"
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -52,7 +53,9 @@ def _load():
     L.ttc_lqr_stash_bytes.restype = sz
     L.ttc_lqr_stash_bytes.argtypes = [i64, i32, i32, i32, i32]
     L.ttc_lqr_workspace_bytes.restype = sz
-    L.ttc_lqr_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32]
+    L.ttc_lqr_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32, i32]
+    L.ttc_lqr_fallback_bytes.restype = sz
+    L.ttc_lqr_fallback_bytes.argtypes = [i64, i32, i32, i32, i32]
     L.ttc_lqr_forward.restype = ctypes.c_int
     L.ttc_lqr_forward.argtypes = [f32p] * 9 + [i64, i32, i32, i32, i32, i32] + [f32p, f32p, f32p, ctypes.c_void_p]
     L.ttc_lqr_backward.restype = ctypes.c_int
@@ -62,7 +65,7 @@ def _load():
     L.ttc_lqr_compact_stash_bytes.restype = sz
     L.ttc_lqr_compact_stash_bytes.argtypes = [i64, i32, i32, i32]
     L.ttc_lqr_factored_workspace_bytes.restype = sz
-    L.ttc_lqr_factored_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32, i32, i32, i32, i32]
+    L.ttc_lqr_factored_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32, i32, i32, i32, i32, i32]
     L.ttc_lqr_forward_factored.restype = ctypes.c_int
     L.ttc_lqr_forward_factored.argtypes = ([f32p] * 11 + [i64, i32, i32, i32, i32, i32, i32, i32]
                                            + [f32p, f32p, ctypes.c_void_p, sz, f32p, ctypes.c_void_p])

@@ -24,16 +24,17 @@ Differences from the reference, by design:
   (per-step gains, closed-loop costates).  ``stable_backward=True`` uses the stable
   path for every problem.
 * ``precision``: the Riccati sweep (the feedback gains) runs in fp32 or fp64.
-  ``"auto"`` (default) picks fp64 for horizons ``T >= FP64_HORIZON`` (512): on long,
-  barely discounted horizons the value matrix reaches ~1e17 and fp32 rounding
-  corrupts the gains (the reference's own fp32 solvers lose the gradients
-  entirely there).  Everything else (rollouts, costates, gradients) is fp32.
   The fp32 sweep runs on the matrix cores (MFMA) as the symplectic sweep (three
   matrix products per step, one certified solve at the end; the problems the
   certificate rejects are recomputed with Riccati steps, then by the row-layout
-  kernel).  ``"fp32-riccati"`` selects per-step Riccati on the matrix cores,
-  ``"fp32-row"`` the vector-ALU row-layout kernels (forward sweep and backward
-  rollout).
+  kernel).  ``"auto"`` (default): for horizons ``T >= FP64_HORIZON`` (512) the
+  problems the symplectic certificate rejects are recomputed in fp64 instead, and the
+  backward's stable path runs in fp64 -- on long, barely discounted horizons the value
+  matrix reaches ~1e17 and fp32 rounding corrupts the gains of those problems (the
+  reference's own fp32 solvers lose the gradients entirely there).  ``"fp64"``: every
+  sweep in fp64 (row layout).  ``"fp32-riccati"`` selects per-step Riccati on the matrix
+  cores, ``"fp32-row"`` the vector-ALU row-layout kernels (forward sweep and backward
+  rollout), ``"riccati"`` per-step Riccati in fp32 or, at long horizons, in fp64.
 
 Environment knobs:
 ``TTC_LQR_STASH`` = ``auto`` (default: keep the stash from the forward when it fits
@@ -54,7 +55,7 @@ import os
 import torch
 
 from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS, \
-    FLAG_COMPACT_STASH
+    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
            "SUPPORTED_DIMS", "last_backward_stats"]
@@ -113,8 +114,9 @@ def riccati_flags(precision: str, T: int, Dp: int) -> int:
     """
     assert precision in ("fp32", "fp32-riccati", "fp32-row", "fp64", "auto", "riccati"), \
         f"unknown precision {precision}"
+    long_fp64 = T >= FP64_HORIZON and lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_RICCATI)
     if precision == "riccati":
-        return riccati_flags("auto", T, Dp) or FLAG_RICCATI_STEPS
+        return FLAG_FP64_RICCATI if long_fp64 else FLAG_RICCATI_STEPS
     if precision == "fp32-row":
         return FLAG_ROW_KERNEL
     if precision == "fp32-riccati":
@@ -123,9 +125,18 @@ def riccati_flags(precision: str, T: int, Dp: int) -> int:
         assert lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_RICCATI), \
             f"fp64 Riccati kernels exist for state dims up to 32, got {Dp}"
         return FLAG_FP64_RICCATI
-    if precision == "auto" and T >= FP64_HORIZON and lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_RICCATI):
-        return FLAG_FP64_RICCATI
+    if precision == "auto" and long_fp64:
+        return FLAG_FP64_RESCUE
     return 0
+
+
+def _fallback_slack(P: int, Dp: int, T: int, flags: int) -> int:
+    """Extra backward workspace for the problems the certificate rejects: long horizons reject
+    many (config 5: about a fifth), and each fallback pass is a serial T-step sweep, so give
+    room for a quarter of the problems in one pass (capped by the workspace budget)."""
+    if T < FP64_HORIZON or P <= 0:
+        return 0
+    return lib.ttc_lqr_fallback_bytes(max(P // 4, 8), Dp, Dp, T, flags)
 
 
 def _stash_budget(device) -> int:
@@ -216,8 +227,8 @@ class HipLQRSolveFunc(torch.autograd.Function):
         with_st = 1 if st is not None else 0
         # one pass over all tokens when it fits the budget; the library picks the largest
         # token chunk that fits whatever it is given (at least one token's worth)
-        full = lib.ttc_lqr_workspace_bytes(bs, nh, Dp, Dp, T, with_st)
-        ws_bytes = max(min(full, budget), lib.ttc_lqr_workspace_bytes(1, nh, Dp, Dp, T, with_st))
+        full = lib.ttc_lqr_workspace_bytes(bs, nh, Dp, Dp, T, with_st, flags) + _fallback_slack(bs * nh, Dp, T, flags)
+        ws_bytes = max(min(full, budget), lib.ttc_lqr_workspace_bytes(1, nh, Dp, Dp, T, with_st, flags))
         ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         n_fb = ctypes.c_int64(0)
@@ -348,8 +359,8 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         st = None if kind is None else torch.empty((stash_bytes if kind == "full" else compact_bytes) // 4,
                                                    device=dev, dtype=torch.float32)
         ws_stash = {None: 0, "full": 1, "compact": 2}[kind]
-        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16))
-        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16))
+        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16), flags)
+        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16), flags)
         ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
         fwd = lib.ttc_lqr_forward_factored_bf16 if bf16 else lib.ttc_lqr_forward_factored
         with torch.cuda.device(dev):
@@ -398,8 +409,9 @@ class HipLQRFactoredFunc(torch.autograd.Function):
              E(bs, nh, Dp), E(bs, nh, Dp), E(rb, Dp, Dp), E(rq, Dp, Dp)]
         status = torch.zeros(1, device=dev, dtype=torch.int32)
         with_st = 0 if st is None else (2 if flags & FLAG_COMPACT_STASH else 1)
-        full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16))
-        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16))
+        full = (lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16), flags)
+                + _fallback_slack(bs * nh, Dp, T, flags))
+        one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16), flags)
         ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         n_fb = ctypes.c_int64(0)
