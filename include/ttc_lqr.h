@@ -45,6 +45,7 @@ extern "C" {
 #define TTC_LQR_EINVAL 1        /* bad sizes / null pointer / workspace too small */
 #define TTC_LQR_EUNSUPPORTED 2  /* d, du combination not compiled */
 #define TTC_LQR_ELAUNCH 3       /* HIP launch error */
+#define TTC_LQR_ESCRATCH 4      /* ttc_lqr_backward_noalloc: one token's layout exceeds its fixed scratch */
 
 #define TTC_LQR_STATUS_NONFINITE 1
 #define TTC_LQR_STATUS_LARGE 2
@@ -271,6 +272,29 @@ int ttc_lqr_backward_factored_bf16(const uint16_t* A_diag, const uint16_t* coeff
                                    uint16_t* grad_B_basis, uint16_t* grad_Q_basis, void* workspace,
                                    size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
                                    void* stream);
+
+/* ---- Allocation-free backward ----
+ * No counterpart in the reference.  For callers that cannot allocate device memory -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc: ttc_lqr_backward with
+ * the workspace replaced by a fixed device scratch of TTC_LQR_NOALLOC_SCRATCH_BYTES (256 MiB), a
+ * file-scope array of the library that each GPU it runs on holds until the process ends.  Same
+ * arguments, results and status bits as ttc_lqr_backward; the tokens are processed in chunks that
+ * fit the scratch (one stream synchronisation per chunk).  Returns TTC_LQR_ESCRATCH when even one
+ * token's layout does not fit (e.g. d = 64 with T = 1024).  Calls no hipMalloc / hipFree.  Calls
+ * that overlap on one GPU share its scratch and race: the caller orders them. */
+#define TTC_LQR_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+
+/* Size of the fixed scratch of ttc_lqr_backward_noalloc. */
+size_t ttc_lqr_noalloc_scratch_bytes(void);
+
+int ttc_lqr_backward_noalloc(const float* A_diag, const float* B, const float* Q, const float* R_inv,
+                             const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
+                             const float* log_gamma_Q, const float* h0, const float* u, const float* d_u,
+                             int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T, int32_t flags,
+                             const float* stash, float* grad_A_diag, float* grad_B, float* grad_Q,
+                             float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,
+                             float* grad_log_gamma_Q, float* grad_h0, float grad_limit, int32_t* status,
+                             int64_t* n_fallback, void* stream);
 
 /* ---- Host (CPU) solver: the same problems on CPU tensors ----
  * Replace the reference's device-agnostic pure-PyTorch solvers for CPU tensors:

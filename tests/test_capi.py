@@ -33,7 +33,8 @@ def test_header_declares_expected_entry_points():
         "ttc_lqr_compact_stash_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
-        "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host", "ttc_lqr_fallback_bytes"])
+        "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host", "ttc_lqr_fallback_bytes",
+        "ttc_lqr_backward_noalloc", "ttc_lqr_noalloc_scratch_bytes"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -45,7 +46,7 @@ def test_library_exports_every_declared_symbol(L):
 
 def test_version_and_strerror(L):
     assert L.ttc_lqr_version().decode().startswith("ttc-lqr-gfx950")
-    for code in range(4):
+    for code in range(5):
         assert L.ttc_lqr_strerror(code)
     assert L.ttc_lqr_strerror(99) == b"unknown error"
 
@@ -206,3 +207,19 @@ def test_fallback_and_precision_sizing(L):
     ws = L.ttc_lqr_workspace_bytes(10, 8, d, d, 64, 0, STABLE | FP64)
     assert ws >= 8 * 80 * 64 * (d * d + 4 * d)
     assert L.ttc_lqr_supported_flags(16, 16, RESCUE) == 1 and L.ttc_lqr_supported_flags(64, 64, RESCUE) == 0
+
+
+def test_noalloc_argument_validation(L):
+    """ttc_lqr_backward_noalloc rejects what its fixed scratch cannot hold before touching a device."""
+    assert L.ttc_lqr_noalloc_scratch_bytes() == 256 << 20
+    p = ctypes.c_void_p(16)
+    n_fb = ctypes.c_int64(-1)
+    args = lambda n, d, T, flags: ([p] * 11 + [n, 16, d, d, T, flags, None] + [p] * 9  # noqa: E731
+                                   + [float("inf"), None, ctypes.byref(n_fb), None])
+    assert L.ttc_lqr_backward_noalloc(*args(0, 16, 64, 0)) == 0 and n_fb.value == 0   # empty batch
+    assert L.ttc_lqr_backward_noalloc(*args(1, 24, 64, 0)) == 2                       # unsupported dims
+    assert L.ttc_lqr_backward_noalloc(*args(-1, 16, 64, 0)) == 1                      # bad sizes
+    # d = 64, T = 4096, 16 heads: one token's fallback layout alone exceeds 256 MiB
+    assert L.ttc_lqr_workspace_bytes(1, 16, 64, 64, 4096, 0, 0) > 256 << 20
+    assert L.ttc_lqr_backward_noalloc(*args(1, 64, 4096, 0)) == 4                     # TTC_LQR_ESCRATCH
+    assert b"scratch" in L.ttc_lqr_strerror(4)

@@ -1,0 +1,75 @@
+"""GPU test of ttc_lqr_backward_noalloc (the allocation-free backward over the library's fixed
+device scratch) through the C ABI: on two calls in a row, the second with a smaller input, its
+nine gradients, status word and fallback count equal those of ttc_lqr_backward on the same inputs
+with a caller-allocated workspace (the same kernels: bitwise equal; the bar checked is the 1e-4
+parity bar).  Cases: a config-2 slice (one chunk), a batch that the 256 MiB scratch splits into
+several token chunks, and config-5 stress inputs whose rejected problems take the stable path
+inside the scratch."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.inputs import layer_solver_inputs, make_x
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ["A_diag", "B", "Q", "R_inv", "Q_f", "lgA", "lgB", "lgQ", "h0"]
+
+
+def _inputs(cfg, n_tok, seed):
+    ins = layer_solver_inputs(cfg, make_x(cfg, n_tokens=n_tok, seed=seed))
+    return [t.contiguous().cuda() for t in ins]
+
+
+def _grads_like(ins):
+    A, B, Q, R, Qf, lA, lB, lQ, h0 = ins
+    return [torch.empty_like(t) for t in (A, B, Q, R, Qf, lA, lB, lQ, h0)]
+
+
+def _backward(ins, T, noalloc, stash):
+    from ttc.solvers._lib import lib
+    N, H, d = ins[0].shape
+    dev = ins[0].device
+    u = torch.empty(N, H, d, device=dev)
+    st = torch.empty(lib.ttc_lqr_stash_bytes(N, H, d, d, T) // 4, device=dev) if stash else None
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in ins], N, H, d, d, T, 0, u.data_ptr(),
+                             None if st is None else st.data_ptr(), status.data_ptr(), s)
+    assert rc == 0
+    dU = torch.randn(N, H, d, generator=torch.Generator(device=dev).manual_seed(N + T), device=dev)
+    g = _grads_like(ins)
+    status.zero_()
+    n_fb = ctypes.c_int64(-1)
+    common = [*[t.data_ptr() for t in ins], u.data_ptr(), dU.data_ptr(), N, H, d, d, T, 0,
+              None if st is None else st.data_ptr(), *[t.data_ptr() for t in g]]
+    if noalloc:
+        rc = lib.ttc_lqr_backward_noalloc(*common, math.inf, status.data_ptr(), ctypes.byref(n_fb), s)
+    else:
+        ws_bytes = lib.ttc_lqr_workspace_bytes(N, H, d, d, T, int(stash), 0)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        rc = lib.ttc_lqr_backward(*common, ws.data_ptr(), ws.numel(), math.inf, status.data_ptr(),
+                                  ctypes.byref(n_fb), s)
+    assert rc == 0, lib.ttc_lqr_strerror(rc)
+    torch.cuda.synchronize()
+    return [t.cpu() for t in g], int(status.item()), int(n_fb.value)
+
+
+@pytest.mark.parametrize("cfg,n1,n2,T,stash", [(2, 256, 40, 64, True), (2, 1200, 300, 64, False),
+                                               (5, 64, 16, 64, True)])
+def test_noalloc_backward_equals_workspace_backward(cfg, n1, n2, T, stash):
+    for n_tok in (n1, n2):  # two calls in a row, the second smaller
+        ins = _inputs(cfg, n_tok, seed=n_tok + cfg)
+        ref, st_ref, fb_ref = _backward(ins, T, noalloc=False, stash=stash)
+        out, st_out, fb_out = _backward(ins, T, noalloc=True, stash=stash)
+        errs = {n: float((a.double() - b.double()).abs().max() / max(b.double().abs().max(), 1e-30))
+                for n, a, b in zip(NAMES, out, ref)}
+        same = all(torch.equal(a, b) for a, b in zip(out, ref))
+        print(f"cfg{cfg} tokens={n_tok} T={T} stash={stash}: fallback {fb_out} (workspace path {fb_ref}), "
+              f"bitwise equal {same}, max rel diff {max(errs.values()):.1e}", flush=True)
+        assert st_out == st_ref
+        assert fb_out == fb_ref
+        assert max(errs.values()) <= 1e-4, errs

@@ -836,6 +836,9 @@ const char* ttc_lqr_strerror(int code) {
     case TTC_LQR_EINVAL: return "invalid argument (sizes, null pointer or workspace too small)";
     case TTC_LQR_EUNSUPPORTED: return "unsupported (d, du): kernels exist for d == du in {16, 32, 64}";
     case TTC_LQR_ELAUNCH: return "HIP kernel launch failed";
+    case TTC_LQR_ESCRATCH:
+      return "problem too large for the fixed scratch of ttc_lqr_backward_noalloc (one token's backward layout "
+             "exceeds ttc_lqr_noalloc_scratch_bytes()); use ttc_lqr_backward with a workspace";
     default: return "unknown error";
   }
 }
@@ -899,6 +902,23 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
                      float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,
                      float* grad_log_gamma_Q, float* grad_h0, void* workspace, size_t workspace_bytes,
                      float grad_limit, int32_t* status, int64_t* n_fallback, void* stream) {
+  return ttc::backward_entry(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, u, d_u, n_tokens,
+                             heads, d, du, T, flags, stash, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f,
+                             grad_log_gamma_A, grad_log_gamma_B, grad_log_gamma_Q, grad_h0, workspace,
+                             workspace_bytes, grad_limit, status, n_fallback, stream);
+}
+
+}  // extern "C"
+
+namespace ttc {
+
+int backward_entry(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
+                   const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
+                   const float* u, const float* d_u, int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
+                   int32_t T, int32_t flags, const float* stash, float* grad_A_diag, float* grad_B, float* grad_Q,
+                   float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,
+                   float* grad_log_gamma_Q, float* grad_h0, void* workspace, size_t workspace_bytes,
+                   float grad_limit, int32_t* status, int64_t* n_fallback, void* stream) {
   if (n_fallback) *n_fallback = 0;
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
@@ -917,6 +937,10 @@ int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const 
                        static_cast<char*>(workspace), workspace_bytes, grad_limit, status, n_fallback,
                        reinterpret_cast<hipStream_t>(stream));
 }
+
+}  // namespace ttc
+
+extern "C" {
 
 
 size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, int32_t du, int32_t b_rank,

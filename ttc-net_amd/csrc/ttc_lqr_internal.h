@@ -102,4 +102,13 @@ int launch_unpack_quu0(const float* packed, const float* B, const float* lgB, co
 int launch_bf16_to_f32(const uint16_t* in, int64_t n, float* out, hipStream_t s);
 int launch_f32_to_bf16(const float* in, int64_t n, uint16_t* out, hipStream_t s);
 size_t factor_partial_floats(int64_t M, int R, int E);
+// The body of ttc_lqr_backward (argument checks, then the backward over the given workspace);
+// ttc_lqr_backward_noalloc calls it with its fixed device scratch.
+int backward_entry(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
+                   const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
+                   const float* u, const float* d_u, int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
+                   int32_t T, int32_t flags, const float* stash, float* grad_A_diag, float* grad_B, float* grad_Q,
+                   float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A, float* grad_log_gamma_B,
+                   float* grad_log_gamma_Q, float* grad_h0, void* workspace, size_t workspace_bytes,
+                   float grad_limit, int32_t* status, int64_t* n_fallback, void* stream);
 }  // namespace ttc

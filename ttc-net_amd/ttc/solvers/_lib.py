@@ -77,6 +77,11 @@ def _load():
     L.ttc_lqr_rescale.argtypes = [f32p, f32p, i64, i32, i32, i32, i32, f32p, ctypes.c_void_p]
     L.ttc_lqr_rescale_backward.restype = ctypes.c_int
     L.ttc_lqr_rescale_backward.argtypes = [f32p, f32p, f32p, i64, i32, i32, i32, i32, f32p, ctypes.c_void_p]
+    L.ttc_lqr_noalloc_scratch_bytes.restype = sz
+    L.ttc_lqr_noalloc_scratch_bytes.argtypes = []
+    L.ttc_lqr_backward_noalloc.restype = ctypes.c_int
+    L.ttc_lqr_backward_noalloc.argtypes = ([f32p] * 11 + [i64, i32, i32, i32, i32, i32] + [f32p] + [f32p] * 9
+                                           + [ctypes.c_float, f32p, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p])
     L.ttc_lqr_forward_host.restype = ctypes.c_int
     L.ttc_lqr_forward_host.argtypes = [f32p] * 9 + [i64, i32, i32, i32, i32] + [f32p, f32p, i32]
     L.ttc_lqr_backward_host.restype = ctypes.c_int
