@@ -12,8 +12,10 @@ Prints one JSON line: value = forward+backward LQR solves/s; the forward-only
 rate, tokens/s, the fp32 roofline of the forward kernel (algorithmic flops per
 problem F_fwd = T(4 d^2 du + 2 d^3), timed with HIP events on the launch stream)
 and a CPU baseline (an op-for-op restatement of the reference `riccati` solver,
-fwd and autograd fwd+bwd, on a bounded token sample, all host cores) ride along,
-as do configs 3 and 4 on 8,192-token samples (`extra_configs`).
+fwd and autograd fwd+bwd, on a bounded token sample, all host cores, with the reference's
+fp32 solvers' and this solver's errors against the fp64 oracle on that sample) ride along,
+as do configs 3 and 4 on 8,192-token samples (`extra_configs`, config 4 also with bf16
+storage) and configs 3 and 4 at full size, one step each (`full_size`).
 `--sweep horizon|batch` runs the reference bench's sweeps instead (one line per point).
 """
 from __future__ import annotations
@@ -33,6 +35,14 @@ for _p in (ROOT, os.path.join(ROOT, "ttc-net_amd")):
         sys.path.insert(0, _p)
 
 METRIC = "LQR solves/sec fwd & fwd+bwd (h=16,T=64) + % HBM/MFMA roofline, 1×MI355X"
+
+
+def metric_for(d, T):
+    """BASELINE.json's metric for the headline config (h=16, T=64); the same measure of other
+    configurations names their own h and T."""
+    return METRIC.replace("(h=16,T=64)", f"(h={d},T={T})")
+
+
 PEAK_FP32_MFMA = 157.3e12   # MI355X dense fp32 matrix peak (published)
 PEAK_FP64 = 78.6e12         # MI355X fp64 peak (published; vector and matrix)
 PEAK_HBM = 8.0e12
@@ -69,6 +79,8 @@ def parse():
                     help="comma list of further configs measured on a token sample after the main one "
                          "(forward and fwd+bwd, reported under 'extra_configs'); '' for none")
     ap.add_argument("--extra-tokens", type=int, default=8192, help="token sample of the extra configs")
+    ap.add_argument("--no-full-size", action="store_true",
+                    help="skip the full-size configs 3 and 4 (one step each, ~1 minute) of the default line")
     ap.add_argument("--factored", action="store_true",
                     help="measure the solver on the layer's low-rank factors (coeff_B, coeff_Q, coeff_Qf + bases, "
                          "expanded per token chunk on the device) instead of materialised B, Q, Q_f: the only "
@@ -97,8 +109,56 @@ def traffic_from_profiles(kernel_tag: str):
         return None
 
 
-def cpu_baseline(ins_cpu, T, H, sample_tokens):
-    """Reference `riccati` restatement (oracle.ref_torch) on the host, fwd and fwd+bwd."""
+def _relerr(x, ref):
+    import numpy as np
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    e = float(np.abs(x - ref).max() / max(float(np.abs(ref).max()), 1e-30)) if ref.size else 0.0
+    return e if math.isfinite(e) else None  # None: non-finite (NaN / inf) output
+
+
+NAMES = ["A_diag", "B", "Q", "R_inv", "Q_f", "lgA", "lgB", "lgQ", "h0"]
+
+
+def accuracy_vs_fp64(ins_cpu, d_u_cpu, T, grad_limit):
+    """u and the nine gradients of (a) the reference's `riccati` and `kkt` solvers restated op for op
+    in fp32 on the host (oracle/ref_torch.py) and (b) this build's HIP solver, each against the fp64
+    oracle (oracle/lqr64.py) on the same inputs and the same upstream gradient: per tensor
+    max|x - x64| / max|x64| (Q / Q_f: symmetric gradients), None where an output is non-finite."""
+    import numpy as np
+    import torch
+    from oracle.lqr64 import LQRProblem, solve_grads
+    from oracle.ref_torch import kkt_solve, riccati_solve
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+    ref = solve_grads(LQRProblem(*ins_cpu, T), d_u_cpu.double().numpy())
+
+    def run(fn, dev):
+        xs = [t.detach().clone().to(dev).float().requires_grad_(True) for t in ins_cpu]
+        u = fn(*xs, T)
+        gs = torch.autograd.grad(u, xs, d_u_cpu.to(dev).to(u.dtype), allow_unused=True)
+        out = {"u": u.detach().cpu().double().numpy()}
+        for n, g in zip(NAMES, gs):
+            g = g.detach().cpu().double().numpy()
+            out[n] = 0.5 * (g + np.swapaxes(g, -1, -2)) if n in ("Q", "Q_f") else g
+        return out
+
+    res = {}
+    for name, fn, dev in (("reference_riccati_fp32", riccati_solve, "cpu"), ("reference_kkt_fp32", kkt_solve, "cpu"),
+                          ("hip", lambda *a: hip_lqr_solve(*a, grad_limit=grad_limit), "cuda")):
+        try:
+            with np.errstate(all="ignore"):
+                out = run(fn, dev)
+            per = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
+        except RuntimeError as e:  # e.g. a guard of the solver
+            per = {"error": str(e)}
+        vals = [v for k, v in per.items() if k != "error"]
+        res[name] = {"max": (None if (not vals or any(v is None for v in vals)) else max(vals)), "per_output": per}
+    return res
+
+
+def cpu_baseline(ins_cpu, T, H, sample_tokens, d_u_cpu=None, grad_limit=1e6):
+    """Reference `riccati` restatement (oracle.ref_torch) on the host, fwd and fwd+bwd, plus the
+    accuracy of the reference's fp32 solvers and of the HIP solver against fp64 on the sample."""
     import torch
     from oracle.ref_torch import riccati_solve
     cores = os.cpu_count() or 1
@@ -125,12 +185,22 @@ def cpu_baseline(ins_cpu, T, H, sample_tokens):
             fn()
             ts.append(time.perf_counter() - t0)
         res[name] = P / statistics.median(ts)
-    return {"value": res["fwd_bwd"], "unit": "solves/s", "cores": torch.get_num_threads(), "kind": "port",
-            "fwd_value": res["fwd"],
-            "sample": f"{sample_tokens} tokens x {H} heads = {P} problems of the same workload, T={T}; "
-                      f"oracle/ref_torch.riccati_solve (reference direct_lqr_solve restated), fwd median of 5, "
-                      f"fwd+bwd (autograd) median of 3, torch threads={torch.get_num_threads()}, "
-                      f"os.cpu_count()={cores}"}
+    out = {"value": res["fwd_bwd"], "unit": "solves/s", "cores": torch.get_num_threads(), "kind": "port",
+           "fwd_value": res["fwd"],
+           "sample": f"{sample_tokens} tokens x {H} heads = {P} problems of the same workload, T={T}; "
+                     f"oracle/ref_torch.riccati_solve (reference direct_lqr_solve restated), fwd median of 5, "
+                     f"fwd+bwd (autograd) median of 3, torch threads={torch.get_num_threads()}, "
+                     f"os.cpu_count()={cores}"}
+    if d_u_cpu is not None:
+        n_acc = sample_tokens if T < 512 else min(sample_tokens, 16)
+        acc = accuracy_vs_fp64([t[:n_acc] for t in sl], d_u_cpu[:n_acc], T, grad_limit)
+        out["ref_rel_err"] = acc["reference_riccati_fp32"]["max"]
+        out["ref_kkt_rel_err"] = acc["reference_kkt_fp32"]["max"]
+        out["hip_rel_err"] = acc["hip"]["max"]
+        out["accuracy"] = {"vs": "fp64 oracle (oracle/lqr64.py), same inputs and upstream gradient, "
+                                 f"{n_acc} tokens x {H} heads; per tensor max|x-x64|/max|x64| over u and the nine "
+                                 "gradients (None: non-finite output)", **acc}
+    return out
 
 
 def _solver_for(ins):
@@ -138,10 +208,11 @@ def _solver_for(ins):
     return hip_lqr_solve_factored if len(ins) == 11 else hip_lqr_solve
 
 
-def layer_workload(cfg, tokens, dev, factored=False):
+def layer_workload(cfg, tokens, dev, factored=False, normal_du=False):
     """Solver inputs of a config (seeded layer front-end on synthetic x: the nine materialised
     inputs, or with `factored` the eleven low-rank ones) and the d_u that dy ~ N(0,1) induces
-    through the layer back-end (l2norm rescale + out_proj)."""
+    through the layer back-end (l2norm rescale + out_proj); with `normal_du`, d_u ~ N(0,1)
+    directly (no extra solver forward: the full-size entries)."""
     import torch
     from ttc import TTCLayer
     from ttc.layers.ttc_layer import l2norm
@@ -161,6 +232,10 @@ def layer_workload(cfg, tokens, dev, factored=False):
         front = layer.factored_inputs(x) if factored else layer.solver_inputs(x)
         ins = [t.detach().float().contiguous() for t in front]
         del front
+        if normal_du:
+            d_u = torch.randn(ins[0].shape[0], c["num_heads"], c["h_dim"], generator=g, device=dev)
+            _note(f"workload cfg{cfg}: {ins[0].shape[0]} tokens, factored={factored}, d_u ~ N(0,1)")
+            return ins, d_u, list(xshape)
         u0 = _solver_for(ins)(*ins, T)
     _note(f"workload cfg{cfg}: {ins[0].shape[0]} tokens, factored={factored}")
     u_req = u0.clone().requires_grad_(True)
@@ -313,14 +388,15 @@ def main():
     achieved = F_fwd * P / (fwd_gpu_ms * 1e-3)
     fwd_bytes = 4 * (3 * d + 2 * d + d * d + 1 + d) + 4 * (d * d + d * d) / H
     traffic = traffic_from_profiles(f"lqr_fwd_cfg{args.config}")
-    kern = f"lqr_fwd_blk_kernel<{d}>" + (" (symplectic sweep)" if d == 16 else " (blocked Riccati)")
-    # the solver's precision="auto" runs the fp64 Riccati sweep for T >= 512 where d <= 32
-    fp64 = T >= 512 and d <= 32
-    peak = PEAK_FP64 if fp64 else PEAK_FP32_MFMA
-    if fp64:
-        kern = f"lqr_fwd_kernel<{d}, double> (fp64 Riccati, row layout)"
+    kern = f"lqr_fwd_blk_kernel<{d}>" + (" (symplectic sweep)" if d in (16, 32, 64) else "")
+    # precision="auto" at T >= 512 (d <= 32): the same fp32 matrix-core sweep, the problems its
+    # certificate rejects (a few per cent) recomputed by the fp64 row-layout sweep; priced against
+    # the fp32 matrix peak as a whole
+    long_h = T >= 512 and d <= 32
+    if long_h:
+        kern += " + fp64 row-layout rescue of the rejected problems (lqr_rescue_fine_kernel<double>)"
     out = {
-        "metric": METRIC,
+        "metric": metric_for(d, T),
         "value": P / step_s,
         "unit": "solves/s",
         "n_gpus": 1,
@@ -330,7 +406,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64" if fp64 else "f32",
+        "dtype": "f32+f64" if long_h else "f32",
         "data": "synthetic (seeded N(0,1) x, random-init layer weights)",
         "config": {"workload": f"cfg{args.config}: TTCLayer(in={c['in_dim']},out={c['out_dim']},h={d},heads={H},"
                                f"b_rank={c['b_rank']},q_rank={c['q_rank']}) T={T}, x{xshape} -> "
@@ -344,8 +420,8 @@ def main():
         "bwd_fallback_problems": r["bwd_fallback_problems"],
         "tokens_per_s_fwd_bwd": N / step_s,
         "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
-        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / peak, "traffic": traffic,
+        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_FP32_MFMA / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA, "traffic": traffic,
                      "kernel": kern, "flops_per_problem": F_fwd,
                      "algorithmic_bytes_per_problem": fwd_bytes},
     }
@@ -353,20 +429,10 @@ def main():
     for cfg in [x.strip() for x in args.extra_configs.split(",") if x.strip()]:
         if cfg == args.config:
             continue
-        ce = CONFIGS[cfg]
-        Te, He, de = ce["T"], ce["num_heads"], ce["h_dim"]
-        ins_e, du_e, xs_e = layer_workload(cfg, args.extra_tokens, dev)
-        Pe = ins_e[0].shape[0] * He
-        re_ = time_solver(ins_e, du_e, Te, 3, 1, grad_limit=ce.get("grad_limit", 1e6))
-        ach = flops_fwd(de, Te) * Pe / (re_["fwd_ms"] * 1e-3)
-        extras.append({"config": f"cfg{cfg}", "x": xs_e, "d": de, "T": Te, "heads": He, "problems": Pe,
-                       "fwd_ms": re_["fwd_ms"], "fwd_solves_per_s": Pe / (re_["fwd_ms"] * 1e-3),
-                       "fwd_bwd_ms": re_["step_ms"], "fwd_bwd_solves_per_s": Pe / (re_["step_ms"] * 1e-3),
-                       "bwd_fallback_problems": re_["bwd_fallback_problems"],
-                       "roofline_frac": ach / PEAK_FP32_MFMA, "achieved_tflops": ach / 1e12,
-                       "traffic": traffic_from_profiles(f"lqr_fwd_cfg{cfg}")})
-        del ins_e, du_e
-        torch.cuda.empty_cache()
+        extras.append(extra_entry(cfg, args.extra_tokens, dev))
+    if args.config == "2" and "4" in args.extra_configs:
+        # config 4 as stored (bf16): the factored bf16 entry points on the same token sample
+        extras.append(extra_entry("4", args.extra_tokens, dev, bf16=True))
     out["extra_configs"] = extras
     if not args.factored:
         # the layer's default path: the same solve on the low-rank factors, B / Q / Q_f expanded per
@@ -378,6 +444,11 @@ def main():
                            "input_bytes_per_problem": 4 * (5 * d + 1 + (c["b_rank"] + c["q_rank"]) / H + c["q_rank"])}
         del ins_f, du_f
         torch.cuda.empty_cache()
+    if args.config == "2" and not args.no_full_size:
+        # BASELINE configs 3 and 4 at full size under this run's clock: one forward and one
+        # forward+backward step each, on the factored inputs (the materialised Q_f alone would be
+        # 137 GB); d_u ~ N(0,1)
+        out["full_size"] = [full_size_entry(cfg, dev) for cfg in ("3", "4")]
     if not args.no_cpu_baseline:
         n_s = min(args.cpu_sample_tokens, N)
         ins_cpu = [t.detach()[:n_s].cpu() if i < 9 else t.detach().cpu() for i, t in enumerate(ins)]
@@ -385,10 +456,63 @@ def main():
             A, cB, cQ, R, cQf, lA, lB, lQ, h0, Bs, Gs = ins_cpu
             ins_cpu = [A, torch.einsum("nr,rij->nij", cB, Bs), torch.einsum("nr,rij->nij", cQ, Gs), R,
                        torch.einsum("nhr,rij->nhij", cQf, Gs), lA, lB, lQ, h0]
-        out["cpu_baseline"] = cpu_baseline(ins_cpu, T, H, min(args.cpu_sample_tokens, N))
+        out["cpu_baseline"] = cpu_baseline(ins_cpu, T, H, n_s, d_u_cpu=d_u[:n_s].detach().cpu(),
+                                           grad_limit=c.get("grad_limit", 1e6))
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out), flush=True)
+
+
+def extra_entry(cfg, tokens, dev, bf16=False):
+    """A further configuration on a token sample: forward (HIP events) and fwd+bwd, roofline
+    fraction of the forward, measured HBM traffic where profiled.  bf16: the factored inputs
+    stored as bf16 (config 4's storage), through the _bf16 entry points."""
+    import torch
+    ce = CONFIGS[cfg]
+    Te, He, de = ce["T"], ce["num_heads"], ce["h_dim"]
+    ins_e, du_e, xs_e = layer_workload(cfg, tokens, dev, factored=bf16)
+    if bf16:
+        ins_e = [t.to(torch.bfloat16) for t in ins_e]
+        du_e = du_e.to(torch.bfloat16)
+    Pe = ins_e[0].shape[0] * He
+    re_ = time_solver(ins_e, du_e, Te, 3, 1, grad_limit=ce.get("grad_limit", 1e6))
+    ach = flops_fwd(de, Te) * Pe / (re_["fwd_ms"] * 1e-3)
+    e = {"config": f"cfg{cfg}" + ("-bf16" if bf16 else ""), "x": xs_e, "d": de, "T": Te, "heads": He,
+         "problems": Pe, "storage": "bf16 (factored inputs, d_u and gradients)" if bf16 else "fp32",
+         "fwd_ms": re_["fwd_ms"], "fwd_solves_per_s": Pe / (re_["fwd_ms"] * 1e-3),
+         "fwd_bwd_ms": re_["step_ms"], "fwd_bwd_solves_per_s": Pe / (re_["step_ms"] * 1e-3),
+         "bwd_fallback_problems": re_["bwd_fallback_problems"],
+         "roofline_frac": ach / PEAK_FP32_MFMA, "achieved_tflops": ach / 1e12,
+         "traffic": None if bf16 else traffic_from_profiles(f"lqr_fwd_cfg{cfg}")}
+    del ins_e, du_e
+    torch.cuda.empty_cache()
+    return e
+
+
+def full_size_entry(cfg, dev):
+    """One config at its full BASELINE size on the factored inputs: one timed forward (HIP events)
+    and one timed forward+backward step, no warm-up."""
+    import torch
+    ce = CONFIGS[cfg]
+    Te, He, de = ce["T"], ce["num_heads"], ce["h_dim"]
+    t0 = time.perf_counter()
+    ins_f, du_f, xs = layer_workload(cfg, 0, dev, factored=True, normal_du=True)
+    Pe = ins_f[0].shape[0] * He
+    re_ = time_solver(ins_f, du_f, Te, 1, 0, grad_limit=ce.get("grad_limit", 1e6))
+    ach = flops_fwd(de, Te) * Pe / (re_["fwd_ms"] * 1e-3)
+    e = {"config": f"cfg{cfg}", "x": xs, "d": de, "T": Te, "heads": He, "problems": Pe,
+         "workload": "full BASELINE x through the factored solver (B, Q, Q_f expanded per token chunk on the "
+                     "device), d_u ~ N(0,1), one forward and one fwd+bwd step, no warm-up",
+         "fwd_ms": re_["fwd_ms"], "fwd_solves_per_s": Pe / (re_["fwd_ms"] * 1e-3),
+         "fwd_bwd_ms": re_["step_ms"], "fwd_bwd_solves_per_s": Pe / (re_["step_ms"] * 1e-3),
+         "tokens_per_s_fwd_bwd": ins_f[0].shape[0] / (re_["step_ms"] * 1e-3),
+         "bwd_fallback_problems": re_["bwd_fallback_problems"],
+         "roofline_frac": ach / PEAK_FP32_MFMA, "achieved_tflops": ach / 1e12,
+         "wall_s": None}
+    del ins_f, du_f
+    torch.cuda.empty_cache()
+    e["wall_s"] = time.perf_counter() - t0
+    return e
 
 
 if __name__ == "__main__":

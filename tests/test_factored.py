@@ -332,3 +332,35 @@ def test_compact_stash_matches_full_stash(cfg, n_tok, monkeypatch):
     assert np.array_equal(full["u"], chunked["u"])
     for k in NAMES11:
         assert _relerr(chunked[k], full[k]) <= 2e-5, k
+
+
+BF16_TOL = 2.0 ** -8  # results are fp32 computations rounded to bf16 (half an ulp: 2^-9 of each value)
+
+
+@pytest.mark.parametrize("cfg,n_tok", [(4, 2), (2, 16)])
+def test_bf16_storage_against_oracle(cfg, n_tok):
+    """bf16 storage (config 4 stores its activations in bf16): the eleven factored inputs and
+    d_u handed over as bf16 (``ttc_lqr_*_factored_bf16``), u and all eleven gradients returned
+    as bf16, against the fp64 oracle evaluated on the same bf16 values (widened exactly).
+    Tolerance: per tensor max|x - x64| / max|x64| <= 2^-8 -- the fp32 solve (~1e-6) plus the
+    rounding of each output to bf16 (at most half an ulp, 2^-9 relative)."""
+    from ttc.solvers.hip_lqr import hip_lqr_solve_factored
+    ins = [t.to(torch.bfloat16) for t in factored_inputs(cfg, n_tok, seed=17)]
+    T = CONFIGS[cfg]["T"]
+    N, H, d = ins[0].shape
+    dU = torch.randn(N, H, d, generator=torch.Generator().manual_seed(23)).to(torch.bfloat16)
+    ref = oracle_factored([t.float() for t in ins], T, dU.double().numpy())
+    dev = torch.device("cuda:0")
+    xs = [t.to(dev).requires_grad_(True) for t in ins]
+    u = hip_lqr_solve_factored(*xs, T)
+    assert u.dtype == torch.bfloat16
+    (u * dU.to(dev)).sum().backward()
+    out = {"u": u.detach().float().cpu().double().numpy()}
+    for n, t in zip(NAMES11, xs):
+        assert t.grad.dtype == torch.bfloat16
+        out[n] = t.grad.float().cpu().double().numpy()
+    errs = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES11}
+    print(f"[bf16 cfg{cfg}] N={N} H={H} d={d} T={T}: " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()),
+          flush=True)
+    bad = {k: v for k, v in errs.items() if not (v <= BF16_TOL)}
+    assert not bad, f"bf16 cfg{cfg}: rel err above {BF16_TOL}: {bad}"

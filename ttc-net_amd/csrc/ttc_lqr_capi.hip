@@ -519,6 +519,9 @@ static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, 
     io_counts(nc, H, d, du, rb, rq, n);
     for (int k = 0; k < (backward ? 10 : 9); ++k) {
       L.cin[k] = off;
+      // the forward's expansion reads the bf16 coefficients directly (the backward's basis
+      // reductions read fp32 copies)
+      if (!backward && (k == 1 || k == 2 || k == 4)) continue;
       off += align256(n[k] * sizeof(float));
     }
     if (backward) {
@@ -566,7 +569,8 @@ static int64_t fact_chunk(int64_t n_tokens, int H, int d, int du, int rb, int rq
   return chunk;
 }
 
-static int expand_chunk(const float* cB, const float* cQ, const float* cQf, const float* Bs, const float* Gs,
+template <typename TC>
+static int expand_chunk(const TC* cB, const TC* cQ, const TC* cQf, const float* Bs, const float* Gs,
                         int64_t nc, int H, int d, int du, int rb, int rq, float* Bx, float* Qx, float* Qfx,
                         hipStream_t s) {
   int rc = launch_expand(cB, nc, rb, Bs, d * du, Bx, s);
@@ -636,10 +640,7 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
     io_counts(nc, H, d, du, rb, rq, n);
     auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
     const float* a = St::in(A_diag, p0 * d, n[0], cin(0), s, rc);
-    const float* cb = St::in(coeff_B, n0 * rb, n[1], cin(1), s, rc);
-    const float* cq = St::in(coeff_Q, n0 * rq, n[2], cin(2), s, rc);
     const float* r = St::in(R_inv, p0 * du, n[3], cin(3), s, rc);
-    const float* cqf = St::in(coeff_Qf, p0 * rq, n[4], cin(4), s, rc);
     const float* la = St::in(log_gamma_A, p0, n[5], cin(5), s, rc);
     const float* lb = St::in(log_gamma_B, p0 * du, n[6], cin(6), s, rc);
     const float* lq = St::in(log_gamma_Q, p0 * d, n[7], cin(7), s, rc);
@@ -648,7 +649,9 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
     float* Bx = reinterpret_cast<float*>(ws + L.Bx);
     float* Qx = reinterpret_cast<float*>(ws + L.Qx);
     float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
-    rc = expand_chunk(cb, cq, cqf, Bs, Gs, nc, H, d, du, rb, rq, Bx, Qx, Qfx, s);
+    // the expansion reads the coefficients as stored (bf16: widened in registers)
+    rc = expand_chunk(coeff_B + n0 * rb, coeff_Q + n0 * rq, coeff_Qf + p0 * rq, Bs, Gs, nc, H, d, du, rb, rq, Bx, Qx,
+                      Qfx, s);
     if (rc != TTC_LQR_OK) return rc;
     float* v1 = stash ? stash + p0 * dd : nullptr;
     float* q0 = stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;

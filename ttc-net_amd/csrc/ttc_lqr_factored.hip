@@ -36,7 +36,13 @@ constexpr int kExpandChunk = 16;  // ranks whose loads are issued together
 // of kExpandChunk whose basis and coefficient loads are all issued before their FMAs (one
 // memory latency per chunk instead of one per rank), and the rows leave with nontemporal
 // stores (written once, read by the next kernel from HBM): 2.1 -> 6.5 TB/s of stores.
-__global__ __launch_bounds__(256) void expand_kernel(const float* __restrict__ coeff, int64_t M, int R,
+// Coefficients as stored: fp32, or bf16 bit patterns (widened exactly in registers, so bf16
+// storage needs no fp32 copy of them).
+__device__ __forceinline__ float coeff_value(const float* p) { return *p; }
+__device__ __forceinline__ float coeff_value(const uint16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
+
+template <typename TC>
+__global__ __launch_bounds__(256) void expand_kernel(const TC* __restrict__ coeff, int64_t M, int R,
                                                      const float* __restrict__ basis, int E,
                                                      float* __restrict__ out) {
   const int E4 = E >> 2;
@@ -49,7 +55,7 @@ __global__ __launch_bounds__(256) void expand_kernel(const float* __restrict__ c
                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(mb_l & 0xffffffff));
   const int e = (int)(t - mb * E4) * 4;
   const int64_t m0 = mb * kExpandRows;
-  const float* crow[kExpandRows];
+  const TC* crow[kExpandRows];
 #pragma unroll
   for (int i = 0; i < kExpandRows; ++i) crow[i] = coeff + (m0 + i < M ? m0 + i : M - 1) * R;  // tail: clamped, not stored
   float acc[kExpandRows][4];
@@ -64,7 +70,7 @@ __global__ __launch_bounds__(256) void expand_kernel(const float* __restrict__ c
 #pragma unroll
     for (int i = 0; i < kExpandRows; ++i)
 #pragma unroll
-      for (int k = 0; k < kExpandChunk; ++k) cr[i][k] = crow[i][r0 + k];
+      for (int k = 0; k < kExpandChunk; ++k) cr[i][k] = coeff_value(crow[i] + r0 + k);
 #pragma unroll
     for (int k = 0; k < kExpandChunk; ++k)
 #pragma unroll
@@ -79,7 +85,7 @@ __global__ __launch_bounds__(256) void expand_kernel(const float* __restrict__ c
     const float4 b = *reinterpret_cast<const float4*>(basis + (int64_t)r0 * E + e);
 #pragma unroll
     for (int i = 0; i < kExpandRows; ++i) {
-      const float cr = crow[i][r0];
+      const float cr = coeff_value(crow[i] + r0);
       acc[i][0] = fmaf(cr, b.x, acc[i][0]);
       acc[i][1] = fmaf(cr, b.y, acc[i][1]);
       acc[i][2] = fmaf(cr, b.z, acc[i][2]);
@@ -287,13 +293,22 @@ size_t factor_partial_floats(int64_t M, int R, int E) {
   return (size_t)(S + S2) * (size_t)R * (size_t)E;
 }
 
-int launch_expand(const float* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s) {
+template <typename TC>
+static int launch_expand_t(const TC* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s) {
   if (E % 256 != 0) return TTC_LQR_EINVAL;
   const int64_t threads = (M + kExpandRows - 1) / kExpandRows * (E / 4);
   if (threads <= 0) return TTC_LQR_OK;
-  hipLaunchKernelGGL(expand_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, coeff, M, R, basis, E,
-                     out);
+  hipLaunchKernelGGL(expand_kernel<TC>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, coeff, M, R, basis,
+                     E, out);
   return launched() ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+}
+
+int launch_expand(const float* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s) {
+  return launch_expand_t(coeff, M, R, basis, E, out, s);
+}
+
+int launch_expand(const uint16_t* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s) {
+  return launch_expand_t(coeff, M, R, basis, E, out, s);
 }
 
 int launch_project(const float* X, int64_t M, int E, const float* basis, int R, float* out, hipStream_t s) {

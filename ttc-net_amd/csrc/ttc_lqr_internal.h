@@ -92,6 +92,8 @@ int launch_ham64_mfma(const float* A, const float* B, const float* Q, const floa
 // Low-rank front-end (ttc_lqr_factored.hip): expansion of coefficient x basis sums and
 // their chain rule.  Rows of E = d * du floats; ranks R <= 64; E in {256, 1024, 4096}.
 int launch_expand(const float* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s);
+// the same with bf16 coefficients (bit patterns), widened in registers
+int launch_expand(const uint16_t* coeff, int64_t M, int R, const float* basis, int E, float* out, hipStream_t s);
 int launch_project(const float* X, int64_t M, int E, const float* basis, int R, float* out, hipStream_t s);
 int launch_reduce(const float* coeff, int64_t M, int R, const float* X, int E, float* partial, float* out,
                   int accumulate, hipStream_t s);
