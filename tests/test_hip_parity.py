@@ -431,16 +431,16 @@ def test_random_shapes(seed):
     assert np.isfinite(out["u"]).all()
 
 
-def _indefinite_terminal_inputs(s, seed=2):
+def _indefinite_terminal_inputs(s, seed=2, H=4):
     """Problem 1 of 8 gets Q_f = -s I with a strong, barely discounted B: Quu turns
     indefinite (nonsingular), so the matrix-core kernel's Cholesky guard fires for the
     wave holding problems 0-3 and that wave finishes on the pivoted row-layout sweep,
     while problems 4-7 stay on the matrix cores.  s = 2: indefinite from the last step
     (t = T-1) on; s = 0.2: positive definite until t = 0 (a mid-horizon switch)."""
-    ins = bench_solver_inputs(2, 4, 16, seed=seed)
+    ins = bench_solver_inputs(2, H, 16, seed=seed)
     g = torch.Generator().manual_seed(seed)
     B = torch.randn(2, 16, 16, generator=g) * 0.25
-    lgB = torch.full((2, 4, 16), -0.01)
+    lgB = torch.full((2, H, 16), -0.01)
     Qf = ins[4].clone()
     Qf[0, 1] = -s * torch.eye(16)
     return [ins[0], B, ins[2], ins[3], Qf, ins[5], lgB, ins[7], ins[8]]
@@ -451,6 +451,16 @@ def _indefinite_terminal_inputs(s, seed=2):
 @pytest.mark.parametrize("precision", ["fp32", "fp32-riccati"])
 def test_indefinite_Quu_switches_to_pivoted_sweep(s, stash, precision):
     check_case(f"indef{s}", _indefinite_terminal_inputs(s), 6, stash=stash, precision=precision)
+
+
+@pytest.mark.parametrize("s", [2.0, 0.2])
+@pytest.mark.parametrize("stash", ["always", "never"])
+def test_head_group_backward_with_indefinite_Quu0(s, stash):
+    """H = 8: the d = 16 head-group Hamiltonian backward (its own pivoted solve of
+    Quu_0 w_0 = -d_u) on a group whose problem 1 has Q_f = -s I, so that its Quu_0 is
+    indefinite; s = 2 sends the group to the stable path, s = 0.2 stays on the head-group
+    kernel."""
+    check_case(f"indef-h8-{s}", _indefinite_terminal_inputs(s, H=8), 6, stash=stash)
 
 
 @pytest.mark.parametrize("T", [64, 256])

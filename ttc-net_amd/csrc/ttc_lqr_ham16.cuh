@@ -47,7 +47,11 @@ struct Ham16 {
   static constexpr size_t LDS_BYTES = sizeof(float) * WPB * PER_WAVE;
 };
 
-__device__ __forceinline__ float swap8(float v) { return ror16f<8>(v); }  // lane c <-> c ^ 8
+// lane c <-> c ^ 8 (DPP row_ror:8).  Every lane of a row has a valid source, so bound_ctrl is
+// immaterial; setting it lets the compiler fold the move into the consuming VOP2 instruction.
+__device__ __forceinline__ float swap8(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, true));
+}
 
 __device__ __forceinline__ v4f swap8(v4f v) { return v4f{swap8(v[0]), swap8(v[1]), swap8(v[2]), swap8(v[3])}; }
 
@@ -69,6 +73,25 @@ __device__ __forceinline__ v4f mfma_cross(const float* X, const float* Y, int g,
   const v4f b = ld4(Y + c * Ham16::LD + 4 * (g ^ 2));
 #pragma unroll
   for (int s = 0; s < 4; ++s) acc = mfma16x16x4(a[s], b[s], acc);
+  return acc;
+}
+
+// C-layout tile -> row-major LDS tile with the trajectory columns interleaved: column c is
+// stored at 4 (c & 3) + (c >> 2), so one 16-byte read of row i gives trajectories
+// g, 4 + g (primal) and 8 + g, 12 + g (their adjoints).
+__device__ __forceinline__ void st_tile_interleaved(float* t, int g, int c, v4f v) {
+  const int col = 4 * (c & 3) + (c >> 2);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) t[(4 * g + r) * Ham16::LD + col] = v[r];
+}
+
+// acc += X_p X_a' (primal columns against their adjoints, 8 trajectories), X stored by
+// st_tile_interleaved: acc[i][j] += sum_{k < 8} X[i][k] X[j][k + 8].  Two products instead of
+// the four of mfma_cross(X, X): the full sum X Pi X' = acc + acc' is formed once at the end.
+__device__ __forceinline__ v4f mfma_half_cross(const float* X, int g, int c, v4f acc) {
+  const v4f a = ld4(X + c * Ham16::LD + 4 * g);  // X[c][g], X[c][4+g], X[c][8+g], X[c][12+g]
+  acc = mfma16x16x4(a[0], a[2], acc);
+  acc = mfma16x16x4(a[1], a[3], acc);
   return acc;
 }
 
@@ -141,7 +164,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     aug[17] = aug[18] = aug[19] = 0.f;
     float piv;
     int pos;
-    gauss_jordan<16, 20, 4>(aug, c, prow, piv, pos);
+    gauss_jordan<16, 20, 0, 17>(aug, c, prow, piv, pos);
     TS[(8 + 4 * pa + g) * Ham16::LD + pos] = -aug[16] / piv;  // adjoint column of problem 4pa+g
   }
   wave_sync();
@@ -236,68 +259,107 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   //   grad lgB:   (t+1) beta (u B'lambda~ + w B'lambda) = 2 (t+1) W,
   //   grad R_inv: -u w / R_inv^2                          = W / R_inv,
   // so the loop sums W and (t+1) W (sP, sPt; one lane of each pair suffices).
-  v4f lb4;
+  // Discounts by recurrence: q_t = exp(lgQ t), e^{lgA (t+1)} and -R_inv beta_t^2 are multiplied
+  // by their one-step factors each step and recomputed from the exponential every kRefresh
+  // steps, so the rounding of the products spans at most kRefresh - 1 multiplications
+  // (< 1e-6 relative).
+  constexpr int kRefresh = 8;
+  v4f lb4, eq, eb, q, nb2;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) lb4[k] = 2.0f * lb2[k];
+  for (int k = 0; k < 4; ++k) {
+    lb4[k] = 2.0f * lb2[k];
+    eq[k] = __builtin_amdgcn_exp2f(lq2[k]);
+    eb[k] = __builtin_amdgcn_exp2f(lb4[k]);
+    // held in registers: otherwise the allocator recomputes the exponentials in the loop
+    asm volatile("" : "+v"(eq[k]), "+v"(eb[k]));
+  }
+  float ea = __builtin_amdgcn_exp2f(la2);
+  asm volatile("" : "+v"(ea));
+  // alpha_0 lambda~_1 is not needed until the end: parked in the (idle) exchange tile
+  st4(TS + 4 * lane, accH0);
+
+  float eA = 0.f;
   float* Z = tile + 2 * Ham16::MAT;  // one buffer each: a wave's LDS accesses run in order
   float* X = Z + Ham16::MAT;
   float* Y = X + Ham16::MAT;
+  v4f gQh = v4f{0.f, 0.f, 0.f, 0.f};  // sum_t X1_p X1_a' (grad_Q = (gQh + gQh') / 2 at the end)
   float tf = 0.0f;
   for (int t = 1; t < T; ++t) {
     tf += 1.0f;
     const float tp1 = tf + 1.0f;
-    // state cost on h_t: Qc_t = D_t Q D_t, D_t = diag(exp(lgQ t))
-    v4f q, X1;
+    if ((t - 1) % kRefresh == 0) {  // uniform branch
+      eA = __builtin_amdgcn_exp2f(la2 * tp1);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      q[k] = __builtin_amdgcn_exp2f(lq2[k] * tf);
-      X1[k] = q[k] * S[k];
+      for (int k = 0; k < 4; ++k) {
+        q[k] = __builtin_amdgcn_exp2f(lq2[k] * tf);
+        nb2[k] = -rinv[k] * __builtin_amdgcn_exp2f(lb4[k] * tp1);
+      }
+    } else {
+      eA *= ea;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        q[k] *= eq[k];
+        nb2[k] *= eb[k];
+      }
     }
+    // state cost on h_t: Qc_t = D_t Q D_t, D_t = diag(exp(lgQ t))
+    v4f X1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) X1[k] = q[k] * S[k];
     v4f QX = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) QX = mfma16x16x4(Qa[s], X1[s], QX);
-    st_tile_rowmajor(Z, g, c, X1);
-    const float eA = __builtin_amdgcn_exp2f(la2 * tp1);
-    v4f al, b2;
-    {
-      const v4f QXx = swap8(QX);  // Qc h = q o QX; q is the same on primal and adjoint lanes
+    st_tile_interleaved(Z, g, c, X1);
+    v4f al;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        accLQ[k] = fmaf(tf * X1[k], QXx[k], accLQ[k]);  // t (h Qc h~ | h~ Qc h)
-        al[k] = fmaf(a4[k], eA, 1.0f);
-        L[k] = fmaf(-q[k], QX[k], L[k]) * __builtin_amdgcn_rcpf(al[k]);
-        b2[k] = __builtin_amdgcn_exp2f(lb4[k] * tp1);  // beta_t^2
-      }
+    for (int k = 0; k < 4; ++k) {
+      al[k] = fmaf(a4[k], eA, 1.0f);
+      L[k] = fmaf(-q[k], QX[k], L[k]) * __builtin_amdgcn_rcpf(al[k]);
     }
     BtL = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) BtL = mfma16x16x4(Bt[s], L[s], BtL);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) BU[k] = (-rinv[k] * b2[k]) * BtL[k];
+    for (int k = 0; k < 4; ++k) BU[k] = nb2[k] * BtL[k];
     st_tile_rowmajor(X, g, c, L);
     st_tile_rowmajor(Y, g, c, BU);
-    {
-      const v4f Lx = swap8(L), BtLx = swap8(BtL);
-      const float tea = tp1 * eA;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float gAt = S[k] * Lx[k];                // h_t lambda~_{t+1} | h~_t lambda_{t+1}
-        accA[k] = fmaf(gAt, eA, accA[k]);
-        accLA[k] = fmaf(gAt, tea, accLA[k]);
-        const float w = BU[k] * BtLx[k];
-        sP[k] += w;
-        sPt[k] = fmaf(tp1, w, sPt[k]);
-      }
-    }
     // h_{t+1} = alpha_t h_t + B (beta o U)
     v4f Sn = al * S;
 #pragma unroll
     for (int s = 0; s < 4; ++s) Sn = mfma16x16x4(Bm[s], BU[s], Sn);
-    S = Sn;
     wave_sync();  // Z, X, Y written
-    gQ = mfma_cross(Z, Z, g, c, gQ);
+    // Primal / adjoint cross terms: the partner column c ^ 8 of X1, L and beta o U read back
+    // from the tiles (LDS reads instead of cross-lane moves on the vector ALU).  Each term is
+    // summed over the two lanes of a problem at the end, so either factor may come from the
+    // partner:  t (h Qc h~ + h~ Qc h),  h_t lambda~_{t+1} + h~_t lambda_{t+1},  W_t.
+    {
+      const int cx = c ^ 8;
+      const int ix = 4 * (cx & 3) + (cx >> 2);
+      const float tea = tp1 * eA;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int row = (4 * g + k) * Ham16::LD;
+        const float X1x = Z[row + ix], Lx = X[row + cx], BUx = Y[row + cx];
+        accLQ[k] = fmaf(tf * QX[k], X1x, accLQ[k]);
+        const float gAt = S[k] * Lx;
+        accA[k] = fmaf(gAt, eA, accA[k]);
+        accLA[k] = fmaf(gAt, tea, accLA[k]);
+        const float w = BtL[k] * BUx;
+        sP[k] += w;
+        sPt[k] = fmaf(tp1, w, sPt[k]);
+      }
+    }
+    S = Sn;
+    gQh = mfma_half_cross(Z, g, c, gQh);
     gB = mfma_cross(X, Y, g, c, gB);
   }
+  accH0 = ld4(TS + 4 * lane);
+
+  // grad_Q sum over the steps t >= 1: gQh + gQh' (the transpose through an LDS tile)
+  wave_sync();
+  st_tile_rowmajor(Z, g, c, gQh);
+  wave_sync();
+  gQ += gQh + ld4(Z + c * Ham16::LD + 4 * g);
 
   // ---- terminal: grad Q_f = sym(h_T h~_T'), certificate lambda_T = Q_f h_T (row layout) ----
   wave_sync();
@@ -306,6 +368,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   wave_sync();
   unsigned bad = 0u;
   float fin = 0.f;
+  float gmax = 0.f;  // largest guarded gradient magnitude of the lane
 #pragma unroll
   for (int pa = 0; pa < 2; ++pa) {
     const int jj = 4 * pa + g;
@@ -317,13 +380,20 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     const float* qfp = Qf + pp * 256;
     float fh = 0.f, fhb = 0.f;
     const float hc = TS[jj * Ham16::LD + c], hbc = TS[(8 + jj) * Ham16::LD + c];
+    float gq[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const float qf = 0.5f * (qfp[c * 16 + k] + qfp[k * 16 + c]);
-      fh = fmaf(qf, hv[k], fh);
-      fhb = fmaf(qf, hbv[k], fhb);
-      fin += fabsf(0.5f * fmaf(hc, hbv[k], hbc * hv[k]));  // grad Q_f row c (stored below)
+      const float qf2 = qfp[c * 16 + k] + qfp[k * 16 + c];  // 2 sym(Q_f)
+      fh = fmaf(qf2, hv[k], fh);
+      fhb = fmaf(qf2, hbv[k], fhb);
+      gq[k] = 0.5f * fmaf(hc, hbv[k], hbc * hv[k]);        // grad Q_f row c
+      fin += fabsf(gq[k]);
+      gmax = fmaxf(gmax, fabsf(gq[k]));
     }
+    fh *= 0.5f;
+    fhb *= 0.5f;
+    // stored now; a group that fails the certificate is rewritten by the stable path
+    st_global_row<16>(gQf + (pp * 16 + c) * 16, gq);
     const float E1 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(lam - fh))));
     const float E2 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(lamb - fhb))));
     const float M1 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(fh) + fabsf(lam))));
@@ -357,15 +427,12 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     return;
   }
 
-  int flags = 0;
+  // Past the certificate every output of the group is finite (their magnitudes sum to the
+  // finite `fin`), so the guard reduces to the largest magnitude against the limit.  The
+  // reference's guard covers A_diag, B, Q, R_inv, Q_f and h0, not the log-discounts.
   if (!adj) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      // the reference's guard covers A_diag, B, Q, R_inv, Q_f and h0, not the log-discounts
-      flag_value<16>(fA[k], grad_limit, flags);
-      flag_value<16>(fR[k], grad_limit, flags);
-      flag_value<16>(fH0[k], grad_limit, flags);
-    }
+    for (int k = 0; k < 4; ++k) gmax = fmaxf(gmax, fmaxf(fabsf(fA[k]), fmaxf(fabsf(fR[k]), fabsf(fH0[k]))));
     st4(gA + p * 16 + 4 * g, fA);
     st4(glgB + p * 16 + 4 * g, fLB);
     st4(gRinv + p * 16 + 4 * g, fR);
@@ -373,33 +440,17 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     st4(gh0 + p * 16 + 4 * g, fH0);
     if (g == 0) glgA[p] = la_sum;
   }
-#pragma unroll
-  for (int pa = 0; pa < 2; ++pa) {
-    const int jj = 4 * pa + g;
-    const int64_t pp = p0 + jj;
-    float hv[16], hbv[16], gq[16];
-    ld_row<16>(TS + jj * Ham16::LD, hv);
-    ld_row<16>(TS + (8 + jj) * Ham16::LD, hbv);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      gq[k] = 0.5f * fmaf(hv[c], hbv[k], hbv[c] * hv[k]);
-      flag_value<16>(gq[k], grad_limit, flags);
-    }
-    st_global_row<16>(gQf + (pp * 16 + c) * 16, gq);
-  }
   // group sums of grad_B / grad_Q: [i = 4g + r][j = c]
   float* ob = gBg + (DIRECT ? n : G) * 256;
   float* oq = gQg + (DIRECT ? n : G) * 256;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    if (DIRECT) {  // the token's head sums; otherwise headsum_kernel checks the completed sums
-      flag_value<16>(gB[r], grad_limit, flags);
-      flag_value<16>(gQ[r], grad_limit, flags);
-    }
+    if (DIRECT)  // the token's head sums; otherwise headsum_kernel checks the completed sums
+      gmax = fmaxf(gmax, fmaxf(fabsf(gB[r]), fabsf(gQ[r])));
     ob[(4 * g + r) * 16 + c] = gB[r];
     oq[(4 * g + r) * 16 + c] = gQ[r];
   }
-  if (flags && status != nullptr) atomicOr(status, flags);
+  if (gmax >= grad_limit && status != nullptr) atomicOr(status, TTC_LQR_STATUS_LARGE);
 }
 
 }  // namespace ttc

@@ -127,7 +127,7 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
     aug[D + 1] = aug[D + 2] = aug[D + 3] = 0.f;
     float piv;
     int pos;
-    gauss_jordan<D, D + 4>(aug, li, prow, piv, pos);
+    gauss_jordan<D, D + 4, 0, D + 1>(aug, li, prow, piv, pos);
     TS[(8 + jj) * LDT + pos] = -aug[D] / piv;  // adjoint column of problem jj
   }
   __syncthreads();

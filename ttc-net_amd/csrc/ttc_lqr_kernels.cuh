@@ -189,8 +189,11 @@ __device__ __forceinline__ double pivot_recip(double x) { return 1.0 / x; }
 // CHUNK > 0 reads the pivot row CHUNK elements at a time, each chunk's loads followed by its
 // updates (a scheduling barrier keeps the loads from being hoisted): fewer live registers
 // for kernels whose peak is this elimination, one LDS latency per chunk instead of one per row.
-template <int D, int W, int CHUNK = 0, typename R>
+// NC <= W: the columns that carry data (the rest is padding to whole 16-byte vectors and is
+// left as it is).
+template <int D, int W, int CHUNK = 0, int NC = W, typename R>
 __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& mypiv, int& pos) {
+  static_assert(NC > D && NC <= W, "data columns");
   constexpr unsigned kIdxBits = (D == 16) ? 4u : (D == 32 ? 5u : 6u);
   constexpr unsigned kIdxMask = (1u << kIdxBits) - 1u;
   constexpr int VN = V16<R>::N;
@@ -223,7 +226,7 @@ __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& my
       const R inv = D == 16 ? pivot_recip(pkv) : R(1) / pkv;  // (wider: register pressure)
       const R f = me ? R(0) : aug[k] * inv;
 #pragma unroll
-      for (int c = k + 1; c < W; ++c) aug[c] = fma(-f, pr[c], aug[c]);
+      for (int c = k + 1; c < NC; ++c) aug[c] = fma(-f, pr[c], aug[c]);
     } else {
       static_assert(CHUNK % VN == 0 && W % CHUNK == 0, "pivot-row chunks");
       pkv = prow[k];
@@ -236,7 +239,7 @@ __device__ __forceinline__ void gauss_jordan(R (&aug)[W], int li, R* prow, R& my
         for (int c = 0; c < CHUNK; c += VN) V16<R>::ld(prow + c0 + c, pr + c);
 #pragma unroll
         for (int c = 0; c < CHUNK; ++c)
-          if (c0 + c > k) aug[c0 + c] = fma(-f, pr[c], aug[c0 + c]);
+          if (c0 + c > k && c0 + c < NC) aug[c0 + c] = fma(-f, pr[c], aug[c0 + c]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }

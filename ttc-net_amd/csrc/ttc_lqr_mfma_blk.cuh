@@ -923,7 +923,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       wave_sync();  // all rows read before the pivot-row buffer (aliasing them) is written
       float piv;
       int pos;
-      gauss_jordan<D, D + 4, (D + 4) % 8 == 0 ? 8 : 4>(aug, li, region(qr[pa]), piv, pos);
+      gauss_jordan<D, D + 4, (D + 4) % 8 == 0 ? 8 : 4, D + 1>(aug, li, region(qr[pa]), piv, pos);
       const float u0 = -aug[D] / piv;
       if (store) {
         if (WRITE_U) u_out[po0[pa] * D + pos] = u0;
