@@ -49,6 +49,8 @@ struct HamW {
   static constexpr int OFF_RED = OFF_PV + NW * PPP * PROW;
   static constexpr int FLOATS = OFF_RED + NW * 8;
   static constexpr size_t LDS_BYTES = sizeof(float) * FLOATS;
+  // after the rollout the NW x NW grad_Q tiles are exchanged through the tile regions
+  static_assert(NW * NW * RM <= OFF_TS, "grad_Q exchange fits the rollout tiles");
 };
 
 // acc += sum_J M[I][J] X_J: row block I of a D x D by D x 16 product, X_J lane-major in LDS.
@@ -73,6 +75,20 @@ __device__ __forceinline__ void cross_blocks(const float* Xi, const float* Y0, i
     const v4f b = ld4(Y0 + J * RM + c * Ham16::LD + 4 * (g ^ 2));
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc[J] = mfma16x16x4(a[s], b[s], acc[J]);
+  }
+}
+
+// acc[J] += X_I,p X_J,a' (primal trajectories of block I against the adjoints of block J),
+// tiles stored by st_tile_interleaved: acc[J][i][j] += sum_{k < 8} X_I[i][k] X_J[j][k + 8].
+// The full X_I Pi X_J' is acc[I][J] + acc[J][I]', formed once after the rollout.
+template <int NW, int RM>
+__device__ __forceinline__ void half_cross_blocks(const float* Xi, const float* X0, int g, int c, v4f (&acc)[NW]) {
+  const v4f a = ld4(Xi + c * Ham16::LD + 4 * g);
+#pragma unroll
+  for (int J = 0; J < NW; ++J) {
+    const v4f b = ld4(X0 + J * RM + c * Ham16::LD + 4 * g);
+    acc[J] = mfma16x16x4(a[0], b[2], acc[J]);
+    acc[J] = mfma16x16x4(a[1], b[3], acc[J]);
   }
 }
 
@@ -253,63 +269,100 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
   //   grad lgB:   (t+1) beta (u B'lambda~ + w B'lambda) = 2 (t+1) W,
   //   grad R_inv: -u w / R_inv^2                          = W / R_inv,
   // so the loop sums W and (t+1) W (sP, sPt; one lane of each pair suffices).
-  v4f lb4;
+  // Discounts by recurrence: q_t = exp(lgQ t), e^{lgA (t+1)} and -R_inv beta_t^2 are multiplied
+  // by their one-step factors each step and recomputed from the exponential every kRefresh
+  // steps, so the rounding of the products spans at most kRefresh - 1 multiplications
+  // (< 1e-6 relative).
+  constexpr int kRefresh = 8;
+  v4f lb4, eq, eb, q, nb2;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) lb4[k] = 2.0f * lb2[k];
+  for (int k = 0; k < 4; ++k) {
+    lb4[k] = 2.0f * lb2[k];
+    eq[k] = __builtin_amdgcn_exp2f(lq2[k]);
+    eb[k] = __builtin_amdgcn_exp2f(lb4[k]);
+    // held in registers: otherwise the allocator recomputes the exponentials in the loop
+    asm volatile("" : "+v"(eq[k]), "+v"(eb[k]));
+  }
+  float ea = __builtin_amdgcn_exp2f(la2);
+  asm volatile("" : "+v"(ea));
+  float eA = 0.f;
+  // Primal / adjoint cross terms take the partner column c ^ 8 of X1, Lambda and beta o U
+  // from this wave's own row-major tiles (LDS reads instead of cross-lane moves; each term is
+  // summed over the two lanes of a problem at the end, so either factor may come from the
+  // partner).  Z = q o S is stored with interleaved trajectory columns (st_tile_interleaved):
+  // its partner column is at (4 (c & 3) + (c >> 2)) ^ 2.
+  const int cx = c ^ 8;
+  const int ix = (4 * (c & 3) + (c >> 2)) ^ 2;
   float tf = 0.0f;
   for (int t = 1; t < T; ++t) {
     tf += 1.0f;
     const float tp1 = tf + 1.0f;
-    // state cost on h_t: Qc_t = D_t Q D_t, D_t = diag(exp(lgQ t))
-    v4f q, X1;
+    if ((t - 1) % kRefresh == 0) {  // uniform branch
+      eA = __builtin_amdgcn_exp2f(la2 * tp1);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      q[k] = __builtin_amdgcn_exp2f(lq2[k] * tf);
-      X1[k] = q[k] * S[k];
+      for (int k = 0; k < 4; ++k) {
+        q[k] = __builtin_amdgcn_exp2f(lq2[k] * tf);
+        nb2[k] = -rinv[k] * __builtin_amdgcn_exp2f(lb4[k] * tp1);
+      }
+    } else {
+      eA *= ea;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        q[k] *= eq[k];
+        nb2[k] *= eb[k];
+      }
     }
-    st_tile_rowmajor(ZR + I * W::RM, g, c, X1);
+    // state cost on h_t: Qc_t = D_t Q D_t, D_t = diag(exp(lgQ t))
+    v4f X1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) X1[k] = q[k] * S[k];
+    st_tile_interleaved(ZR + I * W::RM, g, c, X1);
     st4(ZL + I * W::LM + 4 * lane, X1);
     __syncthreads();  // Z written
     const v4f QX = block_product<NW>(Qa, ZL, lane, v4f{0.f, 0.f, 0.f, 0.f});
-    const float eA = __builtin_amdgcn_exp2f(la2 * tp1);
-    v4f al, b2;
-    {
-      const v4f QXx = swap8(QX);  // Qc h = q o QX; q is the same on primal and adjoint lanes
+    v4f al;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        accLQ[k] = fmaf(tf * X1[k], QXx[k], accLQ[k]);  // t (h Qc h~ | h~ Qc h)
-        al[k] = fmaf(a4[k], eA, 1.0f);
-        L[k] = fmaf(-q[k], QX[k], L[k]) * __builtin_amdgcn_rcpf(al[k]);
-        b2[k] = __builtin_amdgcn_exp2f(lb4[k] * tp1);  // beta_t^2
-      }
+    for (int k = 0; k < 4; ++k) {
+      // t (h Qc h~ | h~ Qc h): Qc h = q o QX, q the same on primal and adjoint lanes
+      accLQ[k] = fmaf(tf * QX[k], ZR[I * W::RM + (4 * g + k) * Ham16::LD + ix], accLQ[k]);
+      al[k] = fmaf(a4[k], eA, 1.0f);
+      L[k] = fmaf(-q[k], QX[k], L[k]) * __builtin_amdgcn_rcpf(al[k]);
     }
     st_tile_rowmajor(XR + I * W::RM, g, c, L);
     st4(XL + I * W::LM + 4 * lane, L);
-    cross_blocks<NW, W::RM>(ZR + I * W::RM, ZR, g, c, gQ);
+    half_cross_blocks<NW, W::RM>(ZR + I * W::RM, ZR, g, c, gQ);
     __syncthreads();  // X written, Z read
     BtL = block_product<NW>(Bt, XL, lane, v4f{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-    for (int k = 0; k < 4; ++k) BU[k] = (-rinv[k] * b2[k]) * BtL[k];
+    for (int k = 0; k < 4; ++k) BU[k] = nb2[k] * BtL[k];
     st_tile_rowmajor(YR + I * W::RM, g, c, BU);
     st4(YL + I * W::LM + 4 * lane, BU);
-    {
-      const v4f Lx = swap8(L), BtLx = swap8(BtL);
-      const float tea = tp1 * eA;
+    const float tea = tp1 * eA;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const float gAt = S[k] * Lx[k];                // h_t lambda~_{t+1} | h~_t lambda_{t+1}
-        accA[k] = fmaf(gAt, eA, accA[k]);
-        accLA[k] = fmaf(gAt, tea, accLA[k]);
-        const float w = BU[k] * BtLx[k];
-        sP[k] += w;
-        sPt[k] = fmaf(tp1, w, sPt[k]);
-      }
+    for (int k = 0; k < 4; ++k) {
+      // h_t lambda~_{t+1} | h~_t lambda_{t+1}
+      const float gAt = S[k] * XR[I * W::RM + (4 * g + k) * Ham16::LD + cx];
+      accA[k] = fmaf(gAt, eA, accA[k]);
+      accLA[k] = fmaf(gAt, tea, accLA[k]);
     }
     __syncthreads();  // Y written, X read
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float w = BtL[k] * YR[I * W::RM + (4 * g + k) * Ham16::LD + cx];  // W_t
+      sP[k] += w;
+      sPt[k] = fmaf(tp1, w, sPt[k]);
+    }
     // h_{t+1} = alpha_t h_t + B (beta o U);  grad_B += Lambda Pi (beta o U)'
     S = block_product<NW>(Bm, YL, lane, al * S);
     cross_blocks<NW, W::RM>(XR + I * W::RM, YR, g, c, gB);
   }
+  // grad_Q tiles: gQ[I][J] + gQ[J][I]' through LDS (the rollout tiles are free now)
+  __syncthreads();
+#pragma unroll
+  for (int J = 0; J < NW; ++J) st_tile_rowmajor(sm + (I * NW + J) * W::RM, g, c, gQ[J]);
+  __syncthreads();
+#pragma unroll
+  for (int J = 0; J < NW; ++J) gQ[J] += ld4(sm + (J * NW + I) * W::RM + c * Ham16::LD + 4 * g);
 
   // ---- terminal: grad Q_f = sym(h_T h~_T'), certificate lambda_T = Q_f h_T (row layout) ----
   __syncthreads();  // T == 1: the row-layout reads of TS / TL above are done
@@ -318,6 +371,7 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
   __syncthreads();
   unsigned bad = 0u;
   float fin = 0.f;
+  float gmax = 0.f;  // largest guarded gradient magnitude of the lane
 #pragma unroll 1
   for (int pa = 0; pa < 2; ++pa) {
     const int jj = (pa * NW + I) * W::PPP + slot;
@@ -330,18 +384,24 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
     float fh = 0.f, fhb = 0.f;
 #pragma unroll
     for (int k0 = 0; k0 < D; k0 += 16) {
-      float hv[16], hbv[16], qr[16];
+      float hv[16], hbv[16], qr[16], gq[16];
       ld_row<16>(hs + k0, hv);
       ld_row<16>(hbs + k0, hbv);
       ld_global_row<16>(qfp + li * D + k0, qr);
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
-        const float qf = 0.5f * (qr[k] + qfp[(k0 + k) * D + li]);
-        fh = fmaf(qf, hv[k], fh);
-        fhb = fmaf(qf, hbv[k], fhb);
-        fin += fabsf(0.5f * fmaf(hc, hbv[k], hbc * hv[k]));  // grad Q_f row li (stored below)
+        const float qf2 = qr[k] + qfp[(k0 + k) * D + li];  // 2 sym(Q_f)
+        fh = fmaf(qf2, hv[k], fh);
+        fhb = fmaf(qf2, hbv[k], fhb);
+        gq[k] = 0.5f * fmaf(hc, hbv[k], hbc * hv[k]);      // grad Q_f row li
+        fin += fabsf(gq[k]);
+        gmax = fmaxf(gmax, fabsf(gq[k]));
       }
+      // stored now; a group that fails the certificate is rewritten by the stable path
+      st_global_row<16>(gQf + (pp * D + li) * D + k0, gq);
     }
+    fh *= 0.5f;
+    fhb *= 0.5f;
     const float E1 = __uint_as_float(group_max_u32<D>(__float_as_uint(fabsf(lam - fh))));
     const float E2 = __uint_as_float(group_max_u32<D>(__float_as_uint(fabsf(lamb - fhb))));
     const float M1 = __uint_as_float(group_max_u32<D>(__float_as_uint(fabsf(fh) + fabsf(lam))));
@@ -384,41 +444,18 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
 #pragma unroll
   for (int J = 0; J < NW; ++J) la_sum += red[J * 8 + j];
 
-  int flags = 0;
+  // Past the certificate every output of the group is finite (their magnitudes sum to the
+  // finite `fin`), so the guard reduces to the largest magnitude against the limit.  The
+  // reference's guard covers A_diag, B, Q, R_inv, Q_f and h0, not the log-discounts.
   if (!adj) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      // the reference's guard covers A_diag, B, Q, R_inv, Q_f and h0, not the log-discounts
-      flag_value<D>(fA[k], grad_limit, flags);
-      flag_value<D>(fR[k], grad_limit, flags);
-      flag_value<D>(fH0[k], grad_limit, flags);
-    }
+    for (int k = 0; k < 4; ++k) gmax = fmaxf(gmax, fmaxf(fabsf(fA[k]), fmaxf(fabsf(fR[k]), fabsf(fH0[k]))));
     st4(gA + p * D + r0, fA);
     st4(glgB + p * D + r0, fLB);
     st4(gRinv + p * D + r0, fR);
     st4(glgQ + p * D + r0, fLQ);
     st4(gh0 + p * D + r0, fH0);
     if (I == 0 && g == 0) glgA[p] = la_sum;
-  }
-#pragma unroll 1
-  for (int pa = 0; pa < 2; ++pa) {
-    const int jj = (pa * NW + I) * W::PPP + slot;
-    const int64_t pp = p0 + jj;
-    const float* hs = TS + jj * LDT;
-    const float* hbs = TS + (8 + jj) * LDT;
-    const float hc = hs[li], hbc = hbs[li];
-#pragma unroll
-    for (int k0 = 0; k0 < D; k0 += 16) {
-      float hv[16], hbv[16], gq[16];
-      ld_row<16>(hs + k0, hv);
-      ld_row<16>(hbs + k0, hbv);
-#pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        gq[k] = 0.5f * fmaf(hc, hbv[k], hbc * hv[k]);
-        flag_value<D>(gq[k], grad_limit, flags);
-      }
-      st_global_row<16>(gQf + (pp * D + li) * D + k0, gq);
-    }
   }
   // group sums of grad_B / grad_Q: rows r0 + r, columns 16J + c
   float* ob = gBg + (DIRECT ? n : G) * D * D;
@@ -427,14 +464,12 @@ __global__ __launch_bounds__(HamW<D>::THREADS) __attribute__((amdgpu_waves_per_e
   for (int J = 0; J < NW; ++J)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      if (DIRECT) {  // the token's head sums; otherwise headsum_kernel checks the completed sums
-        flag_value<D>(gB[J][r], grad_limit, flags);
-        flag_value<D>(gQ[J][r], grad_limit, flags);
-      }
+      if (DIRECT)  // the token's head sums; otherwise headsum_kernel checks the completed sums
+        gmax = fmaxf(gmax, fmaxf(fabsf(gB[J][r]), fabsf(gQ[J][r])));
       ob[(r0 + r) * D + 16 * J + c] = gB[J][r];
       oq[(r0 + r) * D + 16 * J + c] = gQ[J][r];
     }
-  if (flags && status != nullptr) atomicOr(status, flags);
+  if (gmax >= grad_limit && status != nullptr) atomicOr(status, TTC_LQR_STATUS_LARGE);
 }
 
 }  // namespace ttc
