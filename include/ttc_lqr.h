@@ -148,6 +148,23 @@ int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const f
                     int32_t d, int32_t du, int32_t T, int32_t flags, float* u, float* stash,
                     int32_t* status, void* stream);
 
+/* Bytes of the forward's optional workspace: 4 * (P + 64) with TTC_LQR_FLAG_FP64_RESCUE
+ * (d <= 32), where it holds the list of problems the fp64 rescue recomputes; 0 otherwise.
+ * Same forward as fused_lqr_layer_fwd (ttc/solvers/fused_lqr.py:18-146); the reference's
+ * solver keeps no such list (its fp32 sweep solves every problem the same way). */
+size_t ttc_lqr_forward_workspace_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
+                                       int32_t T, int32_t flags);
+
+/* ttc_lqr_forward with a workspace of ttc_lqr_forward_workspace_bytes(): the fp64 rescue of
+ * a long-horizon symplectic sweep then lists its problems and runs full sweeps of 64 / d
+ * problems per wave (without it, or with a smaller one, each wave sweeps whichever of 64 / d
+ * consecutive problems are marked).  Results are identical either way. */
+int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, const float* R_inv,
+                       const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
+                       const float* log_gamma_Q, const float* h0, int64_t n_tokens, int32_t heads,
+                       int32_t d, int32_t du, int32_t T, int32_t flags, float* u, float* stash,
+                       void* workspace, size_t workspace_bytes, int32_t* status, void* stream);
+
 /* Backward: gradients of sum(d_u * u) w.r.t. the nine inputs.
  * Replaces fused_lqr_layer_bwd (ttc/solvers/fused_lqr.py:148-253).
  * u: the forward's output (needed by the fast path; may be NULL with

@@ -34,7 +34,8 @@ def test_header_declares_expected_entry_points():
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
         "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host", "ttc_lqr_fallback_bytes",
-        "ttc_lqr_backward_noalloc", "ttc_lqr_noalloc_scratch_bytes"])
+        "ttc_lqr_backward_noalloc", "ttc_lqr_noalloc_scratch_bytes", "ttc_lqr_forward_workspace_bytes",
+        "ttc_lqr_forward_ws"])
 
 
 def test_library_exports_every_declared_symbol(L):
@@ -103,6 +104,22 @@ def test_forward_argument_validation(L):
     assert _fwd(L, d=16, du=32) == 2
     assert _fwd(L, n=0) == 0                  # empty batch: nothing to do
     assert _fwd(L, null_inputs=True) == 1
+
+
+def test_forward_workspace_bytes(L):
+    """The forward's optional workspace holds the fp64 rescue's problem list: 4 bytes a
+    problem plus a 256-byte header, only under TTC_LQR_FLAG_FP64_RESCUE at d <= 32."""
+    from ttc.solvers._lib import FLAG_FP64_RESCUE
+    assert L.ttc_lqr_forward_workspace_bytes(1000, 8, 16, 16, 1024, FLAG_FP64_RESCUE) == 4 * (8000 + 64)
+    assert L.ttc_lqr_forward_workspace_bytes(1000, 8, 32, 32, 1024, FLAG_FP64_RESCUE) == 4 * (8000 + 64)
+    assert L.ttc_lqr_forward_workspace_bytes(1000, 8, 64, 64, 1024, FLAG_FP64_RESCUE) == 0
+    assert L.ttc_lqr_forward_workspace_bytes(1000, 8, 16, 16, 64, 0) == 0
+    assert L.ttc_lqr_forward_workspace_bytes(0, 8, 16, 16, 1024, FLAG_FP64_RESCUE) == 0
+    # validation of the workspace entry matches ttc_lqr_forward's
+    p = ctypes.c_void_p(16)
+    assert L.ttc_lqr_forward_ws(*([p] * 9), -1, 1, 16, 16, 1, 0, p, None, None, 0, None, None) == 1
+    assert L.ttc_lqr_forward_ws(*([p] * 9), 1, 1, 24, 24, 1, 0, p, None, None, 0, None, None) == 2
+    assert L.ttc_lqr_forward_ws(*([p] * 9), 0, 1, 16, 16, 1, 0, p, None, None, 0, None, None) == 0
 
 
 def test_backward_argument_validation(L):

@@ -290,6 +290,44 @@ def test_config5_stress(cfg, T, seed):
     check_case(f"cfg{cfg}", layer_solver_inputs(cfg, x), T, grad_limit=math.inf)
 
 
+@pytest.mark.parametrize("cfg,n_tok", [(5, 64), ("5b", 64)])
+def test_forward_workspace_packs_the_fp64_rescue(cfg, n_tok):
+    """Long horizons (T = 1024, FP64_RESCUE): ttc_lqr_forward_ws lists the problems the
+    symplectic sweep rejects and sweeps them in fp64 four to a wave; ttc_lqr_forward (no
+    workspace) sweeps each marked problem of every group of four in place.  u and the
+    V_1 / Quu_0 stash are bitwise equal, and some problems were rescued."""
+    from ttc.solvers._lib import FLAG_FP64_RESCUE, lib
+    x = make_x(cfg, n_tokens=n_tok, seed=17)
+    ins = [t.float().contiguous().cuda() for t in layer_solver_inputs(cfg, x)]
+    N, H, d = ins[0].shape
+    T = 1024
+    P = N * H
+    ptrs = [t.data_ptr() for t in ins]
+    stream = torch.cuda.current_stream().cuda_stream
+    nws = lib.ttc_lqr_forward_workspace_bytes(N, H, d, d, T, FLAG_FP64_RESCUE)
+    assert nws == 4 * (P + 64)
+    print(f"[fwd-ws cfg{cfg}] N={N} H={H} T={T}", flush=True)
+    outs = []
+    for with_ws in (False, True):
+        u = torch.full((N, H, d), 7.0, device="cuda")
+        st = torch.zeros(lib.ttc_lqr_stash_bytes(N, H, d, d, T) // 4, device="cuda")
+        status = torch.zeros(1, device="cuda", dtype=torch.int32)
+        ws = torch.full((nws,), 0xAB, device="cuda", dtype=torch.uint8)
+        rc = lib.ttc_lqr_forward_ws(*ptrs, N, H, d, d, T, FLAG_FP64_RESCUE, u.data_ptr(), st.data_ptr(),
+                                    ws.data_ptr() if with_ws else None, nws if with_ws else 0, status.data_ptr(),
+                                    stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        outs.append((u.cpu(), st.cpu(), int(status.item())))
+        if with_ws:
+            n_listed = int(ws[:4].view(torch.int32).item())
+            print(f"   {n_listed} of {P} problems rescued in fp64", flush=True)
+            assert 0 < n_listed < P
+    (u0, s0, f0), (u1, s1, f1) = outs
+    assert torch.isfinite(u0).all()
+    assert torch.equal(u0, u1) and torch.equal(s0, s1) and f0 == f1
+
+
 @pytest.mark.parametrize("cfg,n_tok,d_pad", [(4, 1, None), (4, 1, 24)])
 def test_fp64_stable_backward_d32(cfg, n_tok, d_pad):
     """The fp64 stable path at d = 32 (lqr_bwd_kernel<32, double>): a config-4 slice, and the

@@ -171,11 +171,15 @@ static StableLayout stable_layout(int64_t chunk_tokens, int H, int d, int T, boo
 
 static int fwd_d(int d, const float* a, const float* b, const float* q, const float* r, const float* qf,
                  const float* la, const float* lb, const float* lq, const float* hz, int64_t P, int H, int T, float* u,
-                 float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
+                 float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
+                 int32_t* rescue_ws = nullptr) {
   switch (d) {
-    case 16: return launch_fwd_d16(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags);
-    case 32: return launch_fwd_d32(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags);
-    case 64: return launch_fwd_d64(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags);
+    case 16:
+      return launch_fwd_d16(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags, rescue_ws);
+    case 32:
+      return launch_fwd_d32(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags, rescue_ws);
+    case 64:
+      return launch_fwd_d64(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags, rescue_ws);
   }
   return TTC_LQR_EUNSUPPORTED;
 }
@@ -268,6 +272,18 @@ static int64_t fallback_capacity(size_t bytes, int d, int du, int T, bool fp64) 
   return 8 * lo;
 }
 
+// Problems one round of the fp64 row-layout sweep holds on the current device: 64 / d problems
+// per wave, one wave per SIMD (their registers allow no more), four SIMDs per CU.  A fallback
+// pass of a multiple of this many problems fills every round it starts; each round is a serial
+// T-step sweep, so a pass that ends with a part-filled round wastes most of one.
+static int64_t fp64_round_problems(int d) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 0;
+  return (int64_t)(64 / d) * 4 * cus;
+}
+
 // Fallback region reserved by the workspace size queries; a larger workspace gives the
 // fallback larger passes (backward_core uses whatever the main chunk leaves).
 constexpr size_t kFallbackReserve = (size_t)256 << 20;
@@ -357,6 +373,10 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     int64_t Frun = fallback_capacity(workspace_bytes - L.fb, d, du, T, fp64);
     if (Frun < L.F) Frun = L.F;
     if (Frun > Pc) Frun = Pc;
+    if (fp64) {  // whole rounds of the fp64 sweep per pass (a multiple of 8 problems)
+      const int64_t rnd = fp64_round_problems(d);
+      if (rnd > 0 && rnd % 8 == 0 && Frun > rnd) Frun -= Frun % rnd;
+    }
     size_t csz[19];
     const size_t fb_stable = L.fb + compact_sizes(Frun, d, du, csz);
     const float *a = A_diag + p0 * d, *b = B + n0 * dd, *q = Q + n0 * dd, *r = R_inv + p0 * du;
@@ -880,10 +900,25 @@ size_t ttc_lqr_fallback_bytes(int64_t problems, int32_t d, int32_t du, int32_t T
   return fallback_bytes(problems, d, du, T, fp64_stable(flags, d));
 }
 
+size_t ttc_lqr_forward_workspace_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
+                                       int32_t flags) {
+  if (n_tokens <= 0 || heads <= 0 || d <= 0 || du != d || T <= 0) return 0;
+  if (!(flags & TTC_LQR_FLAG_FP64_RESCUE) || d > 32) return 0;  // only the fp64 rescue uses one
+  return ttc::rescue_ws_bytes(n_tokens * heads);
+}
+
 int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
                     const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
                     int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T, int32_t flags, float* u,
                     float* stash, int32_t* status, void* stream) {
+  return ttc_lqr_forward_ws(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, n_tokens, heads, d,
+                            du, T, flags, u, stash, nullptr, 0, status, stream);
+}
+
+int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
+                       const float* log_gamma_A, const float* log_gamma_B, const float* log_gamma_Q, const float* h0,
+                       int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T, int32_t flags, float* u,
+                       float* stash, void* workspace, size_t workspace_bytes, int32_t* status, void* stream) {
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
   if (flags & TTC_LQR_FLAG_COMPACT_STASH) return TTC_LQR_EUNSUPPORTED;  // factored entry points only
@@ -894,8 +929,12 @@ int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const f
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   float* v1 = stash;
   float* q0 = stash ? stash + P * (int64_t)d * d : nullptr;
+  // a workspace too small for the rescue list is not used (the rescue then runs unpacked)
+  const size_t need = ttc_lqr_forward_workspace_bytes(n_tokens, heads, d, du, T, flags);
+  int32_t* rws = (workspace != nullptr && need > 0 && workspace_bytes >= need) ? static_cast<int32_t*>(workspace)
+                                                                                : nullptr;
   return fwd_d(d, A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, v1, q0,
-               stash ? kStashV1 : 0, status, s, flags);
+               stash ? kStashV1 : 0, status, s, flags, rws);
 }
 
 int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,

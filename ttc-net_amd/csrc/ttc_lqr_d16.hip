@@ -5,7 +5,8 @@ namespace ttc {
 
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
+                  int32_t* rescue_ws) {
   // fp64 rescue of a symplectic sweep: without a symplectic sweep to certify (the stable
   // backward's gains, row-layout or Riccati-step kernels asked for) the sweep is fp64 throughout
   if ((flags & TTC_LQR_FLAG_FP64_RESCUE) &&
@@ -17,7 +18,7 @@ int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* 
   if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL))) {
     if (sm != STASH_GAINS && !(flags & TTC_LQR_FLAG_RICCATI_STEPS))
       return launch_fwd_d16_sym(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s,
-                                (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0);
+                                (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0, rescue_ws);
     return launch_fwd_d16_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
   }
   return launch_fwd<16, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);

@@ -8,7 +8,8 @@ namespace ttc {
 template <int SM, bool WU>
 static void launch_s16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                       float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool fp64_rescue) {
+                       float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool fp64_rescue,
+                       int32_t* rescue_ws) {
   using G = MB<16, 4, 1, true>;
   using GT = MB<16, 4, 1, true, true>;
   const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
@@ -22,7 +23,8 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
   if (fp64_rescue) {
     // long horizons: the rejected problems are the ill-conditioned ones, recomputed by the
     // pivoted row-layout sweep in fp64
-    launch_rescue_k<16, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    launch_rescue_k<16, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s,
+                                        rescue_ws);
     return;
   }
   // rescue: the per-step Riccati kernel on the marked problems (its own breakdown guard
@@ -38,17 +40,20 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
 int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                       bool fp64_rescue) {
+                       bool fp64_rescue, int32_t* rescue_ws) {
   if (P <= 0) return TTC_LQR_OK;
   switch (sm) {
     case STASH_NONE:
-      launch_s16<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue);
+      launch_s16<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue,
+                                   rescue_ws);
       break;
     case STASH_V1:
       if (u != nullptr)
-        launch_s16<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue);
+        launch_s16<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue,
+                                   rescue_ws);
       else
-        launch_s16<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue);
+        launch_s16<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue,
+                                    rescue_ws);
       break;
     default:
       return TTC_LQR_EINVAL;

@@ -5,7 +5,8 @@ namespace ttc {
 
 int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
+                  int32_t* rescue_ws) {
   // fp32 sweeps without per-step gains run on the matrix cores unless the row-layout kernel
   // is asked for: the certified symplectic sweep by default (even head counts), per-step
   // Riccati when asked for
@@ -15,7 +16,8 @@ int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* 
     flags |= TTC_LQR_FLAG_FP64_RICCATI;
   if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL)) && sm != STASH_GAINS)
     return launch_fwd_d32_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s,
-                               !(flags & TTC_LQR_FLAG_RICCATI_STEPS), (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0);
+                               !(flags & TTC_LQR_FLAG_RICCATI_STEPS), (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0,
+                               rescue_ws);
   return launch_fwd<32, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);
 }
 

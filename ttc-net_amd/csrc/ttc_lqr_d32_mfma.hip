@@ -25,7 +25,7 @@ template <int SM, bool WU>
 static void launch_b32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool sym,
-                       bool fp64_rescue) {
+                       bool fp64_rescue, int32_t* rescue_ws) {
   if (fp64_rescue) {
     // long horizons (even head counts): the symplectic sweep, its rejected problems recomputed
     // by the pivoted row-layout sweep in fp64
@@ -33,7 +33,8 @@ static void launch_b32(const float* A, const float* B, const float* Q, const flo
       launch_b32_w<SM, WU, 2, 4, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
     else
       launch_b32_w<SM, WU, 2, 1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
-    launch_rescue_k<32, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s);
+    launch_rescue_k<32, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s,
+                                        rescue_ws);
     return;
   }
   if (sym && H % 2 == 0) {
@@ -60,20 +61,21 @@ static void launch_b32(const float* A, const float* B, const float* Q, const flo
 int launch_fwd_d32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                        bool sym, bool fp64_rescue) {
+                        bool sym, bool fp64_rescue, int32_t* rescue_ws) {
   if (P <= 0) return TTC_LQR_OK;
   if (fp64_rescue && H % 2 != 0) return TTC_LQR_EINVAL;  // the symplectic sweep pairs heads of one token
   switch (sm) {
     case STASH_NONE:
-      launch_b32<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym, fp64_rescue);
+      launch_b32<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym, fp64_rescue,
+                                   rescue_ws);
       break;
     case STASH_V1:
       if (u != nullptr)
         launch_b32<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym,
-                                   fp64_rescue);
+                                   fp64_rescue, rescue_ws);
       else
         launch_b32<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, sym,
-                                    fp64_rescue);
+                                    fp64_rescue, rescue_ws);
       break;
     default:
       return TTC_LQR_EINVAL;

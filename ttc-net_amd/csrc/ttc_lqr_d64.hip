@@ -5,7 +5,8 @@ namespace ttc {
 
 int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags) {
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
+                  int32_t* /*rescue_ws: no fp64 rescue at d = 64*/) {
   // fp32 sweeps without per-step gains run on the matrix cores unless the row-layout kernel
   // is asked for: the certified symplectic sweep by default (head counts that are multiples
   // of 4), per-step Riccati when asked for

@@ -1,12 +1,17 @@
 // ttc_lqr_internal.h -- per-D kernel launchers shared by the translation units of libttc_lqr.so.
 //
 // Forward launchers take a stash mode `sm` (STASH_NONE / STASH_GAINS / STASH_V1, see
-// ttc_lqr_kernels.cuh) and its two buffers st_a (gains or V_1) and st_b (Quu_0).
+// ttc_lqr_kernels.cuh) and its two buffers st_a (gains or V_1) and st_b (Quu_0); rescue_ws
+// (optional, rescue_ws_bytes(P)) lets the fp64 rescue of a symplectic sweep pack its problems.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 namespace ttc {
+// Bytes of the fp64 rescue's problem list for P problems: a 64-word header (the count in
+// word 0), then one index per problem.
+inline size_t rescue_ws_bytes(int64_t P) { return (size_t)(64 + (P > 0 ? P : 0)) * sizeof(int32_t); }
+
 int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s);
@@ -15,18 +20,19 @@ int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const fl
 int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                       bool fp64_rescue);
+                       bool fp64_rescue, int32_t* rescue_ws = nullptr);
 int launch_fwd_d32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                        bool sym, bool fp64_rescue);
+                        bool sym, bool fp64_rescue, int32_t* rescue_ws = nullptr);
 int launch_fwd_d64_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
                         bool sym);
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
+                  int32_t* rescue_ws = nullptr);
 int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
@@ -41,7 +47,8 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   hipStream_t s, bool fp64);
 int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
+                  int32_t* rescue_ws = nullptr);
 int launch_bwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
@@ -55,7 +62,8 @@ int launch_ham_d32(const float* A, const float* B, const float* Q, const float* 
                   hipStream_t s, bool fp64);
 int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags);
+                  float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
+                  int32_t* rescue_ws = nullptr);
 int launch_bwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,

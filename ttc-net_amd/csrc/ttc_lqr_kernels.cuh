@@ -1185,10 +1185,80 @@ __global__ __launch_bounds__(64) void lqr_rescue_fine_kernel(
                                 Bs, S, li, valid ? pq : base, valid);
 }
 
+// The fp64 rescue with a workspace (ttc_lqr_forward_ws): the marked problems are listed first,
+// then a grid of one wave per SIMD takes them PPW at a time, so that every sweep it runs is
+// full (the clustered or sparse markers leave most groups of PPW consecutive problems
+// part-filled).  The list's order is whatever the atomics give; each problem is solved on its
+// own, so the results do not depend on it.  Workspace: [0] the count, [64..] the list.
+static __global__ void rescue_list_reset_kernel(int32_t* __restrict__ ws) { ws[0] = 0; }
+
+static __global__ __launch_bounds__(256) void rescue_list_kernel(int64_t P, const float* __restrict__ mark, int64_t mstride,
+                                                          int32_t* __restrict__ ws, const int* __restrict__ status) {
+  if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool m = p < P && isnan(mark[p * mstride]);
+  const unsigned long long b = __ballot(m);
+  if (b == 0ull) return;  // uniform over the wave
+  const int lane = threadIdx.x & 63;
+  int base = 0;
+  if (lane == 0) base = atomicAdd(ws, (int)__popcll(b));
+  base = __shfl(base, 0, 64);
+  if (m) ws[64 + base + (int)__popcll(b & ((1ull << lane) - 1ull))] = (int32_t)p;
+}
+
+template <int D, int SM, bool WRITE_U, typename R>
+__global__ __launch_bounds__(64) void lqr_rescue_listed_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
+    int H, int T, float* __restrict__ u_out, float* __restrict__ kstash, float* __restrict__ q0stash,
+    int* __restrict__ status, const int32_t* __restrict__ ws) {
+  constexpr int PPW = Rescue<D, R>::PPW;
+  extern __shared__ __align__(16) float smem_rf[];
+  R* const smem = reinterpret_cast<R*>(smem_rf);
+  const int lane = threadIdx.x;
+  const int qo = lane / D;
+  const int li = lane % D;
+  R* Bs = smem + qo * Rescue<D, R>::PER;
+  R* S = Bs + Geo<D>::MAT;
+  if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
+  const int64_t n = __builtin_amdgcn_readfirstlane(ws[0]);
+  const int32_t* list = ws + 64;
+  for (int64_t b0 = (int64_t)blockIdx.x * PPW; b0 < n; b0 += (int64_t)gridDim.x * PPW) {
+    const int64_t k = b0 + qo;
+    const bool valid = k < n;
+    const int64_t p = list[valid ? k : b0];
+    rescue_one<D, SM, WRITE_U, R>(A_diag, Bg, Qg, Rinv, Qf, lgA, lgB, lgQ, h0, H, T, u_out, kstash, q0stash, status,
+                                  Bs, S, li, p, valid);
+  }
+}
+
+// CUs of the current device (0 if unknown).
+inline int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return cus;
+}
+
 template <int D, int SM, bool WU, typename RT = float>
 inline void launch_rescue_k(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                             const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
-                            int T, float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s) {
+                            int T, float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s,
+                            int32_t* rescue_ws = nullptr) {
+  const int cus = (std::is_same<RT, double>::value && rescue_ws != nullptr) ? device_cus() : 0;
+  if (cus > 0 && P < ((int64_t)1 << 31)) {
+    const float* mark = WU ? u : st_b;
+    const int64_t mstride = WU ? D : (int64_t)D * D;
+    hipLaunchKernelGGL(rescue_list_reset_kernel, dim3(1), dim3(1), 0, s, rescue_ws);
+    hipLaunchKernelGGL(rescue_list_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, P, mark, mstride,
+                       rescue_ws, status);
+    hipLaunchKernelGGL((lqr_rescue_listed_kernel<D, SM, WU, RT>), dim3((unsigned)(4 * cus)), dim3(64),
+                       (Rescue<D, RT>::LDS_BYTES), s, A, B, Q, R, Qf, lA, lB, lQ, h0, H, T, u, st_a, st_b, status,
+                       rescue_ws);
+    return;
+  }
   if (std::is_same<RT, double>::value) {
     const int64_t blocks = (P + Rescue<D, RT>::PPW - 1) / Rescue<D, RT>::PPW;
     hipLaunchKernelGGL((lqr_rescue_fine_kernel<D, SM, WU, RT>), dim3((unsigned)blocks), dim3(64),

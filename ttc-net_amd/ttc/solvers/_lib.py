@@ -58,6 +58,11 @@ def _load():
     L.ttc_lqr_fallback_bytes.argtypes = [i64, i32, i32, i32, i32]
     L.ttc_lqr_forward.restype = ctypes.c_int
     L.ttc_lqr_forward.argtypes = [f32p] * 9 + [i64, i32, i32, i32, i32, i32] + [f32p, f32p, f32p, ctypes.c_void_p]
+    L.ttc_lqr_forward_workspace_bytes.restype = sz
+    L.ttc_lqr_forward_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32]
+    L.ttc_lqr_forward_ws.restype = ctypes.c_int
+    L.ttc_lqr_forward_ws.argtypes = ([f32p] * 9 + [i64, i32, i32, i32, i32, i32] + [f32p, f32p, ctypes.c_void_p, sz]
+                                     + [f32p, ctypes.c_void_p])
     L.ttc_lqr_backward.restype = ctypes.c_int
     L.ttc_lqr_backward.argtypes = ([f32p] * 11 + [i64, i32, i32, i32, i32, i32] + [f32p] + [f32p] * 9
                                    + [ctypes.c_void_p, sz, ctypes.c_float, f32p, ctypes.POINTER(ctypes.c_int64),

@@ -190,10 +190,15 @@ class HipLQRSolveFunc(torch.autograd.Function):
         keep = (need_grad and bs > 0 and not stable_backward
                 and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev))))
         st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32) if keep else None
+        # the fp64 rescue's problem list (4 bytes a problem; long horizons only)
+        fws_bytes = lib.ttc_lqr_forward_workspace_bytes(bs, nh, Dp, Dp, T, flags)
+        fws = torch.empty(fws_bytes, device=dev, dtype=torch.uint8) if fws_bytes > 0 else None
         with torch.cuda.device(dev):
-            rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, flags, u.data_ptr(),
-                                     None if st is None else st.data_ptr(), status.data_ptr(), _stream_handle(dev))
-        check(rc, "ttc_lqr_forward")
+            rc = lib.ttc_lqr_forward_ws(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, flags, u.data_ptr(),
+                                        None if st is None else st.data_ptr(),
+                                        None if fws is None else fws.data_ptr(), fws_bytes, status.data_ptr(),
+                                        _stream_handle(dev))
+        check(rc, "ttc_lqr_forward_ws")
         if int(status.item()) & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
