@@ -110,6 +110,14 @@ def test_factored_config_slices(cfg, n_tok, stash):
     check_factored(f"cfg{cfg}", factored_inputs(cfg, n_tok), CONFIGS[cfg]["T"], stash=stash)
 
 
+@pytest.mark.parametrize("stash", ["always", "compact"])
+def test_factored_long_horizon_fp64_rescue(stash):
+    """Config 5 at T = 1024 on the factored entry points: the symplectic sweep's rejected
+    problems recomputed in fp64 from the rescue list in the factored workspace; stress
+    gradients exceed the reference's 1e6 guard, so no limit."""
+    check_factored("cfg5-factored", factored_inputs(5, 4, seed=6), 1024, stash=stash, grad_limit=math.inf)
+
+
 @pytest.mark.parametrize("rb,rq", [(8, 40), (1, 64), (17, 3)])
 def test_factored_ranks(rb, rq):
     """Ranks below, between and at the 16-wide tiles of the projection / reduction kernels."""

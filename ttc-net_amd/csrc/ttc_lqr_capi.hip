@@ -490,7 +490,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
 // for bf16 storage the chunk's inputs (and d_u) and per-problem gradients in fp32; last,
 // ttc_lqr_backward's own workspace for the chunk.
 struct FactLayout {
-  size_t bas, gbas, Bx, Qx, Qfx, gB, gQ, gQf, part, cin[10], cg[9], v1t, q0t, inner, total;
+  size_t bas, gbas, Bx, Qx, Qfx, gB, gQ, gQf, part, cin[10], cg[9], v1t, q0t, rlist, inner, total;
 };
 
 // Elements of the per-problem / per-token arrays of a chunk, in argument order:
@@ -556,6 +556,10 @@ static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, 
     off += align256(P * Eq * sizeof(float));
     L.q0t = off;
     off += align256(P * (size_t)du * du * sizeof(float));
+  }
+  if (!backward && fp64) {  // the fp64 rescue's problem list of the chunk
+    L.rlist = off;
+    off += align256(rescue_ws_bytes((int64_t)P));
   }
   if (backward) {
     L.inner = off;
@@ -679,8 +683,9 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
       v1 = reinterpret_cast<float*>(ws + L.v1t);
       q0 = reinterpret_cast<float*>(ws + L.q0t);
     }
+    int32_t* rlist = fp64 ? reinterpret_cast<int32_t*>(ws + L.rlist) : nullptr;
     rc = fwd_d(d, a, Bx, Qx, r, Qfx, la, lb, lq, hz, nc * H, H, T, u + p0 * du, v1, q0, stash ? kStashV1 : 0, status,
-               s, flags & ~TTC_LQR_FLAG_COMPACT_STASH);
+               s, flags & ~TTC_LQR_FLAG_COMPACT_STASH, rlist);
     if (compact && rc == TTC_LQR_OK) rc = launch_pack_upper(v1, nc * H, d, stash + p0 * (dd + d) / 2, s);
   }
   return rc;
