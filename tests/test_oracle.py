@@ -216,6 +216,24 @@ def test_fp64_limit_on_undiscounted_stress_fixture():
     assert 1e-3 < rel(g["A_diag"], z["out_A_diag"]) < 5e-2 and 1e-3 < rel(g["B"], z["out_B"]) < 1e-1
 
 
+def test_reference_fp32_solvers_overflow_on_undiscounted_fixture():
+    """The reference's own solvers in fp32 (oracle/ref_torch.py restates `riccati` =
+    direct_lqr_solve and `kkt` = kkt_lqr_solve) lose the 32 config-5b problems of
+    oracle_cfg5b_undiscounted.npz: their u is non-finite (the value matrices, ~1e17 in exact
+    arithmetic, overflow fp32's Riccati recursion), where the 40-digit u is finite and the
+    HIP solver's is within 1e-7 of it (tests/test_hip_parity.py, the committed goldens)."""
+    from oracle.ref_torch import kkt_solve, riccati_solve
+    z = np.load(os.path.join(GOLDEN, "oracle_cfg5b_undiscounted.npz"))
+    ins = [torch.from_numpy(z[f"in_{k}"]).float() for k in NAMES]
+    assert np.isfinite(z["out_u"]).all()
+    with torch.no_grad():
+        for name, fn in (("riccati", riccati_solve), ("kkt", kkt_solve)):
+            u = fn(*ins, int(z["T"]))
+            bad = int((~torch.isfinite(u)).sum())
+            print(f"reference {name} in fp32: {bad} of {u.numel()} entries of u non-finite")
+            assert bad > 0, name
+
+
 def test_open_loop_costates_fail_on_stress_problem():
     """Why the oracle (and the kernels) use closed-loop costates: the reference's
     open-loop sweep lambda_k = Qc h + A lambda_{k+1} loses the T=1024 stress
