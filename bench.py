@@ -400,7 +400,7 @@ def main():
     # the fp32 matrix peak as a whole
     long_h = T >= 512 and d <= 32
     if long_h:
-        kern += " + fp64 row-layout rescue of the rejected problems (lqr_rescue_fine_kernel<double>)"
+        kern += " + fp64 row-layout rescue of the rejected problems (lqr_rescue_listed_kernel<double>)"
     out = {
         "metric": metric_for(d, T),
         "value": P / step_s,

@@ -14,7 +14,7 @@
 
 namespace ttc {
 
-constexpr int kStashV1 = 2;     // STASH_V1 of ttc_lqr_kernels.cuh
+constexpr int kStashV1 = 2;     // STASH_V1 of ttc_lqr_kernels.hpp
 constexpr int kStashGains = 1;  // STASH_GAINS
 
 // grad_B / grad_Q: sum the per-problem partials over the H heads of each token.

@@ -1,6 +1,6 @@
 // ttc_lqr_d16_ham.hip -- launcher of the d = du = 16 matrix-core Hamiltonian backward
-// (head groups of 8; see ttc_lqr_ham16.cuh).
-#include "ttc_lqr_ham16.cuh"
+// (head groups of 8; see ttc_lqr_ham16.hpp).
+#include "ttc_lqr_ham16.hpp"
 
 namespace ttc {
 

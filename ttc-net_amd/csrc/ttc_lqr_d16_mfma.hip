@@ -1,5 +1,5 @@
 // ttc_lqr_d16_mfma.hip -- launcher of the d = du = 16 matrix-core forward kernel.
-#include "ttc_lqr_mfma16.cuh"
+#include "ttc_lqr_mfma16.hpp"
 
 namespace ttc {
 

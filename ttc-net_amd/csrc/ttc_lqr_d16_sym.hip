@@ -1,7 +1,7 @@
 // ttc_lqr_d16_sym.hip -- launcher of the d = du = 16 symplectic matrix-core forward kernel
 // and its rescue pass (the per-step Riccati kernel on the problems the certificate rejects, or
 // the fp64 row-layout sweep under TTC_LQR_FLAG_FP64_RESCUE).
-#include "ttc_lqr_mfma_blk.cuh"
+#include "ttc_lqr_mfma_blk.hpp"
 
 namespace ttc {
 

@@ -1,6 +1,6 @@
 // ttc_lqr_d32_ham.hip -- launcher of the d = du = 32 matrix-core Hamiltonian backward
-// (head groups of 8, 32/16 waves per group; see ttc_lqr_hamw.cuh).
-#include "ttc_lqr_hamw.cuh"
+// (head groups of 8, 32/16 waves per group; see ttc_lqr_hamw.hpp).
+#include "ttc_lqr_hamw.hpp"
 
 namespace ttc {
 

@@ -1,5 +1,5 @@
 // ttc_lqr_d64.hip -- kernels instantiated for d = du = 64.
-#include "ttc_lqr_kernels.cuh"
+#include "ttc_lqr_kernels.hpp"
 
 namespace ttc {
 

@@ -1,7 +1,7 @@
 // ttc_lqr_d64_mfma.hip -- launcher of the d = du = 64 matrix-core forward kernels (the
 // certified symplectic sweep, or blocked-Cholesky Riccati steps) and their rescue pass
 // (row-layout recompute of the problems the certificate rejects or whose Cholesky broke down).
-#include "ttc_lqr_mfma_blk.cuh"
+#include "ttc_lqr_mfma_blk.hpp"
 
 namespace ttc {
 

@@ -1,5 +1,5 @@
 #pragma once
-// ttc_lqr_ham16.cuh -- certified Hamiltonian backward for d = du = 16 on the matrix cores.
+// ttc_lqr_ham16.hpp -- certified Hamiltonian backward for d = du = 16 on the matrix cores.
 //
 // Same recursion, certificate and outputs as lqr_ham_bwd_kernel (the reference's forward
 // Hamiltonian differentiation, ttc/solvers/symplectic_iter.py:764-885, rolled from
@@ -27,7 +27,7 @@
 // the group sums of grad_B / grad_Q (the token's sums when H == 8); otherwise it writes
 // nothing and appends its index to fail_list, and the caller recomputes the whole group
 // with the stable path.
-#include "ttc_lqr_mfma16.cuh"
+#include "ttc_lqr_mfma16.hpp"
 
 #ifndef TTC_HAM16_WAVES
 #define TTC_HAM16_WAVES 4  // waves per SIMD the registers must allow (119 VGPRs, no spills)

@@ -1,5 +1,5 @@
 #pragma once
-// ttc_lqr_hamw.cuh -- certified Hamiltonian backward for d = du = 32 / 64 on the matrix cores.
+// ttc_lqr_hamw.hpp -- certified Hamiltonian backward for d = du = 32 / 64 on the matrix cores.
 //
 // The head-group rollout of lqr_ham16_mfma_kernel (the reference's forward Hamiltonian
 // differentiation, ttc/solvers/symplectic_iter.py:764-885, rolled from lambda_1 = V_1 h_1;
@@ -24,7 +24,7 @@
 // A group whose problems all pass the certificate writes its per-problem gradients and the
 // group sums of grad_B / grad_Q (the token's sums when H == 8); otherwise it writes nothing
 // and appends its index to fail_list, and the caller recomputes the group on the stable path.
-#include "ttc_lqr_ham16.cuh"
+#include "ttc_lqr_ham16.hpp"
 
 namespace ttc {
 

@@ -1,7 +1,7 @@
 // ttc_lqr_internal.h -- per-D kernel launchers shared by the translation units of libttc_lqr.so.
 //
 // Forward launchers take a stash mode `sm` (STASH_NONE / STASH_GAINS / STASH_V1, see
-// ttc_lqr_kernels.cuh) and its two buffers st_a (gains or V_1) and st_b (Quu_0); rescue_ws
+// ttc_lqr_kernels.hpp) and its two buffers st_a (gains or V_1) and st_b (Quu_0); rescue_ws
 // (optional, rescue_ws_bytes(P)) lets the fp64 rescue of a symplectic sweep pack its problems.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -84,7 +84,7 @@ int launch_ham16_mfma(const float* A, const float* B, const float* Q, const floa
                       float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0,
                       float* gBg, float* gQg, float limit, int32_t* fail_list, int32_t* fail_count,
                       int32_t* status, hipStream_t s);
-// the same for d = 32 / 64 (d / 16 waves per head group; ttc_lqr_hamw.cuh)
+// the same for d = 32 / 64 (d / 16 waves per head group; ttc_lqr_hamw.hpp)
 int launch_ham32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                       const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,
                       const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,

@@ -1,5 +1,5 @@
 #pragma once
-// ttc_lqr_kernels.cuh -- row-layout gfx950 kernels of TTC-Net's batched receding-horizon LQR solve.
+// ttc_lqr_kernels.hpp -- row-layout gfx950 kernels of TTC-Net's batched receding-horizon LQR solve.
 //
 // Problem (one per token n and head h, P = N*H problems), restating
 // ttc/solvers/torch_lqr.py:65-91 and ttc/solvers/lin_solver_lqr.py:113-212:

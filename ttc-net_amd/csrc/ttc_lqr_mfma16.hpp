@@ -1,4 +1,4 @@
-// ttc_lqr_mfma16.cuh -- d = du = 16 forward kernel with the per-step products on
+// ttc_lqr_mfma16.hpp -- d = du = 16 forward kernel with the per-step products on
 // the matrix cores (v_mfma_f32_16x16x4f32).
 //
 // One wave holds 4 LQR problems (q = 0..3).  The registers carry the negated value
@@ -37,7 +37,7 @@
 #include <utility>
 
 #include "ttc_lqr_elim16.h"
-#include "ttc_lqr_kernels.cuh"
+#include "ttc_lqr_kernels.hpp"
 
 namespace ttc {
 

@@ -1,4 +1,4 @@
-// ttc_lqr_mfma_blk.cuh -- d = du in {32, 64} forward kernel: the Riccati sweep as 16x16
+// ttc_lqr_mfma_blk.hpp -- d = du in {32, 64} forward kernel: the Riccati sweep as 16x16
 // tiles on the matrix cores (v_mfma_f32_16x16x4f32), with a blocked Cholesky.
 //
 // A wave holds PPW problems; every D x D matrix is NB x NB tiles (NB = D/16), each tile
@@ -33,7 +33,7 @@
 // Quu_0[p][0][0] when u is not written); lqr_rescue_kernel recomputes every marked problem
 // with the row-layout sweep (pivoted Gauss-Jordan at every step).
 #pragma once
-#include "ttc_lqr_mfma16.cuh"
+#include "ttc_lqr_mfma16.hpp"
 
 #ifndef TTC_SYM_WAVES
 #define TTC_SYM_WAVES 3   // waves per SIMD of the symplectic kernel (144 VGPRs, no spills)
