@@ -108,7 +108,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   extern __shared__ __align__(16) float sm[];
   constexpr float kLog2e = 1.4426950408889634f;
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: G, p0, n in SGPRs
   const int g = lane >> 4;        // MFMA row block; problem slot of the row-layout passes
   const int c = lane & 15;        // MFMA column = trajectory; row of the row-layout passes
   const int j = c & 7;            // my column's problem within the group
@@ -117,7 +117,12 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   if (G * 8 >= P) return;         // whole waves only: no barrier follows
   const int64_t p0 = G * 8;
   const int64_t n = p0 / H;       // the group's token
-  const int64_t p = p0 + j;
+  // the group's rows of every per-problem array: uniform bases (scalar registers), so the
+  // per-lane addressing below is 32-bit offsets from them
+  A_diag += p0 * 16; lgB += p0 * 16; lgQ += p0 * 16; Rinv += p0 * 16; lgA += p0;
+  u0g += p0 * 16; h0 += p0 * 16; dU += p0 * 16; q0s += p0 * 256; v1s += p0 * 256; Qf += p0 * 256;
+  gA += p0 * 16; gRinv += p0 * 16; glgB += p0 * 16; glgQ += p0 * 16; gh0 += p0 * 16; glgA += p0; gQf += p0 * 256;
+  const int p = j;                // my column's problem, relative to the group
   float* wbase = sm + wv * Ham16::PER_WAVE;
   float* tile = wbase;                                   // 6 tiles of 16 x LD
   float* prow = wbase + Ham16::OFF_ROW + g * Ham16::ROW_PER;
@@ -157,7 +162,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   float* TL = tile + Ham16::MAT;
 #pragma unroll
   for (int pa = 0; pa < 2; ++pa) {
-    const int64_t pp = p0 + 4 * pa + g;
+    const int pp = 4 * pa + g;
     float aug[20];
     ld_global_row<16>(q0s + (pp * 16 + c) * 16, *reinterpret_cast<float(*)[16]>(aug));
     aug[16] = dU[pp * 16 + c];
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int pa = 0; pa < 2; ++pa) {
     const int jj = 4 * pa + g;
-    const int64_t pp = p0 + jj;
+    const int pp = jj;
     float vrow[16], hv[16], hbv[16];
     ld_global_row<16>(v1s + (pp * 16 + c) * 16, vrow);
     ld_row<16>(TS + jj * Ham16::LD, hv);
@@ -372,7 +377,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int pa = 0; pa < 2; ++pa) {
     const int jj = 4 * pa + g;
-    const int64_t pp = p0 + jj;
+    const int pp = jj;
     float hv[16], hbv[16];
     ld_row<16>(TS + jj * Ham16::LD, hv);
     ld_row<16>(TS + (8 + jj) * Ham16::LD, hbv);
