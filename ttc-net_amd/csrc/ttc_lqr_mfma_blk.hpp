@@ -111,6 +111,9 @@ struct MB {
 // cond_inf(Y1) <= kSymCondMax and max|P - P'| <= kSymAsymMax max|P|; problems that miss it are
 // recomputed by the rescue pass.
 constexpr float kSymCondMax = 1.0e7f;
+// steps between exact (exp2) evaluations of the symplectic sweep's discount factors; the
+// steps in between multiply the previous step's by a constant ratio
+constexpr int kSymRefresh = 8;
 constexpr float kSymAsymMax = 1.0e-6f;
 
 // max over the D lanes of a problem (D = 16, 32, 64)
@@ -125,9 +128,14 @@ __device__ __forceinline__ float dgroup_max(float v) {
   return v;
 }
 
-// |x| as its bit pattern: non-negative floats order like their bits, so a maximum of |x| is
-// an integer maximum (no NaN canonicalisation; a NaN sorts above infinity)
-__device__ __forceinline__ unsigned absbits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+// max(a, b) that returns NaN when either is NaN (v_maximum3_f32 forms, with |x| as a free
+// source modifier in absmax)
+__device__ __forceinline__ float maxnan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float absmax(float a, float b) { return maxnan(fabsf(a), fabsf(b)); }
+// v of the lane whose byte address (4 * lane) is xaddr
+__device__ __forceinline__ float lane_read(float v, int xaddr) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(xaddr, __float_as_int(v)));
+}
 
 // upper tile (I, J), I <= J, in row-major order of the upper triangle
 template <int NB>
@@ -505,17 +513,49 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   //   M = R^{-1} B_k' Y2'      Y1' <- A_k^{-1} (Y1' + B_k M)      Y2' <- A_k Y2' + Qc_k Y1'
   // (beta enters once, squared, in the row scaling of M).  Every TTC_SYM_RENORM steps the columns of
   // Y-hat (rows of Y, which leave Y1^{-1} Y2 unchanged) are rescaled by powers of 2.
+  // step ratios of the sweep's discount factors (t runs down): e_A(t-1) = e_A(t) 2^{-la2},
+  // q(t-1) = q(t) 2^{-lq2}, beta(t-1)^2 = beta(t)^2 2^{-2 lb2}; lane addresses of the
+  // renormalisation's column maximum (lanes c, 16 + c, 32 + c, 48 + c)
+  float rA_l[NPASS], rQ_l[NPASS], rB2_l[NPASS];
+#pragma unroll
+  for (int pa = 0; pa < NPASS; ++pa) {
+    rA_l[pa] = __builtin_amdgcn_exp2f(-la2_o[pa]);
+    rQ_l[pa] = __builtin_amdgcn_exp2f(-lq2_l[pa]);
+    rB2_l[pa] = __builtin_amdgcn_exp2f(-2.0f * lb2_l[pa]);
+  }
+  const int x16 = (lane ^ 16) << 2, x32 = (lane ^ 32) << 2;
+  if constexpr (G::SYM) {
+    // the sweep leaves the per-problem tile regions unused until its final solve
+#pragma unroll
+    for (int pa = 0; pa < NPASS; ++pa) region(qr[pa])[li] = rinv_l[pa];
+    wave_sync();
+  }
   auto sym_step = [&](const int t) {
     if constexpr (G::SYM) {
-    const float tp1 = (float)(t + 1);
+    // the discount factors e_A = 2^{la2 (t+1)}, q = 2^{lq2 t} and -beta^2 R^{-1} (beta =
+    // 2^{lb2 (t+1)}) from the previous step's (slots 2D, D, 3D) times the step ratios,
+    // recomputed exactly every kSymRefresh steps
+    const bool exact = (T - 1 - t) % kSymRefresh == 0;
 #pragma unroll
     for (int pa = 0; pa < NPASS; ++pa) {
       float* v = vecs + qr[pa] * G::VEC;
-      const float alpha = fmaf(a_l[pa], __builtin_amdgcn_exp2f(la2_o[pa] * tp1), 1.0f);
-      const float beta = __builtin_amdgcn_exp2f(lb2_l[pa] * tp1);
+      float eA, q, nb2;
+      if (exact) {
+        const float tp1 = (float)(t + 1);
+        const float beta = __builtin_amdgcn_exp2f(lb2_l[pa] * tp1);
+        eA = __builtin_amdgcn_exp2f(la2_o[pa] * tp1);
+        q = __builtin_amdgcn_exp2f(lq2_l[pa] * (float)t);
+        nb2 = -(beta * beta) * region(qr[pa])[li];  // R_inv, parked in the free tile region
+      } else {
+        eA = v[2 * D + li] * rA_l[pa];
+        q = v[D + li] * rQ_l[pa];
+        nb2 = v[3 * D + li] * rB2_l[pa];
+      }
+      const float alpha = fmaf(a_l[pa], eA, 1.0f);
       v[li] = alpha;
-      v[D + li] = __builtin_amdgcn_exp2f(lq2_l[pa] * (float)t);  // q
-      v[3 * D + li] = -(beta * beta) * rinv_l[pa];
+      v[D + li] = q;
+      v[2 * D + li] = eA;
+      v[3 * D + li] = nb2;
       v[4 * D + li] = __builtin_amdgcn_rcpf(alpha);
     }
     wave_sync();
@@ -550,12 +590,15 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
 #pragma unroll
       for (int s = 0; s < 4; ++s) NV[q][0][0] = mfma16x16x4(op[s], Y1[q][0][0][s], NV[q][0][0]);
       if (renorm) {
-        unsigned mk = 0u;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mk = max(mk, max(absbits(Y1[q][0][0][r]), absbits(NV[q][0][0][r])));
-        mk = max(mk, (unsigned)__shfl_xor((int)mk, 16, 64));
-        mk = max(mk, (unsigned)__shfl_xor((int)mk, 32, 64));
-        const int e = 1 - __builtin_amdgcn_frexp_expf(__uint_as_float(mk));  // m * 2^e in [1, 2)
+        const v4f& y = Y1[q][0][0];
+        const v4f& n = NV[q][0][0];
+        float mk = maxnan(absmax(y[0], n[0]), fabsf(y[1]));
+        mk = maxnan(maxnan(mk, fabsf(n[1])), fabsf(y[2]));
+        mk = maxnan(maxnan(mk, fabsf(n[2])), fabsf(y[3]));
+        mk = maxnan(mk, fabsf(n[3]));
+        mk = maxnan(mk, lane_read(mk, x16));
+        mk = maxnan(mk, lane_read(mk, x32));
+        const int e = 1 - __builtin_amdgcn_frexp_expf(mk);  // m * 2^e in [1, 2)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           Y1[q][0][0][r] = __builtin_amdgcn_ldexpf(Y1[q][0][0][r], e);
@@ -633,14 +676,14 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       if (renorm) {  // per column 16J + c of Y-hat
 #pragma unroll
         for (int J = 0; J < NB; ++J) {
-          unsigned mk = 0u;
+          float mk = 0.f;
 #pragma unroll
           for (int I = 0; I < NB; ++I)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) mk = max(mk, max(absbits(Y1[q][I][J][r]), absbits(NV[q][I][J][r])));
-          mk = max(mk, (unsigned)__shfl_xor((int)mk, 16, 64));
-          mk = max(mk, (unsigned)__shfl_xor((int)mk, 32, 64));
-          const int e = 1 - __builtin_amdgcn_frexp_expf(__uint_as_float(mk));
+            for (int r = 0; r < 4; ++r) mk = maxnan(mk, absmax(Y1[q][I][J][r], NV[q][I][J][r]));
+          mk = maxnan(mk, lane_read(mk, x16));
+          mk = maxnan(mk, lane_read(mk, x32));
+          const int e = 1 - __builtin_amdgcn_frexp_expf(mk);
 #pragma unroll
           for (int I = 0; I < NB; ++I)
 #pragma unroll
