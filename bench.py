@@ -160,6 +160,18 @@ def accuracy_vs_fp64(ins_cpu, d_u_cpu, T, grad_limit):
     return res
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (the `lscpu` "Model name" line), from /proc/cpuinfo."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(ins_cpu, T, H, sample_tokens, d_u_cpu=None, grad_limit=1e6):
     """Reference `riccati` restatement (oracle.ref_torch) on the host, fwd and fwd+bwd, plus the
     accuracy of the reference's fp32 solvers and of the HIP solver against fp64 on the sample."""
@@ -181,7 +193,7 @@ def cpu_baseline(ins_cpu, T, H, sample_tokens, d_u_cpu=None, grad_limit=1e6):
         torch.autograd.grad(u, xs, torch.ones_like(u))
 
     res = {}
-    for name, fn, reps in (("fwd", fwd, 5), ("fwd_bwd", fwdbwd, 3)):
+    for name, fn, reps in (("fwd", fwd, 5), ("fwd_bwd", fwdbwd, 5)):
         fn()
         _note(f"cpu baseline {name}: warm-up done")
         ts = []
@@ -195,8 +207,8 @@ def cpu_baseline(ins_cpu, T, H, sample_tokens, d_u_cpu=None, grad_limit=1e6):
            "fwd_value": res["fwd"],
            "sample": f"{sample_tokens} tokens x {H} heads = {P} problems of the same workload, T={T}; "
                      f"oracle/ref_torch.riccati_solve (reference direct_lqr_solve restated), fwd median of 5, "
-                     f"fwd+bwd (autograd) median of 3, torch threads={torch.get_num_threads()}, "
-                     f"os.cpu_count()={cores}"}
+                     f"fwd+bwd (autograd) median of 5, each after 1 warm-up, torch threads={torch.get_num_threads()}, "
+                     f"os.cpu_count()={cores}, cpu: {_cpu_model()}"}
     if d_u_cpu is not None:
         n_acc = sample_tokens if T < 512 else min(sample_tokens, 16)
         acc = accuracy_vs_fp64([t[:n_acc] for t in sl], d_u_cpu[:n_acc], T, grad_limit)

@@ -12,6 +12,7 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "ttc_lqr.h")
+FLAG_ROW_KERNEL = 2  # TTC_LQR_FLAG_ROW_KERNEL
 
 
 def declared_functions():
@@ -82,12 +83,22 @@ def test_workspace_bytes_monotone_and_stash_smaller(L):
     b = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 0, 0)
     s = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 1, 0)
     assert 0 < a < b and 0 < s < b
-    # per problem: two d^2 gradient partials + list entry, plus (no stash) V_1 and Quu_0
-    assert s >= 4 * 800000 * (2 * 256 + 1)
-    assert b - s >= 4 * 800000 * (2 * 256)
-    # the fallback region is capped (256 MiB + alignment), so large chunks grow linearly
+    P = 800000
+    # without the stash: V_1 and Quu_0 of every problem
+    assert b - s >= 4 * P * (2 * 256)
+    # the fallback region is capped (256 MiB + alignment), so large chunks grow linearly.  Per
+    # problem: the fallback-list entry, and the grad_B / grad_Q partials of the head sums --
+    # none when a head group of 8 is the token (H = 8, it writes the outputs) ...
     c = L.ttc_lqr_workspace_bytes(200000, 8, 16, 16, 64, 1, 0)
-    assert abs((c - s) - 4 * 800000 * (2 * 256 + 1)) < 4096
+    assert abs((c - s) - 4 * P * 1) < 4096
+    # ... one per head group of 8 (H = 16: two per token) ...
+    s16 = L.ttc_lqr_workspace_bytes(50000, 16, 16, 16, 64, 1, 0)
+    c16 = L.ttc_lqr_workspace_bytes(100000, 16, 16, 16, 64, 1, 0)
+    assert abs((c16 - s16) - 4 * P * (1 + 2 * 256 / 8)) < 4096
+    # ... one per problem on the row-layout rollout
+    sr = L.ttc_lqr_workspace_bytes(100000, 8, 16, 16, 64, 1, FLAG_ROW_KERNEL)
+    cr = L.ttc_lqr_workspace_bytes(200000, 8, 16, 16, 64, 1, FLAG_ROW_KERNEL)
+    assert abs((cr - sr) - 4 * P * (1 + 2 * 256)) < 4096
     assert L.ttc_lqr_workspace_bytes(0, 8, 16, 16, 64, 0, 0) == 0
 
 

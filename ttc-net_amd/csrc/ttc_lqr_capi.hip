@@ -293,8 +293,24 @@ struct FastLayout {
   int64_t F;  // fallback capacity within the reserve
 };
 
-static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash, bool fp64) {
+// The fast path rolls head groups of 8 on the matrix cores (fp32, H % 8 == 0), else one
+// problem per row-layout pass (fp32 or, for the long-horizon flags, fp64).
+static bool head_group_path(int H, int flags, bool fp64) {
+  return H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL) && !fp64;
+}
+
+// Its partial grad_B / grad_Q sums per token, added up by the head sum: none when a head group
+// is the whole token (the group writes the outputs), one per head group, one per problem on
+// the row-layout path.
+static int64_t bq_parts_per_token(int H, int flags, bool fp64) {
+  if (head_group_path(H, flags, fp64)) return H == 8 ? 0 : H / 8;
+  return H;
+}
+
+static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash, int flags) {
+  const bool fp64 = fp64_stable(flags, d);
   const size_t Pc = (size_t)chunk_tokens * (size_t)H;
+  const size_t parts = (size_t)chunk_tokens * (size_t)bq_parts_per_token(H, flags, fp64);
   FastLayout L{};
   size_t off = 0;
   L.v1 = off;
@@ -302,9 +318,9 @@ static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T,
   L.q0 = off;
   off += with_stash ? 0 : align256(Pc * (size_t)du * du * sizeof(float));
   L.gBp = off;
-  off += align256(Pc * (size_t)d * du * sizeof(float));
+  off += align256(parts * (size_t)d * du * sizeof(float));
   L.gQp = off;
-  off += align256(Pc * (size_t)d * d * sizeof(float));
+  off += align256(parts * (size_t)d * d * sizeof(float));
   L.list = off;
   off += align256(Pc * sizeof(int32_t));
   L.cnt = off;
@@ -355,11 +371,11 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
   }
   const bool with_stash = v1s != nullptr;
   // largest token chunk whose layout fits the workspace (the layout grows with the chunk)
-  if (workspace_bytes < fast_layout(1, H, d, du, T, with_stash, fp64).total) return TTC_LQR_EINVAL;
+  if (workspace_bytes < fast_layout(1, H, d, du, T, with_stash, flags).total) return TTC_LQR_EINVAL;
   int64_t chunk = 1, hi = n_tokens;
   while (chunk < hi) {
     const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (fast_layout(mid, H, d, du, T, with_stash, fp64).total <= workspace_bytes) chunk = mid;
+    if (fast_layout(mid, H, d, du, T, with_stash, flags).total <= workspace_bytes) chunk = mid;
     else hi = mid - 1;
   }
   const int64_t dd = (int64_t)d * d;
@@ -368,7 +384,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
   for (int64_t n0 = 0; n0 < n_tokens; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H, Pc = nc * H;
-    const FastLayout L = fast_layout(nc, H, d, du, T, with_stash, fp64);
+    const FastLayout L = fast_layout(nc, H, d, du, T, with_stash, flags);
     // rejected problems per fallback pass: whatever the workspace holds beyond the main layout
     int64_t Frun = fallback_capacity(workspace_bytes - L.fb, d, du, T, fp64);
     if (Frun < L.F) Frun = L.F;
@@ -406,7 +422,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     // long horizons in fp64 (fp64 flags): the rollout per problem in fp64 on the row layout, which
     // accepts far more of their problems than the fp32 head-group rollout (a rejected group is
     // recomputed whole by the stable path, each pass of which is a serial T-step sweep)
-    if (H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL) && !fp64) {
+    if (head_group_path(H, flags, fp64)) {
       // head groups of 8 on the matrix cores: grad_B / grad_Q summed inside the kernel
       // (straight into the outputs when a group is a token, H == 8)
       const bool direct = H == 8;
@@ -505,7 +521,8 @@ static void io_counts(int64_t nc, int H, int d, int du, int rb, int rq, size_t (
 // full V_1 and Quu_0 the chunk then holds in v1t / q0t, in the forward before packing and in
 // the backward after unpacking).
 static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                              bool backward, bool bf16, bool compact, bool fp64) {
+                              bool backward, bool bf16, bool compact, int flags) {
+  const bool fp64 = fp64_stable(flags, d);
   const size_t N = (size_t)nc, P = (size_t)nc * (size_t)H, Eb = (size_t)d * du, Eq = (size_t)d * d;
   const size_t nbas = (size_t)rb * Eb + (size_t)rq * Eq;
   FactLayout L{};
@@ -565,7 +582,7 @@ static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, 
     L.inner = off;
     // ttc_lqr_backward's workspace for this chunk in one pass; the stable path (flag
     // TTC_LQR_FLAG_STABLE_BWD) splits the chunk further inside it (one token at least)
-    const size_t fast = fast_layout(nc, H, d, du, T, with_stash, fp64).total;
+    const size_t fast = fast_layout(nc, H, d, du, T, with_stash, flags).total;
     const size_t stab = stable_layout(1, H, d, T, fp64).total;
     off += fast > stab ? fast : stab;
   }
@@ -581,12 +598,12 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Largest token chunk whose factored layout fits ws_bytes (0 when not even one token fits).
 static int64_t fact_chunk(int64_t n_tokens, int H, int d, int du, int rb, int rq, int T, bool with_stash,
-                          bool backward, bool bf16, bool compact, bool fp64, size_t ws_bytes) {
-  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward, bf16, compact, fp64).total > ws_bytes) return 0;
+                          bool backward, bool bf16, bool compact, int flags, size_t ws_bytes) {
+  if (fact_layout(1, H, d, du, rb, rq, T, with_stash, backward, bf16, compact, flags).total > ws_bytes) return 0;
   int64_t chunk = 1, hi = n_tokens;
   while (chunk < hi) {
     const int64_t mid = chunk + (hi - chunk + 1) / 2;
-    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward, bf16, compact, fp64).total <= ws_bytes)
+    if (fact_layout(mid, H, d, du, rb, rq, T, with_stash, backward, bf16, compact, flags).total <= ws_bytes)
       chunk = mid;
     else hi = mid - 1;
   }
@@ -646,12 +663,12 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
   using St = Store<TS>;
   const bool compact = stash != nullptr && (flags & TTC_LQR_FLAG_COMPACT_STASH);
   const bool fp64 = fp64_stable(flags, d);
-  const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, fp64,
+  const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, flags,
                                    ws_bytes);
   if (chunk == 0) return TTC_LQR_EINVAL;
   const int64_t P = n_tokens * H, dd = (int64_t)d * d;
   const size_t nb = (size_t)rb * d * du, nq = (size_t)rq * d * d;
-  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, fp64);
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, flags);
   int rc = TTC_LQR_OK;
   float* bas = reinterpret_cast<float*>(ws + L0.bas);
   const float* Bs = St::in(B_basis, 0, nb, bas, s, rc);
@@ -659,7 +676,7 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
   for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H;
-    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, fp64);
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, flags);
     size_t n[10];
     io_counts(nc, H, d, du, rb, rq, n);
     auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
@@ -710,9 +727,9 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
   const int Eb = d * du, Eq = d * d;
   const size_t nb = (size_t)rb * Eb, nq = (size_t)rq * Eq;
   const int64_t chunk = fact_chunk(n_tokens > 0 ? n_tokens : 1, H, d, du, rb, rq, T, with_stash, true, St::BF16,
-                                   compact, fp64, ws_bytes);
+                                   compact, flags, ws_bytes);
   if (chunk == 0) return TTC_LQR_EINVAL;
-  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact, fp64);
+  const FactLayout L0 = fact_layout(chunk, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact, flags);
   int rc = TTC_LQR_OK;
   float* bas = reinterpret_cast<float*>(ws + L0.bas);
   float* gbas = reinterpret_cast<float*>(ws + L0.gbas);
@@ -732,7 +749,7 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
   for (int64_t n0 = 0; n0 < n_tokens && rc == TTC_LQR_OK; n0 += chunk) {
     const int64_t nc = (n0 + chunk <= n_tokens) ? chunk : (n_tokens - n0);
     const int64_t p0 = n0 * H, Pc = nc * H;
-    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact, fp64);
+    const FactLayout L = fact_layout(nc, H, d, du, rb, rq, T, with_stash, true, St::BF16, compact, flags);
     size_t n[10];
     io_counts(nc, H, d, du, rb, rq, n);
     auto cin = [&](int k) { return reinterpret_cast<float*>(ws + L.cin[k]); };
@@ -897,7 +914,7 @@ size_t ttc_lqr_workspace_bytes(int64_t chunk_tokens, int32_t heads, int32_t d, i
   if (chunk_tokens <= 0 || heads <= 0 || d <= 0 || du != d || T <= 0) return 0;
   if (flags & TTC_LQR_FLAG_STABLE_BWD)
     return stable_layout(chunk_tokens, heads, d, T, fp64_stable(flags, d)).total;
-  return fast_layout(chunk_tokens, heads, d, du, T, with_stash != 0, fp64_stable(flags, d)).total;
+  return fast_layout(chunk_tokens, heads, d, du, T, with_stash != 0, flags).total;
 }
 
 size_t ttc_lqr_fallback_bytes(int64_t problems, int32_t d, int32_t du, int32_t T, int32_t flags) {
@@ -995,7 +1012,7 @@ size_t ttc_lqr_factored_workspace_bytes(int64_t chunk_tokens, int32_t heads, int
                                         int32_t bf16, int32_t flags) {
   if (chunk_tokens <= 0 || !fact_args_ok(chunk_tokens, heads, d, du, b_rank, q_rank, T) || du != d) return 0;
   return fact_layout(chunk_tokens, heads, d, du, b_rank, q_rank, T, with_stash != 0, backward != 0, bf16 != 0,
-                     with_stash == 2, fp64_stable(flags, d))
+                     with_stash == 2, flags)
       .total;
 }
 

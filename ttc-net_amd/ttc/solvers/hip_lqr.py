@@ -228,13 +228,12 @@ class HipLQRSolveFunc(torch.autograd.Function):
             "h0": torch.empty(bs, nh, Dp, device=dev),
         }
         status = torch.zeros(1, device=dev, dtype=torch.int32)
-        budget = _workspace_budget(dev)
         with_st = 1 if st is not None else 0
         # one pass over all tokens when it fits the budget; the library picks the largest
         # token chunk that fits whatever it is given (at least one token's worth)
         full = lib.ttc_lqr_workspace_bytes(bs, nh, Dp, Dp, T, with_st, flags) + _fallback_slack(bs * nh, Dp, T, flags)
-        ws_bytes = max(min(full, budget), lib.ttc_lqr_workspace_bytes(1, nh, Dp, Dp, T, with_st, flags))
-        ws = torch.empty(max(ws_bytes, 256), device=dev, dtype=torch.uint8)
+        ws = torch.empty(_workspace_bytes(full, lib.ttc_lqr_workspace_bytes(1, nh, Dp, Dp, T, with_st, flags), dev),
+                         device=dev, dtype=torch.uint8)
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         n_fb = ctypes.c_int64(0)
         with torch.cuda.device(dev):
@@ -282,6 +281,15 @@ def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_
 
 def _workspace_budget(dev) -> int:
     return _env_bytes("TTC_LQR_WORKSPACE_BYTES", min(16 << 30, max(1 << 30, _stash_budget(dev))))
+
+
+def _workspace_bytes(full: int, floor: int, dev) -> int:
+    """Bytes of a call's workspace: ``full`` (one pass) when the budget allows, else the budget,
+    at least ``floor`` (one token's worth).  The default budget is never below 1 GiB, so a
+    smaller ``full`` skips the device memory query."""
+    if full <= 1 << 30 and not os.environ.get("TTC_LQR_WORKSPACE_BYTES"):
+        return max(full, floor, 256)
+    return max(min(full, _workspace_budget(dev)), floor, 256)
 
 
 class HipLQRFactoredFunc(torch.autograd.Function):
@@ -366,7 +374,7 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         ws_stash = {None: 0, "full": 1, "compact": 2}[kind]
         full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16), flags)
         one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16), flags)
-        ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
+        ws = torch.empty(_workspace_bytes(full, one, dev), device=dev, dtype=torch.uint8)
         fwd = lib.ttc_lqr_forward_factored_bf16 if bf16 else lib.ttc_lqr_forward_factored
         with torch.cuda.device(dev):
             rc = fwd(*[t.data_ptr() for t in xs], bs, nh, Dp, Dp, rb, rq, T, flags, u.data_ptr(),
@@ -417,7 +425,7 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         full = (lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16), flags)
                 + _fallback_slack(bs * nh, Dp, T, flags))
         one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, with_st, 1, int(bf16), flags)
-        ws = torch.empty(max(min(full, _workspace_budget(dev)), one, 256), device=dev, dtype=torch.uint8)
+        ws = torch.empty(_workspace_bytes(full, one, dev), device=dev, dtype=torch.uint8)
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         n_fb = ctypes.c_int64(0)
         bwd = lib.ttc_lqr_backward_factored_bf16 if bf16 else lib.ttc_lqr_backward_factored
