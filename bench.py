@@ -408,11 +408,12 @@ def main():
     traffic = traffic_from_profiles(f"lqr_fwd_cfg{args.config}")
     kern = f"lqr_fwd_blk_kernel<{d}>" + (" (symplectic sweep)" if d in (16, 32, 64) else "")
     # precision="auto" at T >= 512 (d <= 32): the same fp32 matrix-core sweep, the problems its
-    # certificate rejects (a few per cent) recomputed by the fp64 row-layout sweep; priced against
-    # the fp32 matrix peak as a whole
+    # certificate rejects (a few per cent) recomputed in fp64 (d = 16 on the matrix cores, d = 32
+    # by the row-layout sweep); priced against the fp32 matrix peak as a whole
     long_h = T >= 512 and d <= 32
     if long_h:
-        kern += " + fp64 row-layout rescue of the rejected problems (lqr_rescue_listed_kernel<double>)"
+        kern += (" + fp64 matrix-core rescue of the rejected problems (lqr_fwd64_mfma_kernel)" if d == 16 else
+                 " + fp64 row-layout rescue of the rejected problems (lqr_rescue_listed_kernel<double>)")
     out = {
         "metric": metric_for(d, T),
         "value": P / step_s,
@@ -445,7 +446,8 @@ def main():
     }
     if long_h:
         out["roofline"]["peak_note"] = ("fp32 matrix peak of the symplectic sweep; the rescue's fp64 sweeps run on "
-                                        "the vector ALU (78.6 TFLOP/s fp64)")
+                                        + ("the matrix cores" if d == 16 else "the vector ALU")
+                                        + " (78.6 TFLOP/s fp64)")
     extras = []
     for cfg in [x.strip() for x in args.extra_configs.split(",") if x.strip()]:
         if cfg == args.config:

@@ -293,9 +293,11 @@ def test_config5_stress(cfg, T, seed):
 @pytest.mark.parametrize("cfg,n_tok", [(5, 64), ("5b", 64)])
 def test_forward_workspace_packs_the_fp64_rescue(cfg, n_tok):
     """Long horizons (T = 1024, FP64_RESCUE): ttc_lqr_forward_ws lists the problems the
-    symplectic sweep rejects and sweeps them in fp64 four to a wave; ttc_lqr_forward (no
-    workspace) sweeps each marked problem of every group of four in place.  u and the
-    V_1 / Quu_0 stash are bitwise equal, and some problems were rescued."""
+    symplectic sweep rejects and sweeps them in fp64 on the matrix cores (Cholesky steps, the
+    LU row-layout sweep finishing any whose Cholesky breaks down); ttc_lqr_forward (no
+    workspace) sweeps each marked problem with the LU row-layout sweep.  Both rescue some
+    problems (status bit TTC_LQR_STATUS_RESCUED), and u and the V_1 / Quu_0 stash agree to
+    within 1e-5 of their largest magnitude (two fp64 factorisations, rounded to fp32)."""
     from ttc.solvers._lib import FLAG_FP64_RESCUE, lib
     x = make_x(cfg, n_tokens=n_tok, seed=17)
     ins = [t.float().contiguous().cuda() for t in layer_solver_inputs(cfg, x)]
@@ -319,13 +321,15 @@ def test_forward_workspace_packs_the_fp64_rescue(cfg, n_tok):
         assert rc == 0
         torch.cuda.synchronize()
         outs.append((u.cpu(), st.cpu(), int(status.item())))
-        if with_ws:
-            n_listed = int(ws[:4].view(torch.int32).item())
-            print(f"   {n_listed} of {P} problems rescued in fp64", flush=True)
-            assert 0 < n_listed < P
     (u0, s0, f0), (u1, s1, f1) = outs
-    assert torch.isfinite(u0).all()
-    assert torch.equal(u0, u1) and torch.equal(s0, s1) and f0 == f1
+    assert torch.isfinite(u0).all() and torch.isfinite(u1).all()
+    assert f0 == f1 == 4, (f0, f1)  # TTC_LQR_STATUS_RESCUED only
+    du = ((u1 - u0).abs().max() / u0.abs().max()).item()
+    ds = ((s1 - s0).abs().max() / s0.abs().max()).item()
+    changed = int((u1 != u0).any(-1).sum())
+    print(f"   u rel diff {du:.2e}, stash rel diff {ds:.2e}, {changed} of {P} problems not bitwise equal",
+          flush=True)
+    assert du <= 1e-5 and ds <= 1e-5
 
 
 @pytest.mark.parametrize("cfg,n_tok,d_pad", [(4, 1, None), (4, 1, 24)])
@@ -499,6 +503,17 @@ def test_head_group_backward_with_indefinite_Quu0(s, stash):
     indefinite; s = 2 sends the group to the stable path, s = 0.2 stays on the head-group
     kernel."""
     check_case(f"indef-h8-{s}", _indefinite_terminal_inputs(s, H=8), 6, stash=stash)
+
+
+@pytest.mark.parametrize("s", [2.0, 0.2])
+@pytest.mark.parametrize("stable", [True, False])
+def test_long_horizon_indefinite_Quu_finishes_on_lu(s, stable):
+    """T = 512 (FP64_RESCUE): problem 1 has Q_f = -s I, so its Quu turns indefinite.  Through
+    the stable path for every problem, the fp64 matrix-core gain sweep's Cholesky guard fires
+    for it and the LU row-layout sweep finishes it (the other problems keep their Cholesky
+    gains); on the default path the same holds for the forward's fp64 rescue when the
+    symplectic certificate rejects it.  u and every gradient against the fp64 oracle."""
+    check_case(f"indef-T512-{s}", _indefinite_terminal_inputs(s, H=4), 512, grad_limit=math.inf, stable=stable)
 
 
 @pytest.mark.parametrize("T", [64, 256])

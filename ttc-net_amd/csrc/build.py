@@ -16,7 +16,7 @@ OUT_DIR = os.path.normpath(os.path.join(HERE, "..", "lib"))
 SOURCES = ["ttc_lqr_capi.hip", "ttc_lqr_d16.hip", "ttc_lqr_d16_mfma.hip", "ttc_lqr_d32.hip", "ttc_lqr_d64.hip",
            "ttc_lqr_d32_mfma.hip", "ttc_lqr_d64_mfma.hip", "ttc_lqr_d16_sym.hip",
            "ttc_lqr_factored.hip", "ttc_lqr_d16_ham.hip", "ttc_lqr_d32_ham.hip", "ttc_lqr_d64_ham.hip",
-           "ttc_lqr_epilogue.hip", "ttc_lqr_stash.hip", "ttc_lqr_noalloc.hip"]
+           "ttc_lqr_epilogue.hip", "ttc_lqr_stash.hip", "ttc_lqr_noalloc.hip", "ttc_lqr_d16_f64.hip"]
 HOST_SOURCES = ["ttc_lqr_host.cpp"]  # CPU code (no GPU kernels): compiled by the host compiler
 ARCH = os.environ.get("TTC_LQR_ARCH", "gfx950")
 

@@ -7,6 +7,10 @@ int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
                   int32_t* rescue_ws) {
+  // the stable backward's gains at long horizons: fp64 on the matrix cores
+  if (sm == STASH_GAINS && (flags & TTC_LQR_FLAG_FP64_RESCUE) &&
+      !(flags & (TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_FP64_RICCATI)))
+    return launch_gains64_d16(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, st_a, st_b, status, s);
   // fp64 rescue of a symplectic sweep: without a symplectic sweep to certify (the stable
   // backward's gains, row-layout or Riccati-step kernels asked for) the sweep is fp64 throughout
   if ((flags & TTC_LQR_FLAG_FP64_RESCUE) &&

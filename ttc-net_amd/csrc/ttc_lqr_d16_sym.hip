@@ -21,8 +21,12 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
     hipLaunchKernelGGL((lqr_fwd_blk_kernel<16, 4, 1, SM, WU, true>), grid, block, G::LDS_BYTES, s, A, B, Q, R, Qf,
                        lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status);
   if (fp64_rescue) {
-    // long horizons: the rejected problems are the ill-conditioned ones, recomputed by the
-    // pivoted row-layout sweep in fp64
+    // long horizons: the rejected problems are the ill-conditioned ones, recomputed in fp64 --
+    // listed, on the matrix cores (the LU row-layout sweep finishing any whose Cholesky breaks
+    // down); without a list workspace by the row-layout sweep alone
+    if (rescue_ws != nullptr && launch_rescue64_d16(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, SM,
+                                                    status, s, rescue_ws) != TTC_LQR_EUNSUPPORTED)
+      return;
     launch_rescue_k<16, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s,
                                         rescue_ws);
     return;

@@ -21,6 +21,16 @@ int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const flo
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
                        bool fp64_rescue, int32_t* rescue_ws = nullptr);
+// d = 16, fp64 on the matrix cores (ttc_lqr_d16_f64.hip): the rescue of the problems a symplectic
+// sweep marked (sm = STASH_NONE / STASH_V1; rescue_ws of rescue_ws_bytes(P)), and every gain
+// K_t plus Quu_0 of P problems in fp64 (the stable backward).
+int launch_rescue64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
+                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
+                        int32_t* rescue_ws);
+int launch_gains64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                       const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
+                       float* kst, float* q0s, int32_t* status, hipStream_t s);
 int launch_fwd_d32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,

@@ -1,0 +1,417 @@
+// ttc_lqr_mfma64.hpp -- d = du = 16 Riccati sweep in fp64 on the matrix cores
+// (v_mfma_f64_16x16x4f64): the long-horizon rescue of the problems the fp32 symplectic sweep
+// rejects, and the stable backward's per-step gains.
+//
+// A wave holds four problems, each as 16 x 16 fp64 tiles in the C layout of the f64 MFMA
+// (lane 16g + c holds X[g + 4r][c] in element r, checked on the device; a product over K = 16
+// is four instructions, instruction s covering k = g + 4s, so element s of a tile is the B
+// operand of instruction s, and the A operand when the tile holds the transpose).  Per step t
+// and problem, with N = -V_{t+1} (symmetric), B_k = B diag(beta_t), A_t = diag(alpha_t):
+//   -W   = N B_k                              4 MFMA
+//   -Quu = B_k'(-W) - R                        4 MFMA
+//   rows of [-Quu; -I] -> rows of -L^{-T}       16-pivot DPP elimination (Quu = L L'),
+//                                               16-lane group g on problem g, row layout
+//   M'   = (-L^{-1})(-W') = L^{-1} W'           4 MFMA
+//   N    <- A (N + M'' M') A - Qc              4 MFMA, then symmetrised through LDS
+// (V - W Quu^{-1} W' = V - M''M').  The stable backward's gains and step 0's action take
+//   X = Quu^{-1} Qux = L^{-T} M' A              4 MFMA,  K_t = -X,  u_0 = -X_0 h_0.
+// Tiles go between the C layout and the rows of the elimination through per-problem LDS
+// tiles; -W and -L^{-T} are stored with their columns in the order perm4 so that the operand
+// reads are contiguous.
+//
+// The reference's fused solver runs these Riccati steps in fp32 (lin_solver_lqr.py:113-212);
+// this kernel is the fp64 arithmetic of the same recursion for the long horizons where fp32
+// loses the gains.  Every Cholesky pivot of Quu = R + B'VB is at least min_j 1/R_inv_j in
+// exact arithmetic; a pivot below half of that (rounding-limited: on these horizons Quu reaches
+// 1e17 and more; or Quu indefinite) sends the wave's step to the row-layout sweep's pivoted LU
+// solve of [Quu | Qux] (X = Quu^{-1} Qux, N <- A(N A + W X) - Qc), and the next step tries
+// Cholesky again.  (Keeping such rounding-limited positive pivots cost the undiscounted
+// config-5b fixture an order of magnitude in grad_B against the LU solve.)
+#pragma once
+#include "ttc_lqr_mfma16.hpp"
+
+namespace ttc {
+
+typedef double v4d __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4d mfma64(double a, double b, v4d c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// Column order of the permuted tiles: columns g, g + 4, g + 8, g + 12 at 4g .. 4g + 3.
+__host__ __device__ constexpr int perm4(int j) { return (j & 3) * 4 + (j >> 2); }
+
+// Lane K of each 16-lane row to the whole row (two 32-bit DPP row_newbcast moves).
+template <int K>
+__device__ __forceinline__ double bcast16d(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)b, 0x150 + K, 0xF, 0xF, false);
+  const unsigned hi = (unsigned)__builtin_amdgcn_mov_dpp((int)(unsigned)(b >> 32), 0x150 + K, 0xF, 0xF, false);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// One pivot of the fp64 elimination as fused DPP multiply-adds (v_fmac_f64_dpp with
+// row_newbcast, the one DPP control 64-bit operands take): for m > K,
+//   w[m] += q[m]@lane K * nw,   q[m] += q[m]@lane K * nq
+// (the pivot row is read before it is updated).  The s_nop pairs keep the DPP sources two wait
+// states away from the VALU writes around the statement.
+#define TTC_F2(K, M)                                                                  \
+  "v_fmac_f64_dpp %[w" #M "], %[q" #M "], %[nw] row_newbcast:" #K                   \
+  " row_mask:0xf bank_mask:0xf\n\t"                                                   \
+  "v_fmac_f64_dpp %[q" #M "], %[q" #M "], %[nq] row_newbcast:" #K                   \
+  " row_mask:0xf bank_mask:0xf\n\t"
+
+template <int K>
+struct Elim16d;
+
+#define TTC_ELIM16D(K, FIRST)                                                                            \
+  template <>                                                                                            \
+  struct Elim16d<K> {                                                                                    \
+    static __device__ __forceinline__ void qw(double (&q)[16], double (&w)[16], double nq, double nw) {  \
+      asm volatile("s_nop 2\n\t" TTC_R##FIRST(TTC_F2, K) "s_nop 2"                                      \
+                   : TTC_OPS16(q, q), TTC_OPS16(w, w)                                                    \
+                   : [nq] "v"(nq), [nw] "v"(nw));                                                        \
+    }                                                                                                    \
+  };
+
+TTC_ELIM16D(0, 1)
+TTC_ELIM16D(1, 2)
+TTC_ELIM16D(2, 3)
+TTC_ELIM16D(3, 4)
+TTC_ELIM16D(4, 5)
+TTC_ELIM16D(5, 6)
+TTC_ELIM16D(6, 7)
+TTC_ELIM16D(7, 8)
+TTC_ELIM16D(8, 9)
+TTC_ELIM16D(9, 10)
+TTC_ELIM16D(10, 11)
+TTC_ELIM16D(11, 12)
+TTC_ELIM16D(12, 13)
+TTC_ELIM16D(13, 14)
+TTC_ELIM16D(14, 15)
+
+#undef TTC_ELIM16D
+#undef TTC_F2
+
+struct M64 {
+  static constexpr int LDG = 18;               // row stride of a 16 x 16 tile (doubles; 16-byte rows)
+  static constexpr int TILE = 16 * LDG;
+  // per problem: T0 (rows of -Quu, then of -L^{-T} or X), T1 (-W, N's transpose, X_0), T2 (rows
+  // of -Quu for a pivoted redo), and the step's vectors alpha, alpha (perm4 order), q, q (perm4
+  // order), beta, h_0
+  static constexpr int OFF_VEC = 3 * TILE;
+  static constexpr int PER = OFF_VEC + 6 * 16;
+  static constexpr int PPW = 4;
+  static constexpr size_t LDS_BYTES = sizeof(double) * PPW * PER;
+};
+
+// Pivot reciprocal square root in fp64: the hardware estimate (2^-23 relative) and two Newton
+// steps.
+__device__ __forceinline__ double rsqrt64(double d) {
+  double rs = __builtin_amdgcn_rsq(d);
+  rs = rs * fma(-0.5 * d * rs, rs, 1.5);
+  rs = rs * fma(-0.5 * d * rs, rs, 1.5);
+  return rs;
+}
+
+// SM: STASH_NONE (u), STASH_V1 (V_1 and Quu_0 in fp32, u when WRITE_U) or STASH_GAINS (every
+// K_t and Quu_0 in fp64 into kstash / q0stash, no u).  LISTED: the problems are list[64 ..
+// 64 + list[0]) (the rescue list; the grid loops over it, and returns at once unless `status`
+// carries TTC_LQR_STATUS_RESCUED), else 0 .. P-1, four to a wave.
+template <int SM, bool WRITE_U, bool LISTED>
+__global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
+    const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
+    const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
+    const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0, int64_t P,
+    int H, int T, float* __restrict__ u_out, float* __restrict__ kstash, float* __restrict__ q0stash,
+    int* __restrict__ status, const int32_t* __restrict__ list) {
+  constexpr int LDG = M64::LDG;
+  extern __shared__ __align__(16) double sm64[];
+  const int lane = threadIdx.x;
+  const int g = lane >> 4, c = lane & 15;
+  const int pc = perm4(c);
+  int64_t nprob = P;
+  if constexpr (LISTED) {
+    if (status != nullptr && !(__atomic_load_n(status, __ATOMIC_RELAXED) & TTC_LQR_STATUS_RESCUED)) return;
+    nprob = __builtin_amdgcn_readfirstlane(list[0]);
+  }
+  auto T0 = [&](int q) { return sm64 + q * M64::PER; };
+  auto T1 = [&](int q) { return sm64 + q * M64::PER + M64::TILE; };
+  auto T2 = [&](int q) { return sm64 + q * M64::PER + 2 * M64::TILE; };
+  auto VV = [&](int q) { return sm64 + q * M64::PER + M64::OFF_VEC; };
+
+  for (int64_t b0 = (int64_t)blockIdx.x * 4; b0 < nprob; b0 += (int64_t)gridDim.x * 4) {
+    int64_t pq[4];
+    bool vq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      vq[q] = b0 + q < nprob;
+      const int64_t k = vq[q] ? b0 + q : b0;  // idle slots recompute a real problem, never store
+      if constexpr (LISTED) pq[q] = (int64_t)list[64 + k];
+      else pq[q] = k;
+    }
+    const int64_t pg = g == 0 ? pq[0] : (g == 1 ? pq[1] : (g == 2 ? pq[2] : pq[3]));
+    const bool vg = g == 0 ? vq[0] : (g == 1 ? vq[1] : (g == 2 ? vq[2] : vq[3]));
+
+    // row layout: problem g, index c
+    const double a_c = A_diag[pg * 16 + c];
+    const double lgB_c = lgB[pg * 16 + c];
+    const double lgQ_c = lgQ[pg * 16 + c];
+    const double lgA_g = lgA[pg];
+    // pivot floor of the Cholesky steps: half of min_j 1/R_inv_j (the exact-arithmetic floor)
+    float rmin = 1.0f / Rinv[pg * 16 + c];
+    rmin = fminf(rmin, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rmin), 0x128, 0xF, 0xF, false)));
+    rmin = fminf(rmin, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rmin), 0x124, 0xF, 0xF, false)));
+    rmin = fminf(rmin, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rmin), 0x122, 0xF, 0xF, false)));
+    rmin = fminf(rmin, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rmin), 0x121, 0xF, 0xF, false)));
+    const double piv_floor = 0.5 * (double)rmin;
+
+    // C layout, problem q: B of its token (B[g + 4s][c]), -sym(Q), N = -sym(Q_f), -R (diagonal)
+    double Bo[4][4], nR[4];
+    v4d Qo[4], N[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = pq[q] / H;
+      const float* bq = Bg + n * 256;
+      const float* qq = Qg + n * 256;
+      const float* fq = Qf + pq[q] * 256;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) Bo[q][s] = bq[(g + 4 * s) * 16 + c];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = g + 4 * r;
+        Qo[q][r] = -0.5 * ((double)qq[i * 16 + c] + (double)qq[c * 16 + i]);
+        N[q][r] = -0.5 * ((double)fq[i * 16 + c] + (double)fq[c * 16 + i]);
+      }
+      nR[q] = -1.0 / (double)Rinv[pq[q] * 16 + c];
+    }
+
+    for (int t = T - 1; t >= 0; --t) {
+      {
+        const double tp1 = (double)(t + 1);
+        const double eA = exp(lgA_g * tp1);
+        const double al = fma(a_c, eA, 1.0);
+        const double be = exp(lgB_c * tp1);
+        const double qv = (t > 0) ? exp(lgQ_c * (double)t) : 0.0;
+        double* v = VV(g);
+        v[c] = al;
+        v[16 + pc] = al;
+        v[32 + c] = qv;
+        v[48 + pc] = qv;
+        v[64 + c] = be;
+      }
+      if (SM == STASH_V1 && t == 0) {  // V_1 = -N (fp32 rows)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (vq[q])
+#pragma unroll
+            for (int r = 0; r < 4; ++r) kstash[(pq[q] * 16 + g + 4 * r) * 16 + c] = (float)(-N[q][r]);
+      }
+      wave_sync();
+      // -W = N B_k and -Quu = B_k'(-W) - R; rows of -Quu -> T0 and T2, -W -> T1 (columns in perm4
+      // order)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const double be_c = VV(q)[64 + c];
+        double Bk[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) Bk[s] = Bo[q][s] * be_c;
+        v4d nW = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) nW = mfma64(N[q][s], Bk[s], nW);
+        v4d nQ;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) nQ[r] = (g + 4 * r == c) ? nR[q] : 0.0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) nQ = mfma64(Bk[s], nW[s], nQ);
+        double* t0 = T0(q);
+        double* t1 = T1(q);
+        double* t2 = T2(q);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          t0[c * LDG + g + 4 * r] = nQ[r];  // row c of -Quu (= column c of the symmetric tile)
+          t2[c * LDG + g + 4 * r] = nQ[r];
+          t1[(g + 4 * r) * LDG + pc] = nW[r];
+        }
+        if (SM != STASH_NONE && t == 0 && vq[q]) {  // Quu_0
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t e = (pq[q] * 16 + g + 4 * r) * 16 + c;
+            if constexpr (SM == STASH_GAINS) reinterpret_cast<double*>(q0stash)[e] = -nQ[r];
+            else q0stash[e] = (float)(-nQ[r]);
+          }
+        }
+      }
+      wave_sync();
+      // elimination of my group's problem: rows of [-Quu; -I] -> rows of -L^{-T}
+      bool bad = false;
+      {
+        double* t0 = T0(g);
+        double qrow[16], irow[16];
+        ld_row<16>(t0 + c * LDG, qrow);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) irow[k] = (k == c) ? -1.0 : 0.0;
+        static_for<16>([&](auto kc) {
+          constexpr int k = decltype(kc)::value;
+          const double npiv = bcast16d<k>(qrow[k]);  // -d_k
+          bad |= !(-npiv >= piv_floor && -npiv < INFINITY);  // also catches NaN
+          const double rs = rsqrt64(-npiv);
+          const double ip = rs * rs;
+          const double ni = irow[k] * ip;
+          if constexpr (k < 15) {
+            const double nq = qrow[k] * ip;
+            Elim16d<k>::qw(qrow, irow, nq, ni);
+          }
+          irow[k] *= rs;
+        });
+        double prow[16];
+#pragma unroll
+        for (int m = 0; m < 16; ++m) prow[perm4(m)] = irow[m];
+        wave_sync();
+        st_row<16>(t0 + c * LDG, prow);
+      }
+      wave_sync();
+      if (!__any(bad)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const double* t0 = T0(q);
+          double* t1 = T1(q);
+          const double* v = VV(q);
+          // A operand -L^{-1}[c][g + 4s] = (-L^{-T})[g + 4s][c]; B operand -W'[g + 4s][c] = -W[c][g + 4s]
+          double nU[4], nWt[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) nU[s] = t0[(g + 4 * s) * LDG + pc];
+          ld_row<4>(t1 + c * LDG + 4 * g, nWt);
+          v4d Mt = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+          for (int s = 0; s < 4; ++s) Mt = mfma64(nU[s], nWt[s], Mt);  // M' = L^{-1} W'
+          const double al_c = v[c];
+          if (SM == STASH_GAINS || t == 0) {
+            // X = L^{-T} M' A: A operand L^{-T}[c][g + 4s] = -(-L^{-T})[c][g + 4s]
+            double Lt[4];
+            ld_row<4>(t0 + c * LDG + 4 * g, Lt);
+            v4d X = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) X = mfma64(-Lt[s], Mt[s], X);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) X[r] *= al_c;
+            if constexpr (SM == STASH_GAINS) {
+              if (vq[q]) {
+                double* kd = reinterpret_cast<double*>(kstash) + ((int64_t)pq[q] * T + t) * 256;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -X[r];
+              }
+            }
+            if (t == 0) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) t1[(g + 4 * r) * LDG + c] = X[r];
+            }
+          }
+          if (t > 0) {
+            v4d S = N[q];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) S = mfma64(Mt[s], Mt[s], S);  // N + M''M'
+            double alr[4], qr[4];
+            ld_row<4>(v + 16 + 4 * g, alr);  // alpha[g + 4r]
+            ld_row<4>(v + 48 + 4 * g, qr);   // q[g + 4r]
+            const double q_c = v[32 + c];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) N[q][r] = fma(S[r], alr[r] * al_c, (qr[r] * q_c) * Qo[q][r]);
+          }
+        }
+      } else {
+        // A pivot below the floor (rounding-limited, or Quu indefinite): this step again, for
+        // every problem of the wave, by the row-layout sweep's pivoted LU solve of the rows
+        // [Quu | Qux] (Qux = W'A), X = Quu^{-1} Qux, then N <- A (N A + W X) - Qc.
+        {
+          double aug[32];
+          double qrow[16];
+          ld_row<16>(T2(g) + c * LDG, qrow);
+          const double* t1 = T1(g);
+          const double* v = VV(g);
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            aug[k] = -qrow[k];
+            aug[16 + k] = -t1[k * LDG + pc] * v[k];  // W[k][c] alpha_k
+          }
+          double piv;
+          int pos;
+          solve_rows<16, 32>(aug, c, T0(g), piv, pos);
+          const double ip = 1.0 / piv;
+          double xr[16];
+#pragma unroll
+          for (int k = 0; k < 16; ++k) xr[k] = aug[16 + k] * ip;  // row pos of X
+          wave_sync();
+          st_row<16>(T0(g) + pos * LDG, xr);
+        }
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const double* t0 = T0(q);
+          double* t1 = T1(q);
+          const double* v = VV(q);
+          double Xb[4];  // X[g + 4s][c]: the B operand of W X, and X in the C layout
+#pragma unroll
+          for (int s = 0; s < 4; ++s) Xb[s] = t0[(g + 4 * s) * LDG + c];
+          if constexpr (SM == STASH_GAINS) {
+            if (vq[q]) {
+              double* kd = reinterpret_cast<double*>(kstash) + ((int64_t)pq[q] * T + t) * 256;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -Xb[r];
+            }
+          }
+          if (t == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) t1[(g + 4 * r) * LDG + c] = Xb[r];
+          } else {
+            double nWt[4];  // -W[c][g + 4s]: A operand W[c][k] negated
+            ld_row<4>(t1 + c * LDG + 4 * g, nWt);
+            const double al_c = v[c];
+            v4d S;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] = N[q][r] * al_c;  // N A
+#pragma unroll
+            for (int s = 0; s < 4; ++s) S = mfma64(-nWt[s], Xb[s], S);  // + W X
+            double alr[4], qr[4];
+            ld_row<4>(v + 16 + 4 * g, alr);
+            ld_row<4>(v + 48 + 4 * g, qr);
+            const double q_c = v[32 + c];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) N[q][r] = fma(S[r], alr[r], (qr[r] * q_c) * Qo[q][r]);
+          }
+        }
+      }
+      if (t > 0) {  // N = (N + N') / 2 through the T1 tiles
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) T1(q)[c * LDG + g + 4 * r] = N[q][r];
+        wave_sync();
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) N[q][r] = 0.5 * (N[q][r] + T1(q)[(g + 4 * r) * LDG + c]);
+        wave_sync();
+      }
+    }
+
+    // u_0 = -X_0 h_0 for my group's problem (row c)
+    if constexpr (WRITE_U) {
+      VV(g)[80 + c] = (double)h0[pg * 16 + c];
+      wave_sync();
+      double xr[16], hv[16];
+      ld_row<16>(T1(g) + c * LDG, xr);
+      ld_row<16>(VV(g) + 80, hv);
+      double sacc = 0.0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sacc = fma(xr[j], hv[j], sacc);
+      const float u0 = (float)(-sacc);
+      if (vg) u_out[pg * 16 + c] = u0;
+      if (status != nullptr && vg && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
+    }
+    wave_sync();  // the next batch rewrites the tiles
+  }
+}
+
+}  // namespace ttc
