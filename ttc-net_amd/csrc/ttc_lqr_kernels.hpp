@@ -808,8 +808,12 @@ __device__ __forceinline__ double rcpr(double x) { return 1.0 / x; }
 // stable path (stored gains, closed-loop costates).  grad_B / grad_Q partials go to
 // gBp / gQp for headsum_kernel, as in lqr_bwd_kernel.
 // ---------------------------------------------------------------------------
+#ifndef TTC_HAM64_WAVES
+#define TTC_HAM64_WAVES 2  // waves per SIMD of the fp64 rollout (registers capped; its loop keeps them all)
+#endif
 template <int D, typename R = float>
-__global__ __launch_bounds__(Geo<D>::THREADS) void lqr_ham_bwd_kernel(
+__global__ __launch_bounds__(Geo<D>::THREADS)
+__attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WAVES : 1))) void lqr_ham_bwd_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0,
