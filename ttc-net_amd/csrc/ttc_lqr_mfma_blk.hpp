@@ -167,7 +167,12 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   const int c = lane & 15;          // MFMA column; row of the 16x16 elimination
   const int qe = g / G::GPP;        // my problem in the 16x16 elimination
   const int li = lane % D;          // my row (of D) in the row layout
-  const int64_t pbase = ((int64_t)blockIdx.x * G::WPB + wv) * PPW;
+  // XCD-aware block order: the hardware deals consecutive workgroups round-robin to the 8 XCDs,
+  // each with its own L2; give each XCD a contiguous run of problems instead, so that the
+  // workgroups of one token (which read its B and Q) share an L2
+  const unsigned nblk = gridDim.x, bid = blockIdx.x;
+  const unsigned lblk = (nblk % 8u == 0u) ? (bid % 8u) * (nblk / 8u) + bid / 8u : bid;
+  const int64_t pbase = ((int64_t)lblk * G::WPB + wv) * PPW;
 
   int64_t pid[PPW];
 #pragma unroll
