@@ -89,8 +89,9 @@ extern "C" {
 /* TTC_LQR_FLAG_FP64_RESCUE (d <= 32): fp64 where long horizons need it, fp32 matrix cores
  * elsewhere.  The forward runs the fp32 symplectic sweep and recomputes the problems its
  * certificate rejects -- the ill-conditioned ones, whose value matrices grow to ~1e17 -- with
- * the row-layout Riccati sweep in fp64 (instead of the fp32 rescue tiers); the backward's
- * stable path runs in fp64 as under TTC_LQR_FLAG_FP64_RICCATI.  Combined with
+ * a Riccati sweep in fp64 (instead of the fp32 rescue tiers: at d = 16 on the matrix cores,
+ * given the forward workspace, else on the row layout); the backward's stable path runs in
+ * fp64 (at d = 16 its gains on the matrix cores).  Combined with
  * TTC_LQR_FLAG_ROW_KERNEL or TTC_LQR_FLAG_RICCATI_STEPS (no symplectic sweep to certify), or at
  * d = 32 with an odd head count, it acts as TTC_LQR_FLAG_FP64_RICCATI. */
 #define TTC_LQR_FLAG_FP64_RESCUE 32
