@@ -498,10 +498,11 @@ def test_indefinite_Quu_switches_to_pivoted_sweep(s, stash, precision):
 @pytest.mark.parametrize("s", [2.0, 0.2])
 @pytest.mark.parametrize("stash", ["always", "never"])
 def test_head_group_backward_with_indefinite_Quu0(s, stash):
-    """H = 8: the d = 16 head-group Hamiltonian backward (its own pivoted solve of
-    Quu_0 w_0 = -d_u) on a group whose problem 1 has Q_f = -s I, so that its Quu_0 is
-    indefinite; s = 2 sends the group to the stable path, s = 0.2 stays on the head-group
-    kernel."""
+    """H = 8: the d = 16 head-group Hamiltonian backward on a group whose problem 1 has
+    Q_f = -s I, so that its Quu_0 is indefinite; s = 2 sends the group to the stable path,
+    s = 0.2 stays on the head-group kernel, whose solve of Quu_0 w_0 = -d_u (elimination
+    without row exchanges, valid for positive definite Quu_0) then meets a negative pivot
+    and is redone with partial pivoting."""
     check_case(f"indef-h8-{s}", _indefinite_terminal_inputs(s, H=8), 6, stash=stash)
 
 

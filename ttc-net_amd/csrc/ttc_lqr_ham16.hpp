@@ -21,7 +21,9 @@
 // the C layout; primal / adjoint cross terms pair lanes c and c ^ 8 (DPP row_ror:8).
 // The per-problem pieces -- the adjoint feed-forward w_0 = -Quu_0^{-1} d_u, lambda_1 = V_1 h_1
 // and the terminal certificate lambda_T = Q_f h_T -- run in the row layout (16 lanes per
-// problem, two passes of 4 problems).
+// problem, 4 problems per pass; the solve for w_0 eliminates both passes' systems together,
+// by DPP broadcasts, without row exchanges: Quu_0 is positive definite on this path, and a
+// pass where a pivot says otherwise is solved again with partial pivoting).
 //
 // A group whose problems all pass the certificate writes its per-problem gradients and
 // the group sums of grad_B / grad_Q (the token's sums when H == 8); otherwise it writes
@@ -95,6 +97,87 @@ __device__ __forceinline__ v4f mfma_half_cross(const float* X, int g, int c, v4f
   return acc;
 }
 
+// lane K of each 16-lane row to the whole row (DPP row_newbcast:K).  Every lane has a valid
+// source, so bound_ctrl lets the move fold into its consumer as that instruction's DPP operand.
+template <int K>
+__device__ __forceinline__ float rowbcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + K, 0xF, 0xF, true));
+}
+
+// Gauss-Jordan elimination without row exchanges on two systems [M | b] per lane (lane li of
+// a problem's 16 lanes owns row li of each: x[0..15] = row li of M, x[16] = b[li]; likewise y),
+// the pivot row broadcast from lane k (DPP row_newbcast:k) into every update -- one
+// v_fmac_f32_dpp per updated entry, no LDS round trip and no pivot search.  For a symmetric
+// positive definite M the pivots are those of its LDL' factorisation, all positive, and
+// elimination in the natural order is stable; bad is set on the lanes of a system with a
+// pivot that is not positive or not finite (M not positive definite in working precision),
+// whose result must then be discarded.  On return the solution is x[16] / px on lane li
+// (y[16] / py).
+//
+// The updates of pivot k are one asm statement (the compiler does not fold a row_newbcast
+// move into v_fmac_f32): x[m] += bcast_k(x[m]) * nx for m > k, where nx = 0 on lane k keeps
+// the pivot row itself.  Hazard: a DPP source must not be written by a VALU instruction in
+// the two preceding wait states, so the statement starts and ends with s_nop 1.
+#define TTC_GJ_PAIR(K, M)                                                                   \
+  "v_fmac_f32_dpp %[x" #M "], %[x" #M "], %[nx] row_newbcast:" #K                          \
+  " row_mask:0xf bank_mask:0xf\n\t"                                                         \
+  "v_fmac_f32_dpp %[y" #M "], %[y" #M "], %[ny] row_newbcast:" #K                          \
+  " row_mask:0xf bank_mask:0xf\n\t"
+#define TTC_R16(E, K)
+
+template <int K>
+struct GjSpd2;
+
+#define TTC_GJSPD2(K, FIRST)                                                                                \
+  template <>                                                                                               \
+  struct GjSpd2<K> {                                                                                        \
+    static __device__ __forceinline__ void upd(float (&x)[17], float (&y)[17], float nx, float ny) {        \
+      asm volatile("s_nop 1\n\t" TTC_R##FIRST(TTC_GJ_PAIR, K) TTC_GJ_PAIR(K, 16) "s_nop 1"                  \
+                   : TTC_OPS16(x, x), [x16] "+v"(x[16]), TTC_OPS16(y, y), [y16] "+v"(y[16])                  \
+                   : [nx] "v"(nx), [ny] "v"(ny));                                                           \
+    }                                                                                                       \
+  };
+
+TTC_GJSPD2(0, 1)
+TTC_GJSPD2(1, 2)
+TTC_GJSPD2(2, 3)
+TTC_GJSPD2(3, 4)
+TTC_GJSPD2(4, 5)
+TTC_GJSPD2(5, 6)
+TTC_GJSPD2(6, 7)
+TTC_GJSPD2(7, 8)
+TTC_GJSPD2(8, 9)
+TTC_GJSPD2(9, 10)
+TTC_GJSPD2(10, 11)
+TTC_GJSPD2(11, 12)
+TTC_GJSPD2(12, 13)
+TTC_GJSPD2(13, 14)
+TTC_GJSPD2(14, 15)
+TTC_GJSPD2(15, 16)
+
+#undef TTC_GJSPD2
+#undef TTC_R16
+#undef TTC_GJ_PAIR
+
+__device__ __forceinline__ void gj_spd16x2(float (&x)[17], float (&y)[17], int li, float& px, float& py,
+                                           bool& bad) {
+  px = py = 1.f;
+  bad = false;
+  static_for<16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const float dx = rowbcast<k>(x[k]), dy = rowbcast<k>(y[k]);  // the pivots, held by lane k
+    bad |= !(dx > 0.f) || !(dy > 0.f);                            // also catches NaN
+    const bool own = li == k;
+    const float nx = own ? 0.f : -x[k] * __builtin_amdgcn_rcpf(dx);
+    const float ny = own ? 0.f : -y[k] * __builtin_amdgcn_rcpf(dy);
+    if (own) {
+      px = dx;
+      py = dy;
+    }
+    GjSpd2<k>::upd(x, y, nx, ny);
+  });
+}
+
 template <bool DIRECT>
 __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(TTC_HAM16_WAVES))) void lqr_ham16_mfma_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
@@ -157,20 +240,40 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     }
   }
 
-  // ---- t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (row layout, two passes) ----
+  // ---- t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (row layout: lane (g, c) owns row c
+  // of problems g and 4 + g).  Quu_0 = R + B_0' V_1 B_0 is symmetric positive definite for
+  // the problems this path accepts, so both systems are eliminated together without pivoting;
+  // a pass with a problem whose pivots say otherwise is solved again with partial pivoting.
   float* TS = tile;          // trajectory-major exchange tile [traj][state]
   float* TL = tile + Ham16::MAT;
+  {
+    float a[2][17];
 #pragma unroll
-  for (int pa = 0; pa < 2; ++pa) {
-    const int pp = 4 * pa + g;
-    float aug[20];
-    ld_global_row<16>(q0s + (pp * 16 + c) * 16, *reinterpret_cast<float(*)[16]>(aug));
-    aug[16] = dU[pp * 16 + c];
-    aug[17] = aug[18] = aug[19] = 0.f;
-    float piv;
-    int pos;
-    gauss_jordan<16, 20, 0, 17>(aug, c, prow, piv, pos);
-    TS[(8 + 4 * pa + g) * Ham16::LD + pos] = -aug[16] / piv;  // adjoint column of problem 4pa+g
+    for (int pa = 0; pa < 2; ++pa) {
+      const int pp = 4 * pa + g;
+      ld_global_row<16>(q0s + (pp * 16 + c) * 16, *reinterpret_cast<float(*)[16]>(a[pa]));
+      a[pa][16] = dU[pp * 16 + c];
+    }
+    float piv[2];
+    bool bad;
+    gj_spd16x2(a[0], a[1], c, piv[0], piv[1], bad);
+    const bool redo = __any(bad);  // uniform
+#pragma unroll
+    for (int pa = 0; pa < 2; ++pa) {
+      const int pp = 4 * pa + g;
+      if (redo) {
+        float aug[20];
+        ld_global_row<16>(q0s + (pp * 16 + c) * 16, *reinterpret_cast<float(*)[16]>(aug));
+        aug[16] = dU[pp * 16 + c];
+        aug[17] = aug[18] = aug[19] = 0.f;
+        float pv;
+        int pos;
+        gauss_jordan<16, 20, 0, 17>(aug, c, prow, pv, pos);
+        TS[(8 + 4 * pa + g) * Ham16::LD + pos] = -aug[16] / pv;  // adjoint column of problem 4pa+g
+      } else {
+        TS[(8 + 4 * pa + g) * Ham16::LD + c] = -a[pa][16] / piv[pa];
+      }
+    }
   }
   wave_sync();
   v4f U;  // u_0 (primal columns) / w_0 (adjoint columns), rows 4g..4g+3
@@ -221,9 +324,10 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   for (int s = 0; s < 4; ++s) BtL = mfma16x16x4(Bt[s], L[s], BtL);
 
   // per-lane partial accumulators (primal and adjoint lanes are summed at the end)
-  // (grad lgB / grad R_inv: sP, sPt sum the terms of steps t >= 1 below; they start from the
-  // step-0 terms, primal + adjoint lanes, in the same scaling)
-  v4f accA, accLA, accLQ, accH0, sP, sPt;
+  // (grad R_inv / grad lgB: sW sums the terms of steps t >= 1 below -- their plain sum on the
+  // primal lanes, their (t+1)-weighted sum on the adjoint lanes; it starts from the step-0
+  // terms, primal + adjoint lanes, in the same scaling)
+  v4f accA, accLA, accLQ, accH0, sW;
   {
     const v4f Lx = swap8(L), BtLx = swap8(BtL), Ux = swap8(U);
     v4f cLB, cR;
@@ -240,10 +344,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     cLB += swap8(cLB);
     cR += swap8(cR);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      sP[k] = rinv[k] * cR[k];
-      sPt[k] = 0.5f * cLB[k];
-    }
+    for (int k = 0; k < 4; ++k) sW[k] = adj ? 0.5f * cLB[k] : rinv[k] * cR[k];
   }
   // grad_B += Lambda Pi (beta o U)'
   v4f gB = v4f{0.f, 0.f, 0.f, 0.f}, gQ = v4f{0.f, 0.f, 0.f, 0.f};
@@ -263,7 +364,8 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   // rounding),
   //   grad lgB:   (t+1) beta (u B'lambda~ + w B'lambda) = 2 (t+1) W,
   //   grad R_inv: -u w / R_inv^2                          = W / R_inv,
-  // so the loop sums W and (t+1) W (sP, sPt; one lane of each pair suffices).
+  // so the loop sums W (primal lanes) and (t+1) W (adjoint lanes) into sW: one lane of each
+  // pair suffices for either sum.
   // Discounts by recurrence: q_t = exp(lgQ t), e^{lgA (t+1)} and -R_inv beta_t^2 are multiplied
   // by their one-step factors each step and recomputed from the exponential every kRefresh
   // steps, so the rounding of the products spans at most kRefresh - 1 multiplications
@@ -289,10 +391,12 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   float* Y = X + Ham16::MAT;
   v4f gQh = v4f{0.f, 0.f, 0.f, 0.f};  // sum_t X1_p X1_a' (grad_Q = (gQh + gQh') / 2 at the end)
   float tf = 0.0f;
+  const float adjf = adj ? 1.0f : 0.0f;
   for (int t = 1; t < T; ++t) {
     tf += 1.0f;
-    const float tp1 = tf + 1.0f;
+    const float wt = fmaf(adjf, tf, 1.0f);  // weight of W_t in sW: 1 (primal), t + 1 (adjoint)
     if ((t - 1) % kRefresh == 0) {  // uniform branch
+      const float tp1 = tf + 1.0f;
       eA = __builtin_amdgcn_exp2f(la2 * tp1);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -340,7 +444,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     {
       const int cx = c ^ 8;
       const int ix = 4 * (cx & 3) + (cx >> 2);
-      const float tea = tp1 * eA;
+      const float tea = fmaf(tf, eA, eA);  // (t + 1) e^{lgA (t+1)}
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int row = (4 * g + k) * Ham16::LD;
@@ -349,9 +453,7 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
         const float gAt = S[k] * Lx;
         accA[k] = fmaf(gAt, eA, accA[k]);
         accLA[k] = fmaf(gAt, tea, accLA[k]);
-        const float w = BtL[k] * BUx;
-        sP[k] += w;
-        sPt[k] = fmaf(tp1, w, sPt[k]);
+        sW[k] = fmaf(BtL[k] * BUx, wt, sW[k]);
       }
     }
     S = Sn;
@@ -384,16 +486,15 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     const float lam = TL[jj * Ham16::LD + c], lamb = TL[(8 + jj) * Ham16::LD + c];
     const float* qfp = Qf + pp * 256;
     float fh = 0.f, fhb = 0.f;
-    const float hc = TS[jj * Ham16::LD + c], hbc = TS[(8 + jj) * Ham16::LD + c];
+    const float hc2 = 0.5f * TS[jj * Ham16::LD + c], hbc2 = 0.5f * TS[(8 + jj) * Ham16::LD + c];
     float gq[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const float qf2 = qfp[c * 16 + k] + qfp[k * 16 + c];  // 2 sym(Q_f)
       fh = fmaf(qf2, hv[k], fh);
       fhb = fmaf(qf2, hbv[k], fhb);
-      gq[k] = 0.5f * fmaf(hc, hbv[k], hbc * hv[k]);        // grad Q_f row c
-      fin += fabsf(gq[k]);
-      gmax = fmaxf(gmax, fabsf(gq[k]));
+      gq[k] = fmaf(hc2, hbv[k], hbc2 * hv[k]);             // grad Q_f row c
+      gmax = maxnan(gmax, fabsf(gq[k]));                   // NaN if any is
     }
     fh *= 0.5f;
     fhb *= 0.5f;
@@ -409,12 +510,14 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   // finish the per-problem sums: primal + adjoint lanes, then glgA over the 16 rows
 #pragma unroll
   for (int k = 0; k < 4; ++k) gQ[k] *= 0.5f;
+  fin += gmax;  // grad Q_f: its largest magnitude, NaN or infinite with any of its entries
   const v4f fA = accA + swap8(accA);
-  v4f fLB, fR;
+  const v4f sWx = swap8(sW);
+  v4f fLB, fR;  // (meaningful on the primal lanes, which store them)
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    fLB[k] = 2.0f * sPt[k];
-    fR[k] = sP[k] / rinv[k];
+    fLB[k] = 2.0f * sWx[k];
+    fR[k] = sW[k] / rinv[k];
   }
   const v4f fLQ = accLQ + swap8(accLQ), fH0 = accH0 + swap8(accH0);
   float la_sum = accLA[0] * a4[0] + accLA[1] * a4[1] + accLA[2] * a4[2] + accLA[3] * a4[3];

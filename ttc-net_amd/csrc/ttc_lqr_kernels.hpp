@@ -142,9 +142,11 @@ __device__ __forceinline__ void st_global_row(double* __restrict__ g, const doub
 }
 
 // Max of a 32-bit key over the D lanes of a problem (all lanes get the result).
+// bound_ctrl: a source lane the DPP move cannot read gives 0, the identity of the unsigned
+// max, so the move may be folded into the max as its DPP operand (v_max_u32_dpp).
 template <int N>
 __device__ __forceinline__ unsigned ror16(unsigned v) {
-  return __builtin_amdgcn_mov_dpp(v, 0x120 + N, 0xF, 0xF, false);  // row_ror:N
+  return __builtin_amdgcn_mov_dpp(v, 0x120 + N, 0xF, 0xF, true);  // row_ror:N
 }
 template <int D>
 __device__ __forceinline__ unsigned group_max_u32(unsigned k) {
@@ -170,6 +172,11 @@ __device__ __forceinline__ R group_sum(R v, R* scratch, int li) {
   for (int c = 0; c < D; ++c) s += vals[c];
   return s;
 }
+
+// max(a, b) that returns NaN when either is NaN (v_maximum3_f32 forms, with |x| as a free
+// source modifier in absmax)
+__device__ __forceinline__ float maxnan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float absmax(float a, float b) { return maxnan(fabsf(a), fabsf(b)); }
 
 // Monotone 32-bit key of |x| (fp64: its high word, sign cleared).
 __device__ __forceinline__ unsigned mag_key(float x) { return __float_as_uint(fabsf(x)); }

@@ -128,10 +128,6 @@ __device__ __forceinline__ float dgroup_max(float v) {
   return v;
 }
 
-// max(a, b) that returns NaN when either is NaN (v_maximum3_f32 forms, with |x| as a free
-// source modifier in absmax)
-__device__ __forceinline__ float maxnan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
-__device__ __forceinline__ float absmax(float a, float b) { return maxnan(fabsf(a), fabsf(b)); }
 // v of the lane whose byte address (4 * lane) is xaddr
 __device__ __forceinline__ float lane_read(float v, int xaddr) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(xaddr, __float_as_int(v)));
