@@ -91,4 +91,60 @@ TTC_ELIM16(14, 15)
 
 #undef TTC_ELIM16
 
+// Gauss-Jordan elimination without row exchanges in the row layout, one or two systems
+// [M | b] per lane (lane li of a problem's 16 lanes owns row li: x[0..15] = row li of M,
+// x[16] = b[li]; likewise y).  The updates of pivot k are one asm statement (the compiler
+// does not fold a row_newbcast move into v_fmac_f32):  x[m] += bcast_k(x[m]) * nx for
+// m > k, where nx = 0 on lane k keeps the pivot row itself.  Hazard: a DPP source must not
+// be written by a VALU instruction in the two preceding wait states, so each statement
+// starts and ends with s_nop 1.
+#define TTC_GJ_ONE(K, M)                                                                    \
+  "v_fmac_f32_dpp %[x" #M "], %[x" #M "], %[nx] row_newbcast:" #K                          \
+  " row_mask:0xf bank_mask:0xf\n\t"
+#define TTC_GJ_PAIR(K, M)                                                                   \
+  TTC_GJ_ONE(K, M)                                                                          \
+  "v_fmac_f32_dpp %[y" #M "], %[y" #M "], %[ny] row_newbcast:" #K                          \
+  " row_mask:0xf bank_mask:0xf\n\t"
+#define TTC_R16(E, K)
+
+template <int K>
+struct GjSpd;
+
+#define TTC_GJSPD(K, FIRST)                                                                                 \
+  template <>                                                                                               \
+  struct GjSpd<K> {                                                                                         \
+    static __device__ __forceinline__ void upd(float (&x)[17], float nx) {                                  \
+      asm volatile("s_nop 1\n\t" TTC_R##FIRST(TTC_GJ_ONE, K) TTC_GJ_ONE(K, 16) "s_nop 1"                    \
+                   : TTC_OPS16(x, x), [x16] "+v"(x[16])                                                     \
+                   : [nx] "v"(nx));                                                                         \
+    }                                                                                                       \
+    static __device__ __forceinline__ void upd(float (&x)[17], float (&y)[17], float nx, float ny) {        \
+      asm volatile("s_nop 1\n\t" TTC_R##FIRST(TTC_GJ_PAIR, K) TTC_GJ_PAIR(K, 16) "s_nop 1"                  \
+                   : TTC_OPS16(x, x), [x16] "+v"(x[16]), TTC_OPS16(y, y), [y16] "+v"(y[16])                  \
+                   : [nx] "v"(nx), [ny] "v"(ny));                                                           \
+    }                                                                                                       \
+  };
+
+TTC_GJSPD(0, 1)
+TTC_GJSPD(1, 2)
+TTC_GJSPD(2, 3)
+TTC_GJSPD(3, 4)
+TTC_GJSPD(4, 5)
+TTC_GJSPD(5, 6)
+TTC_GJSPD(6, 7)
+TTC_GJSPD(7, 8)
+TTC_GJSPD(8, 9)
+TTC_GJSPD(9, 10)
+TTC_GJSPD(10, 11)
+TTC_GJSPD(11, 12)
+TTC_GJSPD(12, 13)
+TTC_GJSPD(13, 14)
+TTC_GJSPD(14, 15)
+TTC_GJSPD(15, 16)
+
+#undef TTC_GJSPD
+#undef TTC_R16
+#undef TTC_GJ_PAIR
+#undef TTC_GJ_ONE
+
 }  // namespace ttc

@@ -97,87 +97,6 @@ __device__ __forceinline__ v4f mfma_half_cross(const float* X, int g, int c, v4f
   return acc;
 }
 
-// lane K of each 16-lane row to the whole row (DPP row_newbcast:K).  Every lane has a valid
-// source, so bound_ctrl lets the move fold into its consumer as that instruction's DPP operand.
-template <int K>
-__device__ __forceinline__ float rowbcast(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + K, 0xF, 0xF, true));
-}
-
-// Gauss-Jordan elimination without row exchanges on two systems [M | b] per lane (lane li of
-// a problem's 16 lanes owns row li of each: x[0..15] = row li of M, x[16] = b[li]; likewise y),
-// the pivot row broadcast from lane k (DPP row_newbcast:k) into every update -- one
-// v_fmac_f32_dpp per updated entry, no LDS round trip and no pivot search.  For a symmetric
-// positive definite M the pivots are those of its LDL' factorisation, all positive, and
-// elimination in the natural order is stable; bad is set on the lanes of a system with a
-// pivot that is not positive or not finite (M not positive definite in working precision),
-// whose result must then be discarded.  On return the solution is x[16] / px on lane li
-// (y[16] / py).
-//
-// The updates of pivot k are one asm statement (the compiler does not fold a row_newbcast
-// move into v_fmac_f32): x[m] += bcast_k(x[m]) * nx for m > k, where nx = 0 on lane k keeps
-// the pivot row itself.  Hazard: a DPP source must not be written by a VALU instruction in
-// the two preceding wait states, so the statement starts and ends with s_nop 1.
-#define TTC_GJ_PAIR(K, M)                                                                   \
-  "v_fmac_f32_dpp %[x" #M "], %[x" #M "], %[nx] row_newbcast:" #K                          \
-  " row_mask:0xf bank_mask:0xf\n\t"                                                         \
-  "v_fmac_f32_dpp %[y" #M "], %[y" #M "], %[ny] row_newbcast:" #K                          \
-  " row_mask:0xf bank_mask:0xf\n\t"
-#define TTC_R16(E, K)
-
-template <int K>
-struct GjSpd2;
-
-#define TTC_GJSPD2(K, FIRST)                                                                                \
-  template <>                                                                                               \
-  struct GjSpd2<K> {                                                                                        \
-    static __device__ __forceinline__ void upd(float (&x)[17], float (&y)[17], float nx, float ny) {        \
-      asm volatile("s_nop 1\n\t" TTC_R##FIRST(TTC_GJ_PAIR, K) TTC_GJ_PAIR(K, 16) "s_nop 1"                  \
-                   : TTC_OPS16(x, x), [x16] "+v"(x[16]), TTC_OPS16(y, y), [y16] "+v"(y[16])                  \
-                   : [nx] "v"(nx), [ny] "v"(ny));                                                           \
-    }                                                                                                       \
-  };
-
-TTC_GJSPD2(0, 1)
-TTC_GJSPD2(1, 2)
-TTC_GJSPD2(2, 3)
-TTC_GJSPD2(3, 4)
-TTC_GJSPD2(4, 5)
-TTC_GJSPD2(5, 6)
-TTC_GJSPD2(6, 7)
-TTC_GJSPD2(7, 8)
-TTC_GJSPD2(8, 9)
-TTC_GJSPD2(9, 10)
-TTC_GJSPD2(10, 11)
-TTC_GJSPD2(11, 12)
-TTC_GJSPD2(12, 13)
-TTC_GJSPD2(13, 14)
-TTC_GJSPD2(14, 15)
-TTC_GJSPD2(15, 16)
-
-#undef TTC_GJSPD2
-#undef TTC_R16
-#undef TTC_GJ_PAIR
-
-__device__ __forceinline__ void gj_spd16x2(float (&x)[17], float (&y)[17], int li, float& px, float& py,
-                                           bool& bad) {
-  px = py = 1.f;
-  bad = false;
-  static_for<16>([&](auto kc) {
-    constexpr int k = decltype(kc)::value;
-    const float dx = rowbcast<k>(x[k]), dy = rowbcast<k>(y[k]);  // the pivots, held by lane k
-    bad |= !(dx > 0.f) || !(dy > 0.f);                            // also catches NaN
-    const bool own = li == k;
-    const float nx = own ? 0.f : -x[k] * __builtin_amdgcn_rcpf(dx);
-    const float ny = own ? 0.f : -y[k] * __builtin_amdgcn_rcpf(dy);
-    if (own) {
-      px = dx;
-      py = dy;
-    }
-    GjSpd2<k>::upd(x, y, nx, ny);
-  });
-}
-
 template <bool DIRECT>
 __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(TTC_HAM16_WAVES))) void lqr_ham16_mfma_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,

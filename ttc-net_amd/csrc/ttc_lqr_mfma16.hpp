@@ -86,6 +86,55 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+
+// lane K of each 16-lane row to the whole row (DPP row_newbcast:K).  Every lane has a valid
+// source, so bound_ctrl lets the move fold into its consumer as that instruction's DPP operand.
+template <int K>
+__device__ __forceinline__ float rowbcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + K, 0xF, 0xF, true));
+}
+
+// Solve [M | b] (one system per lane: x, or two: x and y) by the row-layout Gauss-Jordan
+// elimination without row exchanges of GjSpd (ttc_lqr_elim16.h), the pivot of step k
+// broadcast from lane k.  For a symmetric positive definite M the pivots are those of its
+// LDL' factorisation, all positive, and elimination in the natural order is stable; `bad`
+// is set on the lanes of a system with a pivot that is not positive or not finite (M not
+// positive definite in working precision), whose result must then be discarded.  On return
+// the solution is x[16] / px on lane li (y[16] / py).
+__device__ __forceinline__ void gj_spd16x1(float (&x)[17], int li, float& px, bool& bad) {
+  px = 1.f;
+  bad = false;
+  static_for<16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const float dx = rowbcast<k>(x[k]);  // the pivot, held by lane k
+    bad |= !(dx > 0.f);                  // also catches NaN
+    const bool own = li == k;
+    const float nx = own ? 0.f : -x[k] * __builtin_amdgcn_rcpf(dx);
+    if (own) px = dx;
+    GjSpd<k>::upd(x, nx);
+  });
+}
+
+__device__ __forceinline__ void gj_spd16x2(float (&x)[17], float (&y)[17], int li, float& px, float& py,
+                                           bool& bad) {
+  px = py = 1.f;
+  bad = false;
+  static_for<16>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const float dx = rowbcast<k>(x[k]), dy = rowbcast<k>(y[k]);  // the pivots, held by lane k
+    bad |= !(dx > 0.f) || !(dy > 0.f);                            // also catches NaN
+    const bool own = li == k;
+    const float nx = own ? 0.f : -x[k] * __builtin_amdgcn_rcpf(dx);
+    const float ny = own ? 0.f : -y[k] * __builtin_amdgcn_rcpf(dy);
+    if (own) {
+      px = dx;
+      py = dy;
+    }
+    GjSpd<k>::upd(x, y, nx, ny);
+  });
+}
+
+
 __device__ __forceinline__ float row16_min(float v) {
   v = fminf(v, ror16f<8>(v));
   v = fminf(v, ror16f<4>(v));

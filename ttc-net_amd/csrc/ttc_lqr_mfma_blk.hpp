@@ -19,8 +19,10 @@
 //   N + M M' = -(V - W Quu^{-1} W'), upper tiles, one operand -> exactly symmetric
 //   N <- diag(a)(N + M M')diag(a) - diag(q) Q diag(q), lower tiles mirrored via LDS.
 // Step 0 forms W and Quu the same way and solves Quu_0 z = W_0' A_0 h0 (u0 = -z) by
-// partially pivoted Gauss-Jordan in the row layout (lane li owns row li); it also writes
-// the compact stash V_1 / Quu_0.
+// Gauss-Jordan in the row layout (lane li owns row li): at d = 16 first without row
+// exchanges, the pivot rows broadcast by DPP (Quu_0 is positive definite for a certified
+// problem), and with partial pivoting through LDS when a pivot is not positive or wider d;
+// it also writes the compact stash V_1 / Quu_0.
 //
 // Multi-wave workgroups (and every d = 64 launch) keep B and -sym(Q) in LDS, shared by the
 // WPB waves of the workgroup: its WPB * PPW problems are consecutive heads of one token
@@ -972,7 +974,23 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       wave_sync();  // all rows read before the pivot-row buffer (aliasing them) is written
       float piv;
       int pos;
-      gauss_jordan<D, D + 4, (D + 4) % 8 == 0 ? 8 : 4, D + 1>(aug, li, region(qr[pa]), piv, pos);
+      bool pivot = true;
+      if constexpr (D == 16) {
+        // Quu_0 is positive definite for a certified problem: elimination without row
+        // exchanges by DPP broadcasts; a pass where a pivot says otherwise is solved again
+        // with partial pivoting
+        float x[17];
+#pragma unroll
+        for (int k = 0; k < 17; ++k) x[k] = aug[k];
+        bool bad;
+        gj_spd16x1(x, li, piv, bad);
+        pivot = __any(bad);  // uniform
+        if (!pivot) {
+          aug[D] = x[16];
+          pos = li;
+        }
+      }
+      if (pivot) gauss_jordan<D, D + 4, (D + 4) % 8 == 0 ? 8 : 4, D + 1>(aug, li, region(qr[pa]), piv, pos);
       const float u0 = -aug[D] / piv;
       if (store) {
         if (WRITE_U) u_out[po0[pa] * D + pos] = u0;
