@@ -92,6 +92,9 @@ def parse():
                          "distribution (batch 1024, 1 head, d 64, T 64): one JSON line per point with fwd+bwd "
                          "time, solves/s, FLOP/s and peak memory; skips the main measurement")
     ap.add_argument("--sweep-dim", type=int, default=64)
+    ap.add_argument("--horizon", type=int, default=0,
+                    help="profiling aid: override the config's horizon T (0 = the config's own); kernel time "
+                         "against T separates the per-step cost from the per-problem work outside the sweep")
     ap.add_argument("--progress", action="store_true", help="print a line to stderr after every solver call")
     ap.add_argument("--copy-calibration", type=float, default=0.0, metavar="GIB",
                     help="profiling aid: run one plain device copy of this many GiB and exit "
@@ -386,6 +389,8 @@ def main():
     if args.sweep:
         sweep(args)
         return
+    if args.horizon > 0:
+        CONFIGS[args.config] = dict(CONFIGS[args.config], T=args.horizon)
 
     c = CONFIGS[args.config]
     dev = torch.device("cuda:0")

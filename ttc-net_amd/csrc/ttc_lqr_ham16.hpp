@@ -40,7 +40,7 @@ namespace ttc {
 struct Ham16 {
   static constexpr int LD = 20;             // row stride of a 16 x 16 tile in LDS (floats)
   static constexpr int MAT = 16 * LD;       // 320 floats
-  static constexpr int NTILE = 5;           // TS, TL, then Z, X, Y of the step
+  static constexpr int NTILE = 5;           // Z, X, Y of the step, then TS, TL
   static constexpr int OFF_ROW = NTILE * MAT;
   static constexpr int ROW_PER = 24;        // per row-layout problem: the pivot row (20) + skew
   static constexpr int PER_WAVE = OFF_ROW + 4 * ROW_PER;
@@ -163,8 +163,8 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   // of problems g and 4 + g).  Quu_0 = R + B_0' V_1 B_0 is symmetric positive definite for
   // the problems this path accepts, so both systems are eliminated together without pivoting;
   // a pass with a problem whose pivots say otherwise is solved again with partial pivoting.
-  float* TS = tile;          // trajectory-major exchange tile [traj][state]
-  float* TL = tile + Ham16::MAT;
+  float* TS = tile + 3 * Ham16::MAT;  // trajectory-major exchange tile [traj][state]
+  float* TL = tile + 4 * Ham16::MAT;
   {
     float a[2][17];
 #pragma unroll
@@ -268,8 +268,8 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   // grad_B += Lambda Pi (beta o U)'
   v4f gB = v4f{0.f, 0.f, 0.f, 0.f}, gQ = v4f{0.f, 0.f, 0.f, 0.f};
   {
-    float* X = tile + 3 * Ham16::MAT;
-    float* Y = tile + 4 * Ham16::MAT;
+    float* X = tile + Ham16::MAT;
+    float* Y = tile + 2 * Ham16::MAT;
     st_tile_rowmajor(X, g, c, L);
     st_tile_rowmajor(Y, g, c, BU);
     wave_sync();
@@ -305,7 +305,9 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
   st4(TS + 4 * lane, accH0);
 
   float eA = 0.f;
-  float* Z = tile + 2 * Ham16::MAT;  // one buffer each: a wave's LDS accesses run in order
+  // Z first: the step's paired row stores into it then reach their 8-bit dword offsets from
+  // the lane's base address without an extra address add
+  float* Z = tile;  // one buffer each: a wave's LDS accesses run in order
   float* X = Z + Ham16::MAT;
   float* Y = X + Ham16::MAT;
   v4f gQh = v4f{0.f, 0.f, 0.f, 0.f};  // sum_t X1_p X1_a' (grad_Q = (gQh + gQh') / 2 at the end)
