@@ -86,8 +86,8 @@ struct MB {
   // the solution)
   static constexpr int REG = (SYMW && 16 * LDX > REG0) ? 16 * LDX : REG0;
   // the final solve of the symplectic sweep works on [Y1 | -Y2 | I] (Y1^{-1} for the condition
-  // number) up to d = 32; at d = 64 on [Y1 | -Y2], with the pivots' spread as the estimate
-  static constexpr bool SYM_INV = D < 64;
+  // number) at d = 32; at d = 16 and 64 on [Y1 | -Y2], with the pivots' spread as the estimate
+  static constexpr bool SYM_INV = D == 32;
   static constexpr int AUGW = SYM_INV ? 3 * D : 2 * D;
   static_assert(REG % 4 == 0 && REG >= 16 * LDG && REG >= D + 4 && (!SYMW || REG >= AUGW + 4) &&
                     (!SYM || SYMW || REG >= 3 * D),
@@ -109,9 +109,10 @@ struct MB {
   static constexpr size_t LDS_BYTES = sizeof(float) * ((size_t)SH + (size_t)WPB * PER_WAVE);
 };
 
-// Certificate of the symplectic sweep (d = 16): the final solve P = Y1^{-1} Y2 is accepted when
-// cond_inf(Y1) <= kSymCondMax and max|P - P'| <= kSymAsymMax max|P|; problems that miss it are
-// recomputed by the rescue pass.
+// Certificate of the symplectic sweep: the final solve P = Y1^{-1} Y2 is accepted when the
+// condition number of Y1 (cond_inf at d = 32; at d = 16 and 64 its estimate ||Y1||_inf / min|u_kk|
+// from the pivots of the same elimination) is <= kSymCondMax and max|P - P'| <= kSymAsymMax max|P|;
+// problems that miss it are recomputed by the rescue pass.
 constexpr float kSymCondMax = 1.0e7f;
 // steps between exact (exp2) evaluations of the symplectic sweep's discount factors; the
 // steps in between multiply the previous step's by a constant ratio
@@ -819,7 +820,7 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     static_assert(NPASS == 1, "d = 16 final solve: one row-layout pass");
     constexpr int L2 = LDX;
     float* buf = region(qr[0]);
-    float aug[3 * D];
+    float aug[2 * D];
 #pragma unroll
     for (int mtx = 0; mtx < 2; ++mtx) {
       wave_sync();  // the previous rows have been read
@@ -828,8 +829,6 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
       wave_sync();
       ld_row<D>(buf + li * L2, *reinterpret_cast<float(*)[D]>(aug + mtx * D));
     }
-#pragma unroll
-    for (int k = 0; k < D; ++k) aug[2 * D + k] = (k == li) ? 1.0f : 0.0f;
     float rs = 0.f;
 #pragma unroll
     for (int k = 0; k < D; ++k) rs += fabsf(aug[k]);
@@ -837,15 +836,15 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
     wave_sync();  // every row read before the pivot-row buffer (aliasing them) is written
     float piv;
     int pos;
-    gauss_jordan<D, 3 * D, 8>(aug, li, buf, piv, pos);
+    gauss_jordan<D, 2 * D, 8>(aug, li, buf, piv, pos);
     const float ip = 1.0f / piv;
-    float ri = 0.f, pn[D];
+    float pn[D];
 #pragma unroll
-    for (int k = 0; k < D; ++k) {
-      ri += fabsf(aug[2 * D + k]);
-      pn[k] = aug[D + k] * ip;
-    }
-    const float n2 = dgroup_max<D>(ri * fabsf(ip));  // ||Y1^{-1}||_inf
+    for (int k = 0; k < D; ++k) pn[k] = aug[D + k] * ip;
+    // the condition number from the pivots, the diagonal of U in Y1 = L U:
+    // ||Y1||_inf / min|u_kk| <= n cond_inf(Y1) (|l_ij| <= 1 under partial pivoting); the
+    // asymmetry test below is the one that separates the inaccurate problems
+    const float n2 = dgroup_max<D>(fabsf(ip));
     st_row<D>(buf + pos * L2, pn);
     wave_sync();
     float da = 0.f, mx = 0.f;
