@@ -149,6 +149,17 @@ def _stash_budget(device) -> int:
     return min(budget, int(float(cap))) if cap else budget
 
 
+def _stash_fits(device, nbytes: int) -> bool:
+    """``nbytes <= _stash_budget(device)``, deciding from the device's free memory alone when
+    half of it suffices (one driver query, a few microseconds): torch's allocator counters,
+    which the full budget reads, cost hundreds of microseconds per call."""
+    cap = os.environ.get("TTC_LQR_STASH_MAX_BYTES")
+    if cap and nbytes > int(float(cap)):
+        return False
+    free, _total = torch.cuda.mem_get_info(device)
+    return nbytes <= free // 2 or nbytes <= _stash_budget(device)
+
+
 def _stream_handle(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -188,7 +199,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
         need_grad = any(ctx.needs_input_grad[:9])
         stash_bytes = lib.ttc_lqr_stash_bytes(bs, nh, Dp, Dp, T)
         keep = (need_grad and bs > 0 and not stable_backward
-                and (policy == "always" or (policy == "auto" and stash_bytes <= _stash_budget(dev))))
+                and (policy == "always" or (policy == "auto" and _stash_fits(dev, stash_bytes))))
         st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32) if keep else None
         # the fp64 rescue's problem list (4 bytes a problem; long horizons only)
         fws_bytes = lib.ttc_lqr_forward_workspace_bytes(bs, nh, Dp, Dp, T, flags)
@@ -362,10 +373,9 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         compact_bytes = lib.ttc_lqr_compact_stash_bytes(bs, nh, Dp, Dp)
         kind = None  # full / compact stash, or none (the backward re-runs the forward sweep)
         if need_grad and bs > 0 and not stable_backward and policy != "never":
-            budget = _stash_budget(dev) if policy == "auto" else None
-            if policy == "always" or (policy == "auto" and stash_bytes <= budget):
+            if policy == "always" or (policy == "auto" and _stash_fits(dev, stash_bytes)):
                 kind = "full"
-            elif policy == "compact" or compact_bytes <= budget:
+            elif policy == "compact" or _stash_fits(dev, compact_bytes):
                 kind = "compact"
         if kind == "compact":
             flags |= FLAG_COMPACT_STASH
