@@ -709,8 +709,8 @@ lqr_fwd_blk_kernel(const float* __restrict__ A_diag, const float* __restrict__ B
   };
 
   // End of the symplectic sweep: -V_1 = Y1^{-1} (-Y2) by pivoted Gauss-Jordan on the rows
-  // [Y1 | -Y2 | I] (lane li owns row li of problem qr), the certificate, and N = sym(-V_1) in
-  // the C layout.  Returns the accepted problems as bits.
+  // [Y1 | -Y2] ([Y1 | -Y2 | I] at d = 32, for Y1^{-1}; lane li owns row li of problem qr), the
+  // certificate, and N = sym(-V_1) in the C layout.  Returns the accepted problems as bits.
   auto sym_finish = [&]() -> unsigned {
     if constexpr (!G::SYM) {
       return ~0u;
