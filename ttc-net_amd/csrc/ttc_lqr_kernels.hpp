@@ -634,20 +634,31 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     wave_sync();
   }
 
-  // phase 1: rollouts, t = 0..T-1
+  // phase 1: rollouts, t = 0..T-1.  At d = 16 each step's gain row is loaded one step ahead
+  // (in fp64 a wave runs alone on its SIMD, so nothing else hides the load's latency); at
+  // d = 32 / 64 the extra registers would spill.
+  constexpr bool PF = D == 16;
   R h_i = h0[p * D + li];
   R hb_i = R(0);
+  R knext[PF ? D : 1];
+  if constexpr (PF) ld_global_row<D>(kst + ((int64_t)p * T * D + li) * D, knext);
   for (int t = 0; t < T; ++t) {
     const R tp1 = (R)(t + 1);
     const R alpha_i = fma(a_i, exp(lgA_p * tp1), R(1));
     const R beta_i = exp(lgB_i * tp1);
+    R krow[D];
+    if constexpr (PF) {
+#pragma unroll
+      for (int c = 0; c < D; ++c) krow[c] = knext[c];
+      if (t + 1 < T) ld_global_row<D>(kst + (((int64_t)p * T + t + 1) * D + li) * D, knext);
+    }
     v0[li] = h_i;
     v1[li] = hb_i;
     wave_sync();
-    R hv[D], hbv[D], krow[D];
+    R hv[D], hbv[D];
     ld_row<D>(v0, hv);
     ld_row<D>(v1, hbv);
-    ld_global_row<D>(kst + (((int64_t)p * T + t) * D + li) * D, krow);
+    if constexpr (!PF) ld_global_row<D>(kst + (((int64_t)p * T + t) * D + li) * D, krow);
     R u_i = R(0), w_i = (t == 0) ? w0_i : R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
@@ -701,9 +712,32 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
 #pragma unroll
   for (int c = 0; c < D; ++c) { gBrow[c] = R(0); gQrow[c] = R(0); }
 
+  // at d = 16 the step's trajectory entry and gain column are loaded one step ahead, as in phase 1
+  auto trn = traj[((int64_t)p * T + (T - 1)) * D + li];
+  R kcn[PF ? D : 1];
+  if constexpr (PF) {
+#pragma unroll
+    for (int c = 0; c < D; ++c) kcn[c] = R(0);
+    if (T - 1 >= 1) {
+#pragma unroll
+      for (int c = 0; c < D; ++c) kcn[c] = kst[(((int64_t)p * T + (T - 1)) * D + c) * D + li];  // K_{T-1}[c, li]
+    }
+  }
   for (int t = T - 1; t >= 0; --t) {
-    const auto tr = traj[((int64_t)p * T + t) * D + li];
+    const auto tr = PF ? trn : traj[((int64_t)p * T + t) * D + li];
     const R h_t = tr.x, hb_t = tr.y, u_i = tr.z, w_i = tr.w;
+    R kcol[D];
+    if constexpr (PF) {
+#pragma unroll
+      for (int c = 0; c < D; ++c) kcol[c] = kcn[c];
+      if (t >= 1) {  // uniform
+        trn = traj[((int64_t)p * T + (t - 1)) * D + li];
+        if (t - 1 >= 1) {
+#pragma unroll
+          for (int c = 0; c < D; ++c) kcn[c] = kst[(((int64_t)p * T + (t - 1)) * D + c) * D + li];
+        }
+      }
+    }
     const R tp1 = (R)(t + 1);
     const R eA = exp(lgA_p * tp1);
     const R alpha_i = fma(a_i, eA, R(1));
@@ -747,14 +781,13 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
       ld_row<D>(v6, cu);
       ld_row<D>(v7, cw);
       R Qh = R(0), Qhb = R(0), kcu = R(0), kcw = R(0);
-      const R* kp = kst + (((int64_t)p * T + t) * D) * D + li;
 #pragma unroll
       for (int c = 0; c < D; ++c) {
         Qh = fma(Qrow[c], qh[c], Qh);
         Qhb = fma(Qrow[c], qhb[c], Qhb);
         // Q_t = D_t Q D_t:  gradient D_t sym(h hb') D_t  (torch_lqr.py:55)
         gQrow[c] = fma(R(0.5) * q_i, fma(h_t, qhb[c], hb_t * qh[c]), gQrow[c]);
-        const R kji = kp[c * D];  // K_t[c, li]
+        const R kji = PF ? kcol[c] : kst[(((int64_t)p * T + t) * D + c) * D + li];  // K_t[c, li]
         kcu = fma(kji, cu[c], kcu);
         kcw = fma(kji, cw[c], kcw);
       }
