@@ -395,7 +395,7 @@ def _A0_zero_inputs(H, d=16, seed=3):
                                                   (16, 8, "fp32", True), (16, 2, "fp32", False),
                                                   (32, 8, "fp32", False), (64, 8, "fp32", False)])
 def test_A0_zero(d, H, precision, stable):
-    """A_0 = 0 (SURVEY's host-forcible case; the reference's fused kernels divide by A_k):
+    """A_0 = 0 (a_i = -exp(-lgA), which the host can set; the reference's fused kernels divide by A_k):
     symplectic, per-step Riccati, row-layout and fp64 forwards, the head-group backward (whose
     Hamiltonian rollout divides by A_t from t = 1 on, so A_0 = 0 is reachable) and the stable
     path, against the fp64 oracle."""

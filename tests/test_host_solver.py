@@ -117,8 +117,8 @@ def test_stress_inputs(T):
 
 def _A0_zero_inputs(seed=3):
     """a_i = -exp(-lgA) for every state of problem 0, so A_0 = diag(1 + a exp(lgA)) = 0: the
-    state is reset at the first step and only B_0 u_0 drives h_1 (SURVEY's host-forcible case;
-    the reference's fused solver divides by A_k there)."""
+    state is reset at the first step and only B_0 u_0 drives h_1 (a case the host can set; the
+    reference's fused solver divides by A_k there)."""
     ins = [t.clone() for t in bench_solver_inputs(2, 2, 16, seed=seed)]
     A, lgA = ins[0], ins[5]
     A[0, 0] = -torch.exp(-lgA[0, 0])
