@@ -99,3 +99,22 @@ def test_layer_T0_returns_zeros():
     m = TTCLayer(32, 20, 16, 8, 16, 16)
     y = m(torch.randn(2, 3, 32), T=0)
     assert y.shape == (2, 3, 20) and not y.any()
+
+
+def test_bench_traffic_records_and_single_gpu_contract():
+    """bench.py's roofline.traffic comes from the committed rocprofv3 summaries: each forward
+    record parses and lies between the algorithmic bytes of its sample and twice them; and a
+    multi-GPU request exits with status 2 and a message instead of a figure."""
+    import json
+    import subprocess
+    import sys
+    import bench
+    algorithmic = {"lqr_fwd_cfg2": 1668 * 2_097_152}  # bytes per problem x problems of the workload
+    for tag, alg in algorithmic.items():
+        t = bench.traffic_from_profiles(tag)
+        assert t is not None, tag
+        assert alg <= t <= 2 * alg, (tag, t, alg)
+    assert bench.traffic_from_profiles("no_such_kernel") is None
+    res = subprocess.run([sys.executable, bench.__file__, "--gpus", "2"], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 2
+    assert "one GPU" in json.loads(res.stdout.strip().splitlines()[-1])["error"]
