@@ -95,6 +95,15 @@ extern "C" {
  * TTC_LQR_FLAG_ROW_KERNEL or TTC_LQR_FLAG_RICCATI_STEPS (no symplectic sweep to certify), or at
  * d = 32 with an odd head count, it acts as TTC_LQR_FLAG_FP64_RICCATI. */
 #define TTC_LQR_FLAG_FP64_RESCUE 32
+/* TTC_LQR_FLAG_FP64_FALLBACK (d <= 32): fp64 only for the problems a certificate rejects, at
+ * any horizon.  The forward is TTC_LQR_FLAG_FP64_RESCUE's (the fp32 symplectic sweep; the
+ * problems its certificate rejects recomputed by an fp64 Riccati sweep, and TTC_LQR_STATUS_RESCUED
+ * set when there were any).  The backward keeps the fp32 Hamiltonian rollout (head groups on the
+ * matrix cores) and runs its stable path -- the problems the rollout's certificate rejects -- in
+ * fp64.  A caller whose forward did not report TTC_LQR_STATUS_RESCUED may drop the flag for the
+ * backward: the rejected problems of a batch whose sweep certified every problem are accurate on
+ * the fp32 stable path, which is cheaper. */
+#define TTC_LQR_FLAG_FP64_FALLBACK 64
 
 /* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
  * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds
@@ -149,17 +158,19 @@ int ttc_lqr_forward(const float* A_diag, const float* B, const float* Q, const f
                     int32_t d, int32_t du, int32_t T, int32_t flags, float* u, float* stash,
                     int32_t* status, void* stream);
 
-/* Bytes of the forward's optional workspace: 4 * (P + 64) with TTC_LQR_FLAG_FP64_RESCUE
- * (d <= 32), where it holds the list of problems the fp64 rescue recomputes; 0 otherwise.
+/* Bytes of the forward's optional workspace: 4 * (P + 64) with TTC_LQR_FLAG_FP64_RESCUE or
+ * TTC_LQR_FLAG_FP64_FALLBACK (d <= 32), where it holds the list of problems the fp64 rescue
+ * recomputes (word 0: their count; from word 64: their indices); 0 otherwise.
  * Same forward as fused_lqr_layer_fwd (ttc/solvers/fused_lqr.py:18-146); the reference's
  * solver keeps no such list (its fp32 sweep solves every problem the same way). */
 size_t ttc_lqr_forward_workspace_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du,
                                        int32_t T, int32_t flags);
 
 /* ttc_lqr_forward with a workspace of ttc_lqr_forward_workspace_bytes(): the fp64 rescue of
- * a long-horizon symplectic sweep then lists its problems and runs full sweeps of 64 / d
- * problems per wave (without it, or with a smaller one, each wave sweeps whichever of 64 / d
- * consecutive problems are marked).  Results are identical either way. */
+ * a symplectic sweep then lists its problems and runs full sweeps of 64 / d problems per wave
+ * (without it, or with a smaller one, each wave sweeps whichever of 64 / d consecutive problems
+ * are marked).  Results are identical either way.  The list is complete when the call's stream
+ * has finished (a count of 0 when the certificate accepted every problem). */
 int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, const float* R_inv,
                        const float* Q_f, const float* log_gamma_A, const float* log_gamma_B,
                        const float* log_gamma_Q, const float* h0, int64_t n_tokens, int32_t heads,

@@ -65,7 +65,13 @@ def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 8) == 1 and L.ttc_lqr_supported_flags(32, 32, 8 | 4) == 1
-    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 64) == 0
+    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 128) == 0
+    # TTC_LQR_FLAG_FP64_FALLBACK (64) needs the fp64 kernels: d <= 32
+    assert L.ttc_lqr_supported_flags(16, 16, 64) == 1 and L.ttc_lqr_supported_flags(32, 32, 64) == 1
+    assert L.ttc_lqr_supported_flags(64, 64, 64) == 0
+    # it lists the fp64 rescue's problems in the forward workspace, as TTC_LQR_FLAG_FP64_RESCUE does
+    assert L.ttc_lqr_forward_workspace_bytes(3, 8, 16, 16, 64, 64) == 4 * (3 * 8 + 64)
+    assert L.ttc_lqr_forward_workspace_bytes(3, 8, 16, 16, 64, 0) == 0
     assert _fwd(L, flags=16) == 2          # the compact stash needs the factored entry points
     assert _fwd(L, d=64, du=64, flags=1) == 2
 

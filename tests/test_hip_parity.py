@@ -432,6 +432,29 @@ def test_layer_parameter_gradients_match_oracle():
         assert e <= TOL, name
 
 
+@pytest.mark.parametrize("T", [64, 256])
+def test_layer_default_path_on_config5_scales(T):
+    """TTCLayer(solver_impl="hip") with its defaults (factored solve, fused l2_norm rescale,
+    precision "auto") on 512 config-5 tokens (per-token log-normal scales, 4,096 problems):
+    the output and the gradients of in_proj, out_proj, Bs and Qs against fp64 autograd of the
+    oracle layer around the fp64 oracle solve."""
+    from ttc import TTCLayer
+    from _layer_oracle import oracle_layer_grads
+    torch.manual_seed(5)
+    layer = TTCLayer(32, 32, 16, 8, 16, 16, solver_impl="hip").cuda()
+    x = make_x(5, n_tokens=512, seed=31 + T)
+    dy = torch.randn(512, 32, generator=torch.Generator().manual_seed(T))
+    print(f"[layer cfg5-scales T={T}] x {tuple(x.shape)}", flush=True)
+    y = layer(x.cuda(), T=T)
+    (y * dy.cuda()).sum().backward()
+    ref = oracle_layer_grads(layer, x, dy, T)
+    for name, p in (("in_proj", layer.in_proj.weight), ("out_proj", layer.out_proj.weight), ("Bs", layer.Bs),
+                    ("Qs", layer.Qs)):
+        e = _relerr(p.grad.cpu().numpy(), ref[name])
+        print(f"   layer grad {name}: {e:.1e}", flush=True)
+        assert e <= TOL, name
+
+
 def test_padding_odd_dims_and_ragged_problem_count():
     """d=12, du=8 (padded to 16 inside), N*H = 21 problems (not a multiple of the block)."""
     g = torch.Generator().manual_seed(11)
@@ -533,6 +556,19 @@ def test_symplectic_certificate_on_stress_inputs(T):
     for k in ["u"] + NAMES:
         assert _relerr(sym[k], ref[k]) <= TOL, k
         assert _relerr(sym[k], ric[k]) <= TOL, k
+
+
+@pytest.mark.parametrize("T,seed", [(64, 21), (256, 23)])
+def test_default_precision_on_config5_scales_below_fp64_horizon(T, seed):
+    """The default precision on config-5 token scales at horizons below 512, on samples large
+    enough (512 tokens, 4,096 problems) to hold the ill-conditioned problems that fp32 Riccati
+    values cannot resolve: the symplectic certificate rejects them, the forward recomputes them
+    in fp64 (TTC_LQR_FLAG_FP64_FALLBACK), and the problems the backward's certificate rejects
+    take the fp64 stable path.  u and all nine gradients within 1e-4 of the fp64 oracle (the
+    fp32-only tiers missed it on these samples by up to 8e-3 at T = 64 and 0.2 at T = 256)."""
+    x = make_x(5, n_tokens=512, seed=seed)
+    out = check_case(f"cfg5-scales T={T}", layer_solver_inputs(5, x), T, seed=seed, grad_limit=math.inf)
+    assert out["_fallback"] > 0  # the sample exercises the backward's fallback
 
 
 def test_T1_closed_form():

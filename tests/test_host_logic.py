@@ -25,6 +25,26 @@ def test_padded_dim():
         padded_dim(65, 16)
 
 
+def test_precision_flags():
+    """"auto": fp64 for the certificate's rejected problems at every horizon where the fp64
+    kernels exist (d <= 32) -- the long-horizon flag from T = 512 on, the fallback flag below --
+    and fp32 at d = 64; the fallback flag reaches the backward only after a forward that
+    rescued some problem (TTC_LQR_STATUS_RESCUED = 4)."""
+    from ttc.solvers.hip_lqr import backward_flags, riccati_flags
+    from ttc.solvers._lib import FLAG_FP64_FALLBACK, FLAG_FP64_RESCUE, FLAG_FP64_RICCATI, FLAG_RICCATI_STEPS
+    assert riccati_flags("auto", 64, 16) == FLAG_FP64_FALLBACK
+    assert riccati_flags("auto", 511, 32) == FLAG_FP64_FALLBACK
+    assert riccati_flags("auto", 512, 16) == FLAG_FP64_RESCUE
+    assert riccati_flags("auto", 64, 64) == 0 and riccati_flags("auto", 1024, 64) == 0
+    assert riccati_flags("fp32", 64, 16) == 0 and riccati_flags("fp32", 1024, 16) == 0
+    assert riccati_flags("riccati", 64, 16) == FLAG_RICCATI_STEPS
+    assert riccati_flags("riccati", 1024, 16) == FLAG_FP64_RICCATI
+    assert backward_flags(FLAG_FP64_FALLBACK, 0) == 0
+    assert backward_flags(FLAG_FP64_FALLBACK, 4) == FLAG_FP64_FALLBACK
+    assert backward_flags(FLAG_FP64_FALLBACK | 4, 1) == 4  # stable-backward bit kept
+    assert backward_flags(FLAG_FP64_RESCUE, 0) == FLAG_FP64_RESCUE
+
+
 @pytest.mark.parametrize("d,du", [(12, 8), (5, 9), (16, 10)])
 def test_padding_preserves_solution_and_gradients(d, du):
     from ttc.solvers.hip_lqr import _pad_inputs, padded_dim

@@ -141,9 +141,27 @@ static int launch_headsum(const float* part, int64_t N, int H, int DD, float* ou
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // ---- stable path: gains recomputed (or stashed), closed-loop costates ----------------
-// The stable path runs in fp64 under either fp64 flag (kernels for d <= 32).
+// The stable path runs in fp64 under any fp64 flag (kernels for d <= 32).
 static bool fp64_stable(int flags, int d) {
+  return (flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE | TTC_LQR_FLAG_FP64_FALLBACK)) != 0 &&
+         d <= 32;
+}
+
+// The fast path's Hamiltonian rollout runs in fp64 (row layout) under the long-horizon flags;
+// under TTC_LQR_FLAG_FP64_FALLBACK it stays the fp32 rollout.
+static bool fp64_rollout(int flags, int d) {
   return (flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE)) != 0 && d <= 32;
+}
+
+// Flags of a forward sweep (stash mode sm): TTC_LQR_FLAG_FP64_FALLBACK's forward is
+// TTC_LQR_FLAG_FP64_RESCUE's -- the fp32 symplectic sweep with its rejected problems recomputed in
+// fp64, and the stable path's gains in fp64 -- except at d = 32 with an odd head count, which has
+// no symplectic sweep to certify and keeps the fp32 Riccati-step tiers for u and the stash.
+static int forward_flags(int flags, int d, int H, int sm) {
+  if (!(flags & TTC_LQR_FLAG_FP64_FALLBACK)) return flags;
+  flags &= ~TTC_LQR_FLAG_FP64_FALLBACK;
+  if (sm != kStashGains && d == 32 && H % 2 != 0) return flags;
+  return flags | TTC_LQR_FLAG_FP64_RESCUE;
 }
 
 struct StableLayout {
@@ -173,6 +191,7 @@ static int fwd_d(int d, const float* a, const float* b, const float* q, const fl
                  const float* la, const float* lb, const float* lq, const float* hz, int64_t P, int H, int T, float* u,
                  float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
                  int32_t* rescue_ws = nullptr) {
+  flags = forward_flags(flags, d, H, sm);
   switch (d) {
     case 16:
       return launch_fwd_d16(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags, rescue_ws);
@@ -295,22 +314,22 @@ struct FastLayout {
 
 // The fast path rolls head groups of 8 on the matrix cores (fp32, H % 8 == 0), else one
 // problem per row-layout pass (fp32 or, for the long-horizon flags, fp64).
-static bool head_group_path(int H, int flags, bool fp64) {
-  return H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL) && !fp64;
+static bool head_group_path(int H, int flags, int d) {
+  return H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL) && !fp64_rollout(flags, d);
 }
 
 // Its partial grad_B / grad_Q sums per token, added up by the head sum: none when a head group
 // is the whole token (the group writes the outputs), one per head group, one per problem on
 // the row-layout path.
-static int64_t bq_parts_per_token(int H, int flags, bool fp64) {
-  if (head_group_path(H, flags, fp64)) return H == 8 ? 0 : H / 8;
+static int64_t bq_parts_per_token(int H, int flags, int d) {
+  if (head_group_path(H, flags, d)) return H == 8 ? 0 : H / 8;
   return H;
 }
 
 static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash, int flags) {
   const bool fp64 = fp64_stable(flags, d);
   const size_t Pc = (size_t)chunk_tokens * (size_t)H;
-  const size_t parts = (size_t)chunk_tokens * (size_t)bq_parts_per_token(H, flags, fp64);
+  const size_t parts = (size_t)chunk_tokens * (size_t)bq_parts_per_token(H, flags, d);
   FastLayout L{};
   size_t off = 0;
   L.v1 = off;
@@ -422,7 +441,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     // long horizons in fp64 (fp64 flags): the rollout per problem in fp64 on the row layout, which
     // accepts far more of their problems than the fp32 head-group rollout (a rejected group is
     // recomputed whole by the stable path, each pass of which is a serial T-step sweep)
-    if (head_group_path(H, flags, fp64)) {
+    if (head_group_path(H, flags, d)) {
       // head groups of 8 on the matrix cores: grad_B / grad_Q summed inside the kernel
       // (straight into the outputs when a group is a token, H == 8)
       const bool direct = H == 8;
@@ -462,9 +481,9 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
       continue;
     }
     switch (d) {
-      case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64); break;
-      case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64); break;
-      case 64: rc = launch_ham_d64(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64); break;
+      case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64_rollout(flags, d)); break;
+      case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64_rollout(flags, d)); break;
+      case 64: rc = launch_ham_d64(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt, status, s, fp64_rollout(flags, d)); break;
       default: return TTC_LQR_EUNSUPPORTED;
     }
     if (rc != TTC_LQR_OK) return rc;
@@ -892,9 +911,11 @@ int ttc_lqr_supported(int32_t d, int32_t du) { return (d == du && (d == 16 || d 
 
 int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if (!ttc_lqr_supported(d, du)) return 0;
-  if ((flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE)) && d > 32) return 0;
+  if ((flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE | TTC_LQR_FLAG_FP64_FALLBACK)) && d > 32)
+    return 0;
   const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD |
-                        TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH | TTC_LQR_FLAG_FP64_RESCUE;
+                        TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH | TTC_LQR_FLAG_FP64_RESCUE |
+                        TTC_LQR_FLAG_FP64_FALLBACK;
   return (flags & ~known) ? 0 : 1;
 }
 
@@ -925,7 +946,8 @@ size_t ttc_lqr_fallback_bytes(int64_t problems, int32_t d, int32_t du, int32_t T
 size_t ttc_lqr_forward_workspace_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T,
                                        int32_t flags) {
   if (n_tokens <= 0 || heads <= 0 || d <= 0 || du != d || T <= 0) return 0;
-  if (!(flags & TTC_LQR_FLAG_FP64_RESCUE) || d > 32) return 0;  // only the fp64 rescue uses one
+  // only the fp64 rescue uses one
+  if (!(flags & (TTC_LQR_FLAG_FP64_RESCUE | TTC_LQR_FLAG_FP64_FALLBACK)) || d > 32) return 0;
   return ttc::rescue_ws_bytes(n_tokens * heads);
 }
 
@@ -955,6 +977,11 @@ int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, cons
   const size_t need = ttc_lqr_forward_workspace_bytes(n_tokens, heads, d, du, T, flags);
   int32_t* rws = (workspace != nullptr && need > 0 && workspace_bytes >= need) ? static_cast<int32_t*>(workspace)
                                                                                 : nullptr;
+  // the list's count starts at 0 whichever rescue route runs (the unlisted ones never write it)
+  if (rws != nullptr) {
+    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, rws, 0);
+    if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+  }
   return fwd_d(d, A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, v1, q0,
                stash ? kStashV1 : 0, status, s, flags, rws);
 }

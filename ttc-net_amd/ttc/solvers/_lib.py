@@ -11,7 +11,7 @@ import ctypes
 import os
 
 __all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI", "FLAG_ROW_KERNEL",
-           "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS", "FLAG_COMPACT_STASH", "FLAG_FP64_RESCUE"]
+           "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS", "FLAG_COMPACT_STASH", "FLAG_FP64_RESCUE", "FLAG_FP64_FALLBACK"]
 
 FLAG_FP64_RICCATI = 1  # TTC_LQR_FLAG_FP64_RICCATI
 FLAG_ROW_KERNEL = 2    # TTC_LQR_FLAG_ROW_KERNEL
@@ -19,6 +19,7 @@ FLAG_STABLE_BWD = 4    # TTC_LQR_FLAG_STABLE_BWD
 FLAG_RICCATI_STEPS = 8  # TTC_LQR_FLAG_RICCATI_STEPS
 FLAG_COMPACT_STASH = 16  # TTC_LQR_FLAG_COMPACT_STASH
 FLAG_FP64_RESCUE = 32  # TTC_LQR_FLAG_FP64_RESCUE
+FLAG_FP64_FALLBACK = 64  # TTC_LQR_FLAG_FP64_FALLBACK
 
 LIB_NAME = "libttc_lqr.so"
 _HERE = os.path.dirname(os.path.abspath(__file__))

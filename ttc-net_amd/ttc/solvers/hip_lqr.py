@@ -55,7 +55,7 @@ import os
 import torch
 
 from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS, \
-    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE
+    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
            "SUPPORTED_DIMS", "last_backward_stats"]
@@ -65,6 +65,7 @@ FP64_HORIZON = 512
 _FWD_MSG = "Numerical instability detected during fused LQR forward recurrence."
 _BWD_MSG = "Numerical instability detected during fused LQR backward pass."
 _ERROR_BITS = 1 | 2  # TTC_LQR_STATUS_NONFINITE | TTC_LQR_STATUS_LARGE (4 = RESCUED is informational)
+_RESCUED = 4  # TTC_LQR_STATUS_RESCUED
 _RESCALE_MODES = {"none": 0, "l2_norm": 1, "h0_norm": 2}  # TTC_LQR_RESCALE_*
 
 # problems / fallback problems of the most recent backward call (observability)
@@ -110,7 +111,10 @@ def riccati_flags(precision: str, T: int, Dp: int) -> int:
     ``"fp32-riccati"``: per-step Riccati on the matrix cores; ``"fp32-row"``: the
     row-layout fp32 kernels (vector ALU only, forward and the backward's rollout) -- an
     independent cross-check of the matrix-core kernels; ``"fp64"``:
-    fp64 sweep; ``"auto"``: fp64 for T >= FP64_HORIZON where available, else fp32.
+    fp64 sweep; ``"auto"`` (state dims up to 32): for T >= FP64_HORIZON the fp64 rescue of the
+    sweep's rejected problems and the fp64 backward (``TTC_LQR_FLAG_FP64_RESCUE``); below it the
+    fp64 rescue with the fp32 matrix-core backward, whose rejected problems take the fp64
+    stable path (``TTC_LQR_FLAG_FP64_FALLBACK``); d = 64 stays fp32.
     """
     assert precision in ("fp32", "fp32-riccati", "fp32-row", "fp64", "auto", "riccati"), \
         f"unknown precision {precision}"
@@ -127,7 +131,19 @@ def riccati_flags(precision: str, T: int, Dp: int) -> int:
         return FLAG_FP64_RICCATI
     if precision == "auto" and long_fp64:
         return FLAG_FP64_RESCUE
+    if precision == "auto" and lib.ttc_lqr_supported_flags(Dp, Dp, FLAG_FP64_FALLBACK):
+        return FLAG_FP64_FALLBACK
     return 0
+
+
+def backward_flags(flags: int, forward_status: int) -> int:
+    """Flags of the backward after a forward that reported ``forward_status``: under
+    ``TTC_LQR_FLAG_FP64_FALLBACK`` the stable path runs in fp64 only when the forward's certificate
+    rejected some problem of the batch (``TTC_LQR_STATUS_RESCUED``); a batch it certified whole
+    has no problem that needs fp64, and the fp32 stable path is cheaper."""
+    if flags & FLAG_FP64_FALLBACK and not forward_status & _RESCUED:
+        return flags & ~FLAG_FP64_FALLBACK
+    return flags
 
 
 def _fallback_slack(P: int, Dp: int, T: int, flags: int) -> int:
@@ -210,12 +226,13 @@ class HipLQRSolveFunc(torch.autograd.Function):
                                         None if fws is None else fws.data_ptr(), fws_bytes, status.data_ptr(),
                                         _stream_handle(dev))
         check(rc, "ttc_lqr_forward_ws")
-        if int(status.item()) & _ERROR_BITS:
+        fst = int(status.item())
+        if fst & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
             ctx.save_for_backward(*f32, u, *([st] if st is not None else []))
         ctx.meta = (bs, nh, d, du, Dp, T, float(grad_limit), st is not None, [x.dtype for x in ins],
-                    flags | (FLAG_STABLE_BWD if stable_backward else 0))
+                    backward_flags(flags, fst) | (FLAG_STABLE_BWD if stable_backward else 0))
         return u[..., :du].to(out_dtype)
 
     @staticmethod
@@ -399,12 +416,13 @@ class HipLQRFactoredFunc(torch.autograd.Function):
                 rc = lib.ttc_lqr_rescale(u.data_ptr(), xs[8].data_ptr(), bs, nh, Dp, Dp, mode, y.data_ptr(),
                                          _stream_handle(dev))
             check(rc, "ttc_lqr_rescale")
-        if int(status.item()) & _ERROR_BITS:
+        fst = int(status.item())
+        if fst & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
             ctx.save_for_backward(*xs, u, *([st] if st is not None else []))
         ctx.meta = (bs, nh, d, du, Dp, rb, rq, T, float(grad_limit), st is not None, [x.dtype for x in ins],
-                    flags | (FLAG_STABLE_BWD if stable_backward else 0), bf16, mode)
+                    backward_flags(flags, fst) | (FLAG_STABLE_BWD if stable_backward else 0), bf16, mode)
         return y[..., :du].to(out_dtype)
 
     @staticmethod
