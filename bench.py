@@ -71,13 +71,23 @@ def parse():
     ap.add_argument("--config", default="2", choices=list(CONFIGS))
     ap.add_argument("--tokens", type=int, default=0, help="override token count (0 = the config's full x)")
     ap.add_argument("--stash", default=None, choices=["auto", "always", "never"])
-    ap.add_argument("--cpu-sample-tokens", type=int, default=64, help="tokens of the CPU baseline sample")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=0,
+                    help="tokens of the CPU baseline sample (0: 64 below T = 512, 1 from there; the reference "
+                         "restatement's autograd through 1,024 steps takes seconds per token)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-leg", default=None, metavar="NPZ", help=argparse.SUPPRESS)
+    ap.add_argument("--precision", default="auto",
+                    choices=["auto", "riccati", "fp32", "fp32-riccati", "fp32-row", "fp64"],
+                    help="the solver's precision / kernel choice (hip_lqr_solve's `precision`): 'riccati' times what "
+                         "TTCLayer(solver_impl='riccati') runs on CUDA tensors, with --stable-backward what 'kkt' runs")
+    ap.add_argument("--stable-backward", action="store_true",
+                    help="the stable backward for every problem (the 'kkt' key's backward)")
     ap.add_argument("--fwd-only", action="store_true",
                     help="profiling aid: time only the forward solve (the JSON value is then fwd solves/s)")
-    ap.add_argument("--extra-configs", default="3,4",
-                    help="comma list of further configs measured on a token sample after the main one "
-                         "(forward and fwd+bwd, reported under 'extra_configs'); '' for none")
+    ap.add_argument("--extra-configs", default="3,4,5,5b",
+                    help="comma list of further configs measured after the main one (forward and fwd+bwd, "
+                         "reported under 'extra_configs'): 3 and 4 on a token sample, 5 and 5b at full size; "
+                         "'' for none")
     ap.add_argument("--extra-tokens", type=int, default=8192, help="token sample of the extra configs")
     ap.add_argument("--no-factored-extra", action="store_true",
                     help="skip the factored-input measurement of the main config (profiling aid)")
@@ -125,44 +135,6 @@ def _relerr(x, ref):
 NAMES = ["A_diag", "B", "Q", "R_inv", "Q_f", "lgA", "lgB", "lgQ", "h0"]
 
 
-def accuracy_vs_fp64(ins_cpu, d_u_cpu, T, grad_limit):
-    """u and the nine gradients of (a) the reference's `riccati` and `kkt` solvers restated op for op
-    in fp32 on the host (oracle/ref_torch.py) and (b) this build's HIP solver, each against the fp64
-    oracle (oracle/lqr64.py) on the same inputs and the same upstream gradient: per tensor
-    max|x - x64| / max|x64| (Q / Q_f: symmetric gradients), None where an output is non-finite."""
-    import numpy as np
-    import torch
-    from oracle.lqr64 import LQRProblem, solve_grads
-    from oracle.ref_torch import kkt_solve, riccati_solve
-    from ttc.solvers.hip_lqr import hip_lqr_solve
-    ref = solve_grads(LQRProblem(*ins_cpu, T), d_u_cpu.double().numpy())
-    _note("accuracy: fp64 oracle done")
-
-    def run(fn, dev):
-        xs = [t.detach().clone().to(dev).float().requires_grad_(True) for t in ins_cpu]
-        u = fn(*xs, T)
-        gs = torch.autograd.grad(u, xs, d_u_cpu.to(dev).to(u.dtype), allow_unused=True)
-        out = {"u": u.detach().cpu().double().numpy()}
-        for n, g in zip(NAMES, gs):
-            g = g.detach().cpu().double().numpy()
-            out[n] = 0.5 * (g + np.swapaxes(g, -1, -2)) if n in ("Q", "Q_f") else g
-        return out
-
-    res = {}
-    for name, fn, dev in (("reference_riccati_fp32", riccati_solve, "cpu"), ("reference_kkt_fp32", kkt_solve, "cpu"),
-                          ("hip", lambda *a: hip_lqr_solve(*a, grad_limit=grad_limit), "cuda")):
-        try:
-            with np.errstate(all="ignore"):
-                out = run(fn, dev)
-            per = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
-        except RuntimeError as e:  # e.g. a guard of the solver
-            per = {"error": str(e)}
-        _note(f"accuracy: {name} done")
-        vals = [v for k, v in per.items() if k != "error"]
-        res[name] = {"max": (None if (not vals or any(v is None for v in vals)) else max(vals)), "per_output": per}
-    return res
-
-
 def _cpu_model() -> str:
     """The host CPU's model name (the `lscpu` "Model name" line), from /proc/cpuinfo."""
     try:
@@ -175,28 +147,62 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(ins_cpu, T, H, sample_tokens, d_u_cpu=None, grad_limit=1e6):
-    """Reference `riccati` restatement (oracle.ref_torch) on the host, fwd and fwd+bwd, plus the
-    accuracy of the reference's fp32 solvers and of the HIP solver against fp64 on the sample."""
+def _oracle_cfg(cfg: str):
+    return int(cfg) if cfg.isdigit() else cfg
+
+
+def _sample_tokens(args, T: int) -> int:
+    return args.cpu_sample_tokens if args.cpu_sample_tokens > 0 else (64 if T < 512 else 1)
+
+
+def _per_output_errors(out, ref):
+    return {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
+
+
+def _max_or_none(per):
+    vals = [v for k, v in per.items() if k != "error"]
+    return None if (not vals or any(v is None for v in vals)) else max(vals)
+
+
+def cpu_leg(args):
+    """`--cpu-leg NPZ`: the CPU half of the baseline, in a process of its own that bench.py starts
+    before it touches the GPU; this process never does (no HIP library, no torch.cuda).
+
+    On a seeded sample of the configuration's workload (oracle/inputs.py: the layer front-end on
+    synthetic x, the same distribution as the GPU run): times the op-for-op restatement of the
+    reference `riccati` solver (oracle/ref_torch.py; forward, and forward + autograd backward) on
+    all host cores, and measures the reference's fp32 `riccati` and `kkt` solvers against the fp64
+    oracle (oracle/lqr64.py) on the same sample and upstream gradient.  Writes the sample, the
+    gradient and the oracle's outputs to NPZ (the benchmark process measures the HIP solver on
+    them) and prints one JSON line."""
+    import numpy as np
     import torch
-    from oracle.ref_torch import riccati_solve
+    from oracle.inputs import layer_solver_inputs, make_x
+    from oracle.lqr64 import LQRProblem, solve_grads
+    from oracle.ref_torch import kkt_solve, riccati_solve
+    c = CONFIGS[args.config]
+    T = args.horizon if args.horizon > 0 else c["T"]
+    n = _sample_tokens(args, T)
+    ocfg = _oracle_cfg(args.config)
+    ins = layer_solver_inputs(ocfg, make_x(ocfg, n_tokens=n, seed=0))
+    H = ins[0].shape[1]
+    P = n * H
+    d_u = torch.randn(n, H, ins[1].shape[-1], generator=torch.Generator().manual_seed(1))
     cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
-    sl = [t[:sample_tokens].contiguous() for t in ins_cpu]
-    # the reference solver consumes symmetric Q / Q_f (bench_lqr_solvers.py:125,127)
-    P = sl[0].shape[0] * H
 
     def fwd():
         with torch.no_grad():
-            riccati_solve(*sl, T)
+            riccati_solve(*ins, T)
 
     def fwdbwd():
-        xs = [t.clone().requires_grad_(True) for t in sl]
+        xs = [t.clone().requires_grad_(True) for t in ins]
         u = riccati_solve(*xs, T)
         torch.autograd.grad(u, xs, torch.ones_like(u))
 
-    res = {}
-    for name, fn, reps in (("fwd", fwd, 5), ("fwd_bwd", fwdbwd, 5)):
+    reps_fb = 5 if T < 512 else 3
+    rate = {}
+    for name, fn, reps in (("fwd", fwd, 5), ("fwd_bwd", fwdbwd, reps_fb)):
         fn()
         _note(f"cpu baseline {name}: warm-up done")
         ts = []
@@ -205,23 +211,78 @@ def cpu_baseline(ins_cpu, T, H, sample_tokens, d_u_cpu=None, grad_limit=1e6):
             fn()
             ts.append(time.perf_counter() - t0)
             _note(f"cpu baseline {name}: rep {i + 1}/{reps} {ts[-1]:.1f} s")
-        res[name] = P / statistics.median(ts)
-    out = {"value": res["fwd_bwd"], "unit": "solves/s", "cores": torch.get_num_threads(), "kind": "port",
-           "fwd_value": res["fwd"],
-           "sample": f"{sample_tokens} tokens x {H} heads = {P} problems of the same workload, T={T}; "
-                     f"oracle/ref_torch.riccati_solve (reference direct_lqr_solve restated), fwd median of 5, "
-                     f"fwd+bwd (autograd) median of 5, each after 1 warm-up, torch threads={torch.get_num_threads()}, "
-                     f"os.cpu_count()={cores}, cpu: {_cpu_model()}"}
-    if d_u_cpu is not None:
-        n_acc = sample_tokens if T < 512 else min(sample_tokens, 16)
-        acc = accuracy_vs_fp64([t[:n_acc] for t in sl], d_u_cpu[:n_acc], T, grad_limit)
-        out["ref_rel_err"] = acc["reference_riccati_fp32"]["max"]
-        out["ref_kkt_rel_err"] = acc["reference_kkt_fp32"]["max"]
-        out["hip_rel_err"] = acc["hip"]["max"]
-        out["accuracy"] = {"vs": "fp64 oracle (oracle/lqr64.py), same inputs and upstream gradient, "
-                                 f"{n_acc} tokens x {H} heads; per tensor max|x-x64|/max|x64| over u and the nine "
-                                 "gradients (None: non-finite output)", **acc}
-    return out
+        rate[name] = P / statistics.median(ts)
+    ref = solve_grads(LQRProblem(*ins, T), d_u.double().numpy())
+    _note("cpu baseline: fp64 oracle done")
+    acc = {}
+    for name, fn in (("reference_riccati_fp32", riccati_solve), ("reference_kkt_fp32", kkt_solve)):
+        try:
+            xs = [t.detach().clone().requires_grad_(True) for t in ins]
+            with np.errstate(all="ignore"):
+                u = fn(*xs, T)
+                gs = torch.autograd.grad(u, xs, d_u, allow_unused=True)
+                out = {"u": u.detach().double().numpy()}
+                for k, g in zip(NAMES, gs):
+                    g = g.detach().double().numpy()
+                    out[k] = 0.5 * (g + np.swapaxes(g, -1, -2)) if k in ("Q", "Q_f") else g
+            per = _per_output_errors(out, ref)
+        except RuntimeError as e:  # e.g. a singular solve in fp32
+            per = {"error": str(e)}
+        acc[name] = {"max": _max_or_none(per), "per_output": per}
+        _note(f"cpu baseline: {name} accuracy done")
+    np.savez(args.cpu_leg, T=T, dU=d_u.numpy(), **{f"in_{k}": t.numpy() for k, t in zip(NAMES, ins)},
+             **{f"ref_{k}": ref[k] for k in ["u"] + NAMES})
+    print(json.dumps({
+        "value": rate["fwd_bwd"], "unit": "solves/s", "cores": torch.get_num_threads(), "kind": "port",
+        "fwd_value": rate["fwd"],
+        "sample": f"{n} tokens x {H} heads = {P} problems of the same workload (oracle/inputs.py, seed 0), T={T}; "
+                  f"oracle/ref_torch.riccati_solve (reference direct_lqr_solve restated), fwd median of 5, "
+                  f"fwd+bwd (autograd) median of {reps_fb}, each after 1 warm-up, torch threads="
+                  f"{torch.get_num_threads()}, os.cpu_count()={cores}, cpu: {_cpu_model()}; run in a process of "
+                  f"its own that never touches the GPU, before the GPU measurement",
+        "accuracy": acc}), flush=True)
+
+
+def run_cpu_leg(args):
+    """Run `cpu_leg` in a child process (before this process initialises the GPU) and wait for it:
+    returns (its JSON result or None, the NPZ path, its exit status)."""
+    import subprocess
+    import tempfile
+    fd, path = tempfile.mkstemp(prefix="ttc_cpu_leg_", suffix=".npz")
+    os.close(fd)
+    cmd = [sys.executable, os.path.abspath(__file__), "--cpu-leg", path, "--config", args.config,
+           "--cpu-sample-tokens", str(args.cpu_sample_tokens), "--horizon", str(args.horizon)]
+    if PROGRESS:
+        cmd.append("--progress")
+    _note(f"cpu baseline: child process {' '.join(cmd[1:])}")
+    try:
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=900)
+        rc, text = r.returncode, r.stdout
+    except subprocess.TimeoutExpired as e:
+        rc, text = "timeout", e.stdout or ""
+        text = text.decode() if isinstance(text, bytes) else text
+    lines = [line for line in text.splitlines() if line.startswith("{")]
+    res = json.loads(lines[-1]) if lines else None
+    return res, path, rc
+
+
+def hip_accuracy(path, grad_limit, solver_kw):
+    """This solver on the CPU leg's sample (NPZ) against the fp64 oracle outputs saved with it."""
+    import numpy as np
+    import torch
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+    z = np.load(path)
+    T = int(z["T"])
+    xs = [torch.from_numpy(z[f"in_{k}"]).cuda().float().requires_grad_(True) for k in NAMES]
+    try:
+        u = hip_lqr_solve(*xs, T, grad_limit=grad_limit, **solver_kw)
+        gs = torch.autograd.grad(u, xs, torch.from_numpy(z["dU"]).cuda().to(u.dtype))
+        out = {"u": u.detach().cpu().double().numpy()}
+        out.update({k: g.detach().cpu().double().numpy() for k, g in zip(NAMES, gs)})
+        per = _per_output_errors(out, {k: z[f"ref_{k}"] for k in ["u"] + NAMES})
+    except RuntimeError as e:  # a guard of the solver
+        per = {"error": str(e)}
+    return {"max": _max_or_none(per), "per_output": per}
 
 
 def _solver_for(ins):
@@ -274,11 +335,15 @@ def _note(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False, grad_limit=1e6):
+def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False, grad_limit=1e6, solver_kw=None):
     """Forward: mean per-call GPU time from HIP events on the launch stream.  fwd+bwd: wall
-    time of `steps` steps between two device synchronisations."""
+    time of `steps` steps between two device synchronisations, and the peak device memory the
+    steps allocate beyond what is allocated before them (the reference bench's measure,
+    `bench_lqr_solvers.py:48-68`: max_memory_allocated - memory_allocated around fwd+bwd)."""
     import torch
-    hip_lqr_solve = _solver_for(ins)
+    solve = _solver_for(ins)
+    kw = dict(solver_kw or {})
+    hip_lqr_solve = (lambda *a, **k: solve(*a, **kw, **k)) if kw else solve
     stream = torch.cuda.current_stream()
     for i in range(warmup):
         with torch.no_grad():
@@ -308,12 +373,15 @@ def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False, grad_lim
         step()
         _note(f"warm-up fwd+bwd {i + 1}/{warmup}")
     torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
     t0 = time.perf_counter()
     for i in range(steps):
         step()
         _note(f"timed fwd+bwd {i + 1}/{steps}")
     torch.cuda.synchronize()
     res["step_ms"] = (time.perf_counter() - t0) / steps * 1e3
+    res["peak_mem_bytes"] = max(0, torch.cuda.max_memory_allocated() - base)
     from ttc.solvers.hip_lqr import last_backward_stats
     res["bwd_fallback_problems"] = last_backward_stats["fallback"]
     return res
@@ -370,12 +438,20 @@ def main():
     global PROGRESS
     args = parse()
     PROGRESS = args.progress
+    if args.cpu_leg:
+        cpu_leg(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the LQR problems shard over tokens with no "
                                    "exchange (each rank would run these kernels on its N/G tokens), so a "
                                    "multi-GPU figure is not produced here",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    # the CPU baseline first, in a child process that never touches the GPU, started before this
+    # process initialises it (and finished before the GPU is timed, so the two do not share the host)
+    leg = None
+    if not (args.no_cpu_baseline or args.copy_calibration > 0 or args.sweep or args.fwd_only):
+        leg = run_cpu_leg(args)
     import torch
     if args.copy_calibration > 0:
         n = int(args.copy_calibration * (1 << 30)) // 4
@@ -398,8 +474,13 @@ def main():
     ins, d_u, xshape = layer_workload(args.config, args.tokens, dev, factored=args.factored)
     N = ins[0].shape[0]
     P = N * H
+    solver_kw = {}
+    if args.precision != "auto":
+        solver_kw["precision"] = args.precision
+    if args.stable_backward:
+        solver_kw["stable_backward"] = True
     r = time_solver(ins, d_u, T, args.steps, args.warmup, stash=args.stash, fwd_only=args.fwd_only,
-                    grad_limit=c.get("grad_limit", 1e6))
+                    grad_limit=c.get("grad_limit", 1e6), solver_kw=solver_kw)
     fwd_gpu_ms = r["fwd_ms"]
     if args.fwd_only:
         print(json.dumps({"mode": "fwd-only", "fwd_ms": fwd_gpu_ms, "fwd_solves_per_s": P / (fwd_gpu_ms * 1e-3),
@@ -442,8 +523,11 @@ def main():
         "fwd_ms": fwd_gpu_ms,
         "fwd_wall_ms": r["fwd_wall_ms"],
         "bwd_fallback_problems": r["bwd_fallback_problems"],
+        "peak_mem_bytes_fwd_bwd": r["peak_mem_bytes"],
+        "solver": {"precision": args.precision, "stable_backward": args.stable_backward},
         "tokens_per_s_fwd_bwd": N / step_s,
         "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
+        "fwd_bwd_tflops": (F_fwd + flops_bwd(d, T)) * P / step_s / 1e12,
         "roofline": {"bound": "mfma+fp64" if long_h else "mfma", "achieved": achieved / 1e12,
                      "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": achieved / PEAK_FP32_MFMA,
                      "traffic": traffic, "kernel": kern, "flops_per_problem": F_fwd,
@@ -453,11 +537,13 @@ def main():
         out["roofline"]["peak_note"] = ("fp32 matrix peak of the symplectic sweep; the rescue's fp64 sweeps run on "
                                         + ("the matrix cores" if d == 16 else "the vector ALU")
                                         + " (78.6 TFLOP/s fp64)")
+        out["roofline"]["frac_of_fp64_peak"] = achieved / PEAK_FP64
     extras = []
     for cfg in [x.strip() for x in args.extra_configs.split(",") if x.strip()]:
         if cfg == args.config:
             continue
-        extras.append(extra_entry(cfg, args.extra_tokens, dev))
+        # configs 5 / 5b (decode-size and 4 x 1024 batches) at their full BASELINE size
+        extras.append(extra_entry(cfg, 0 if cfg in ("5", "5b") else args.extra_tokens, dev))
     if args.config == "2" and "4" in args.extra_configs:
         # config 4 as stored (bf16): the factored bf16 entry points on the same token sample
         extras.append(extra_entry("4", args.extra_tokens, dev, bf16=True))
@@ -469,6 +555,7 @@ def main():
         rf = time_solver(ins_f, du_f, T, 3, 1, stash=args.stash, grad_limit=c.get("grad_limit", 1e6))
         out["factored"] = {"fwd_ms": rf["fwd_ms"], "fwd_bwd_ms": rf["step_ms"],
                            "fwd_bwd_solves_per_s": P / (rf["step_ms"] * 1e-3),
+                           "peak_mem_bytes_fwd_bwd": rf["peak_mem_bytes"],
                            "input_bytes_per_problem": 4 * (5 * d + 1 + (c["b_rank"] + c["q_rank"]) / H + c["q_rank"])}
         del ins_f, du_f
         torch.cuda.empty_cache()
@@ -477,23 +564,25 @@ def main():
         # forward+backward step each, on the factored inputs (the materialised Q_f alone would be
         # 137 GB); d_u ~ N(0,1)
         out["full_size"] = [full_size_entry(cfg, dev) for cfg in ("3", "4")]
-    if not args.no_cpu_baseline and T >= 512:
-        # switched off: the one GPU-box run of this leg at T = 1024 (2 tokens, complete output) ended
-        # with "terminate called without an active exception" at interpreter teardown; the cause is
-        # not found, so the leg stays off for long horizons
-        out["cpu_baseline"] = None
-        out["cpu_baseline_note"] = "not run at T >= 512 (teardown abort after the leg's one run; cause not found)"
-    elif not args.no_cpu_baseline:
-        n_s = min(args.cpu_sample_tokens, N)
-        ins_cpu = [t.detach()[:n_s].cpu() if i < 9 else t.detach().cpu() for i, t in enumerate(ins)]
-        if len(ins_cpu) == 11:  # the reference solver takes materialised B, Q, Q_f
-            A, cB, cQ, R, cQf, lA, lB, lQ, h0, Bs, Gs = ins_cpu
-            ins_cpu = [A, torch.einsum("nr,rij->nij", cB, Bs), torch.einsum("nr,rij->nij", cQ, Gs), R,
-                       torch.einsum("nhr,rij->nhij", cQf, Gs), lA, lB, lQ, h0]
-        out["cpu_baseline"] = cpu_baseline(ins_cpu, T, H, n_s, d_u_cpu=d_u[:n_s].detach().cpu(),
-                                           grad_limit=c.get("grad_limit", 1e6))
-    else:
-        out["cpu_baseline"] = None
+    out["cpu_baseline"] = None
+    if leg is not None:
+        res, path, rc = leg
+        if res is not None:
+            acc = res.pop("accuracy")
+            acc["hip"] = hip_accuracy(path, c.get("grad_limit", 1e6), solver_kw)
+            res["ref_rel_err"] = acc["reference_riccati_fp32"]["max"]
+            res["ref_kkt_rel_err"] = acc["reference_kkt_fp32"]["max"]
+            res["hip_rel_err"] = acc["hip"]["max"]
+            res["accuracy"] = {"vs": "fp64 oracle (oracle/lqr64.py) on the CPU sample, same upstream gradient "
+                                     "(N(0,1)); per tensor max|x-x64|/max|x64| over u and the nine gradients "
+                                     "(None: non-finite output)", **acc}
+        out["cpu_baseline"] = res
+        if rc != 0:
+            out["cpu_baseline_exit_status"] = rc
+        try:
+            os.unlink(path)
+        except OSError:
+            pass
     print(json.dumps(out), flush=True)
 
 
@@ -511,13 +600,22 @@ def extra_entry(cfg, tokens, dev, bf16=False):
     Pe = ins_e[0].shape[0] * He
     re_ = time_solver(ins_e, du_e, Te, 3, 1, grad_limit=ce.get("grad_limit", 1e6))
     ach = flops_fwd(de, Te) * Pe / (re_["fwd_ms"] * 1e-3)
+    ach_fb = (flops_fwd(de, Te) + flops_bwd(de, Te)) * Pe / (re_["step_ms"] * 1e-3)
     e = {"config": f"cfg{cfg}" + ("-bf16" if bf16 else ""), "x": xs_e, "d": de, "T": Te, "heads": He,
          "problems": Pe, "storage": "bf16 (factored inputs, d_u and gradients)" if bf16 else "fp32",
          "fwd_ms": re_["fwd_ms"], "fwd_solves_per_s": Pe / (re_["fwd_ms"] * 1e-3),
          "fwd_bwd_ms": re_["step_ms"], "fwd_bwd_solves_per_s": Pe / (re_["step_ms"] * 1e-3),
+         "tokens_per_s_fwd_bwd": ins_e[0].shape[0] / (re_["step_ms"] * 1e-3),
          "bwd_fallback_problems": re_["bwd_fallback_problems"],
+         "peak_mem_bytes_fwd_bwd": re_["peak_mem_bytes"],
          "roofline_frac": ach / PEAK_FP32_MFMA, "achieved_tflops": ach / 1e12,
+         "fwd_bwd_tflops": ach_fb / 1e12, "fwd_bwd_frac": ach_fb / PEAK_FP32_MFMA,
          "traffic": None if bf16 else traffic_from_profiles(f"lqr_fwd_cfg{cfg}")}
+    if Te >= 512 and de <= 32:
+        # precision "auto": the fp32 symplectic sweep, its rejected problems and the backward in fp64
+        e["dtype"] = "f32+f64"
+        e["roofline_frac_of_fp64_peak"] = ach / PEAK_FP64
+        e["fwd_bwd_frac_of_fp64_peak"] = ach_fb / PEAK_FP64
     del ins_e, du_e
     torch.cuda.empty_cache()
     return e
@@ -541,6 +639,7 @@ def full_size_entry(cfg, dev):
          "fwd_bwd_ms": re_["step_ms"], "fwd_bwd_solves_per_s": Pe / (re_["step_ms"] * 1e-3),
          "tokens_per_s_fwd_bwd": ins_f[0].shape[0] / (re_["step_ms"] * 1e-3),
          "bwd_fallback_problems": re_["bwd_fallback_problems"],
+         "peak_mem_bytes_fwd_bwd": re_["peak_mem_bytes"],
          "roofline_frac": ach / PEAK_FP32_MFMA, "achieved_tflops": ach / 1e12,
          "wall_s": None}
     del ins_f, du_f

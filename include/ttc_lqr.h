@@ -303,12 +303,13 @@ int ttc_lqr_backward_factored_bf16(const uint16_t* A_diag, const uint16_t* coeff
                                    void* stream);
 
 /* ---- Allocation-free backward ----
- * No counterpart in the reference.  For callers that cannot allocate device memory -- code under
- * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc: ttc_lqr_backward with
- * the workspace replaced by a fixed device scratch of TTC_LQR_NOALLOC_SCRATCH_BYTES (256 MiB), a
- * file-scope array of the library that each GPU it runs on holds until the process ends.  Same
- * arguments, results and status bits as ttc_lqr_backward; the tokens are processed in chunks that
- * fit the scratch (one stream synchronisation per chunk).  Returns TTC_LQR_ESCRATCH when even one
+ * No counterpart in the reference.  For callers that cannot allocate device memory -- tight
+ * serving loops, harnesses that forbid hipMalloc: ttc_lqr_backward with the workspace replaced by
+ * a fixed device scratch of TTC_LQR_NOALLOC_SCRATCH_BYTES (256 MiB), a file-scope array of the
+ * library that each GPU it runs on holds until the process ends.  Same arguments, results and
+ * status bits as ttc_lqr_backward; the tokens are processed in chunks that fit the scratch, and
+ * each chunk reads its rejected-problem count back to the host and synchronises the stream, so
+ * the call cannot be recorded by HIP graph capture.  Returns TTC_LQR_ESCRATCH when even one
  * token's layout does not fit (e.g. d = 64 with T = 1024).  Calls no hipMalloc / hipFree.  Calls
  * that overlap on one GPU share its scratch and race: the caller orders them. */
 #define TTC_LQR_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)

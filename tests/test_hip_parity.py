@@ -412,6 +412,29 @@ def test_fused_lqr_solve_reference_signature():
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("extra", [(), (False,), ("LU",), ("LU", False), ("LU", True)])
+def test_fused_lqr_solve_func_reference_slots(extra):
+    """FusedLQRSolveFunc.apply with the reference's positional slots (fused_lqr.py:255-291):
+    (..., h0, T[, cache_level[, inv_guard]]), including the reference's own fused_lqr_solve call
+    that puts inv_guard in the cache_level slot; forward and the nine gradients of the backward
+    are bitwise those of hip_lqr_solve, and within 1e-4 of the fp64 oracle."""
+    from ttc.solvers import FusedLQRSolveFunc
+    ins = bench_solver_inputs(2, 8, 16, seed=2)
+    T = 24
+    pb = LQRProblem(*ins, T)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(3))
+    ref = run_hip(ins, T, dU.double().numpy())
+    xs = [t.cuda().requires_grad_(True) for t in ins]
+    u = FusedLQRSolveFunc.apply(*xs, T, *extra)
+    (u * dU.cuda()).sum().backward()
+    assert torch.equal(u.detach().cpu().double(), torch.from_numpy(ref["u"]))
+    for n, t in zip(NAMES, xs):
+        assert torch.equal(t.grad.cpu().double(), torch.from_numpy(ref[n])), n
+    ref64 = solve_grads(pb, dU.double().numpy())
+    for k in ["u"] + NAMES:
+        assert _relerr(ref[k], ref64[k]) <= TOL, k
+
+
 def test_layer_parameter_gradients_match_oracle():
     """TTCLayer(solver_impl="hip") (factored solve, fused rescale) on the GPU: gradients of
     in_proj, out_proj, Bs and Qs against fp64 autograd of the oracle layer around the fp64
@@ -453,6 +476,57 @@ def test_layer_default_path_on_config5_scales(T):
         e = _relerr(p.grad.cpu().numpy(), ref[name])
         print(f"   layer grad {name}: {e:.1e}", flush=True)
         assert e <= TOL, name
+
+
+@pytest.mark.parametrize("T", [64, 1024])
+@pytest.mark.parametrize("key,factored", [("riccati", None), ("kkt", None), ("fused", None), ("fused", False)])
+def test_layer_reference_keys_on_gpu(key, factored, T):
+    """TTCLayer(solver_impl=key).cuda() for the reference's registry keys (ttc_layer.py:18-22):
+    "riccati" / "kkt" (HIP kernels with Riccati steps; kkt with the stable backward for every
+    problem; fp64 sweeps at T = 1024), "fused" on its default factored path and on the
+    reference's materialised one (fused_lqr_solve / FusedLQRSolveFunc): the gradients of
+    in_proj, out_proj, Bs and Qs against fp64 autograd of the oracle layer, T = 64 and 1024."""
+    from ttc import TTCLayer
+    from _layer_oracle import oracle_layer_grads
+    torch.manual_seed(7)
+    layer = TTCLayer(32, 32, 16, 8, 16, 16, solver_impl=key, factored=factored).cuda()
+    x = torch.randn(3, 4, 32, generator=torch.Generator().manual_seed(T + 1))
+    dy = torch.randn(3, 4, 32, generator=torch.Generator().manual_seed(T + 2))
+    print(f"[layer key={key} factored={layer.factored} T={T}]", flush=True)
+    y = layer(x.cuda(), T=T)
+    (y * dy.cuda()).sum().backward()
+    ref = oracle_layer_grads(layer, x, dy, T)
+    for name, p in (("in_proj", layer.in_proj.weight), ("out_proj", layer.out_proj.weight), ("Bs", layer.Bs),
+                    ("Qs", layer.Qs)):
+        e = _relerr(p.grad.cpu().numpy(), ref[name])
+        print(f"   layer grad {name}: {e:.1e}", flush=True)
+        assert e <= TOL, name
+
+
+@pytest.mark.parametrize("T,cfg,n_tok,seed", [(64, 5, 16, 5), (1024, 5, 8, 5), (64, 2, 8, 1)])
+@pytest.mark.parametrize("name", ["direct_lqr_solve", "kkt_lqr_solve"])
+def test_reference_solvers_on_cuda_tensors(name, T, cfg, n_tok, seed):
+    """direct_lqr_solve / kkt_lqr_solve (ttc.solvers.torch_lqr, the reference's module path and
+    signature, torch_lqr.py:93-140) on CUDA tensors: u and the nine gradients against the fp64
+    oracle on config-5 token scales (T = 64 and 1024) and a config-2 slice.  They keep the
+    reference's 1e6 guard, so d_u is scaled (gradients are linear in it) to put the largest
+    guarded gradient at 1e3."""
+    import ttc.solvers.torch_lqr as TL
+    fn = getattr(TL, name)
+    ins = layer_solver_inputs(cfg, make_x(cfg, n_tokens=n_tok, seed=seed))
+    pb = LQRProblem(*ins, T)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(seed + 3)).double().numpy()
+    ref = solve_grads(pb, dU)
+    s = min(1.0, 1e3 / max(np.abs(ref[k]).max() for k in ("A_diag", "B", "Q", "R_inv", "Q_f", "h0")))
+    xs = [t.cuda().requires_grad_(True) for t in ins]
+    u = fn(*xs, T)
+    (u * torch.from_numpy(dU * s).float().cuda()).sum().backward()
+    errs = {"u": _relerr(u.detach().cpu().numpy(), ref["u"])}
+    for n, t in zip(NAMES, xs):
+        errs[n] = _relerr(t.grad.cpu().numpy(), ref[n] * s)
+    print(f"[{name} cfg{cfg} T={T}] d_u scale {s:.1e} " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()),
+          flush=True)
+    assert max(errs.values()) <= TOL, errs
 
 
 def test_padding_odd_dims_and_ragged_problem_count():
@@ -569,6 +643,27 @@ def test_default_precision_on_config5_scales_below_fp64_horizon(T, seed):
     x = make_x(5, n_tokens=512, seed=seed)
     out = check_case(f"cfg5-scales T={T}", layer_solver_inputs(5, x), T, seed=seed, grad_limit=math.inf)
     assert out["_fallback"] > 0  # the sample exercises the backward's fallback
+
+
+@pytest.mark.parametrize("factored", [False, True])
+def test_profiler_ranges_name_the_reference_stages(factored):
+    """A torch.profiler trace of a forward + backward attributes the solver's time to ranges named
+    after the reference's stages (fused_lqr.py:58,186,200): fwd:lqr_symplectic_rev_iter,
+    bwd:lqr_symplectic_fwd_iter_diff, plus the host's status waits (and, through TTCLayer's factored
+    path, the fused rescale's two ranges)."""
+    from ttc import TTCLayer
+    layer = TTCLayer(32, 32, 16, 8, 16, 16, solver_impl="hip", factored=factored).cuda()
+    x = torch.randn(2, 3, 32, device="cuda")
+    layer(x, T=8).sum().backward()  # warm-up outside the trace
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        layer(x, T=8).sum().backward()
+    names = {e.name for e in prof.events()}
+    want = {"fwd:lqr_symplectic_rev_iter", "bwd:lqr_symplectic_fwd_iter_diff", "fwd:ttc_lqr_status",
+            "bwd:ttc_lqr_status"}
+    if factored:
+        want |= {"fwd:ttc_lqr_rescale", "bwd:ttc_lqr_rescale_backward"}
+    print(sorted(n for n in names if ":" in n and ("fwd" in n or "bwd" in n)), flush=True)
+    assert want <= names, want - names
 
 
 def test_T1_closed_form():

@@ -138,3 +138,27 @@ def test_bench_traffic_records_and_single_gpu_contract():
     res = subprocess.run([sys.executable, bench.__file__, "--gpus", "2"], capture_output=True, text=True, timeout=120)
     assert res.returncode == 2
     assert "one GPU" in json.loads(res.stdout.strip().splitlines()[-1])["error"]
+
+
+def test_bench_cpu_leg_child(tmp_path):
+    """bench.py's CPU-baseline leg as the benchmark runs it: a child process that never touches the
+    GPU (no HIP library is loaded in it) times the reference restatement on a CPU sample, measures
+    the reference's fp32 solvers against the fp64 oracle, writes the sample and the oracle outputs
+    for the GPU process, prints one JSON line and exits 0."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = tmp_path / "leg.npz"
+    code = ("import runpy, sys; sys.argv = ['bench.py', '--cpu-leg', %r, '--config', '2', '--cpu-sample-tokens', "
+            "'2', '--horizon', '6']; runpy.run_path(%r, run_name='__main__'); "
+            "assert not [m for m in sys.modules if m == 'ttc' or m.startswith('ttc.')], 'HIP library loaded'"
+            % (str(out), os.path.join(root, "bench.py")))
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300, cwd=root)
+    assert r.returncode == 0, r.stderr[-2000:]
+    res = json.loads([line for line in r.stdout.splitlines() if line.startswith("{")][-1])
+    assert res["kind"] == "port" and res["value"] > 0 and res["fwd_value"] > 0
+    assert res["accuracy"]["reference_riccati_fp32"]["max"] < 1e-4
+    z = np.load(out)
+    assert int(z["T"]) == 6 and z["in_A_diag"].shape == (2, 8, 16) and z["ref_u"].shape == (2, 8, 16)

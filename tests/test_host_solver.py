@@ -137,7 +137,7 @@ def test_reference_export_surface():
     import ttc
     import ttc.solvers as S
     from ttc.layers.ttc_layer import LQR_SOLVER_IMPL_MAP
-    from ttc.solvers.fused_lqr import fused_lqr_solve, FusedLQRSolveFunc  # noqa: F401
+    from ttc.solvers.fused_lqr import fused_lqr_solve, FusedLQRSolveFunc
     from ttc.solvers.torch_lqr import direct_lqr_solve, kkt_lqr_solve
     assert hasattr(ttc, "TTCLayer")
     for name in ("direct_lqr_solve", "kkt_lqr_solve", "fused_lqr_solve"):
@@ -147,6 +147,12 @@ def test_reference_export_surface():
         assert key in LQR_SOLVER_IMPL_MAP
     ref_params = ["A_diag", "B", "Q", "R_inv_diag", "Q_f", "gamma_A", "gamma_B", "gamma_Q", "h0", "T", "inv_guard"]
     assert list(inspect.signature(fused_lqr_solve).parameters) == ref_params
+    # the autograd Function keeps the reference's positional slots (fused_lqr.py:255-269):
+    # apply(..., h0, T, cache_level="LU", inv_guard=False)
+    fsig = inspect.signature(FusedLQRSolveFunc.forward)
+    assert list(fsig.parameters) == ["ctx"] + ref_params[:10] + ["cache_level", "inv_guard"]
+    assert fsig.parameters["cache_level"].default == "LU" and fsig.parameters["inv_guard"].default is False
+    assert FusedLQRSolveFunc is not S.HipLQRSolveFunc
     sig = inspect.signature(S.hip_lqr_solve)
     assert list(sig.parameters)[10] == "inv_guard"
     for k in ("grad_limit", "stash", "precision", "stable_backward"):

@@ -48,6 +48,7 @@ into passes that fit, and one pass is fastest).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 import os
@@ -180,6 +181,29 @@ def _stream_handle(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+@contextlib.contextmanager
+def _stage(dev, name: str):
+    """The device of a library call, inside a profiler range named after the reference's stage it
+    covers (``torch.profiler.record_function``, as the reference names its stages,
+    ``fused_lqr.py:58,103,112,186,200``): ``fwd:lqr_symplectic_rev_iter`` is the forward call
+    (the sweep, the final solve -- the reference's ``fwd:torch.linalg.lu_solve`` -- and step 0 --
+    its ``fwd:lqr_symplectic_dec_first_step`` -- run in one launch sequence here),
+    ``bwd:lqr_symplectic_fwd_iter_diff`` the backward call (its ``Quu_0`` solve is the
+    reference's ``bwd:torch.linalg.lu_solve``); ``*:ttc_lqr_status`` is the host's wait for the
+    status word."""
+    if dev is None:
+        with torch.profiler.record_function(name):
+            yield
+        return
+    with torch.cuda.device(dev), torch.profiler.record_function(name):
+        yield
+
+
+def _read_status(status, name: str) -> int:
+    with _stage(None, name):
+        return int(status.item())
+
+
 class HipLQRSolveFunc(torch.autograd.Function):
 
     @staticmethod
@@ -220,13 +244,13 @@ class HipLQRSolveFunc(torch.autograd.Function):
         # the fp64 rescue's problem list (4 bytes a problem; long horizons only)
         fws_bytes = lib.ttc_lqr_forward_workspace_bytes(bs, nh, Dp, Dp, T, flags)
         fws = torch.empty(fws_bytes, device=dev, dtype=torch.uint8) if fws_bytes > 0 else None
-        with torch.cuda.device(dev):
+        with _stage(dev, "fwd:lqr_symplectic_rev_iter"):
             rc = lib.ttc_lqr_forward_ws(*[t.data_ptr() for t in f32], bs, nh, Dp, Dp, T, flags, u.data_ptr(),
                                         None if st is None else st.data_ptr(),
                                         None if fws is None else fws.data_ptr(), fws_bytes, status.data_ptr(),
                                         _stream_handle(dev))
         check(rc, "ttc_lqr_forward_ws")
-        fst = int(status.item())
+        fst = _read_status(status, "fwd:ttc_lqr_status")
         if fst & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
@@ -264,7 +288,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
                          device=dev, dtype=torch.uint8)
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         n_fb = ctypes.c_int64(0)
-        with torch.cuda.device(dev):
+        with _stage(dev, "bwd:lqr_symplectic_fwd_iter_diff"):
             rc = lib.ttc_lqr_backward(
                 *[t.data_ptr() for t in f32], u.data_ptr(), dU.data_ptr(), bs, nh, Dp, Dp, T, flags,
                 None if st is None else st.data_ptr(),
@@ -273,7 +297,7 @@ class HipLQRSolveFunc(torch.autograd.Function):
                 ws.data_ptr(), ws.numel(), limit, status.data_ptr(), ctypes.byref(n_fb), _stream_handle(dev))
         check(rc, "ttc_lqr_backward")
         last_backward_stats.update(problems=bs * nh, fallback=int(n_fb.value))
-        if int(status.item()) & _ERROR_BITS:
+        if _read_status(status, "bwd:ttc_lqr_status") & _ERROR_BITS:
             raise RuntimeError(_BWD_MSG)
         out = (g["A"][..., :d], g["B"][:, :d, :du], g["Q"][:, :d, :d], g["R"][..., :du], g["Qf"][:, :, :d, :d],
                g["lA"], g["lB"][..., :du], g["lQ"][..., :d], g["h0"][..., :d])
@@ -403,7 +427,7 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16), flags)
         ws = torch.empty(_workspace_bytes(full, one, dev), device=dev, dtype=torch.uint8)
         fwd = lib.ttc_lqr_forward_factored_bf16 if bf16 else lib.ttc_lqr_forward_factored
-        with torch.cuda.device(dev):
+        with _stage(dev, "fwd:lqr_symplectic_rev_iter"):
             rc = fwd(*[t.data_ptr() for t in xs], bs, nh, Dp, Dp, rb, rq, T, flags, u.data_ptr(),
                      None if st is None else st.data_ptr(), ws.data_ptr(), ws.numel(), status.data_ptr(),
                      _stream_handle(dev))
@@ -412,11 +436,11 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         y = u
         if mode:
             y = torch.empty_like(u)
-            with torch.cuda.device(dev):
+            with _stage(dev, "fwd:ttc_lqr_rescale"):
                 rc = lib.ttc_lqr_rescale(u.data_ptr(), xs[8].data_ptr(), bs, nh, Dp, Dp, mode, y.data_ptr(),
                                          _stream_handle(dev))
             check(rc, "ttc_lqr_rescale")
-        fst = int(status.item())
+        fst = _read_status(status, "fwd:ttc_lqr_status")
         if fst & _ERROR_BITS:
             raise RuntimeError(_FWD_MSG)
         if need_grad:
@@ -441,7 +465,7 @@ class HipLQRFactoredFunc(torch.autograd.Function):
             dU[..., :du] = d_u.to(store)
         if mode:  # d_y -> d_u through the fused rescale
             dY, dU = dU, torch.empty_like(dU)
-            with torch.cuda.device(dev):
+            with _stage(dev, "bwd:ttc_lqr_rescale_backward"):
                 rc = lib.ttc_lqr_rescale_backward(u.data_ptr(), xs[8].data_ptr(), dY.data_ptr(), bs, nh, Dp, Dp, mode,
                                                   dU.data_ptr(), _stream_handle(dev))
             check(rc, "ttc_lqr_rescale_backward")
@@ -457,13 +481,13 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         limit = grad_limit if math.isfinite(grad_limit) else float("inf")
         n_fb = ctypes.c_int64(0)
         bwd = lib.ttc_lqr_backward_factored_bf16 if bf16 else lib.ttc_lqr_backward_factored
-        with torch.cuda.device(dev):
+        with _stage(dev, "bwd:lqr_symplectic_fwd_iter_diff"):
             rc = bwd(*[t.data_ptr() for t in xs], u.data_ptr(), dU.data_ptr(), bs, nh, Dp, Dp, rb, rq, T, flags,
                      None if st is None else st.data_ptr(), *[t.data_ptr() for t in g], ws.data_ptr(), ws.numel(),
                      limit, status.data_ptr(), ctypes.byref(n_fb), _stream_handle(dev))
         check(rc, "ttc_lqr_backward_factored" + ("_bf16" if bf16 else ""))
         last_backward_stats.update(problems=bs * nh, fallback=int(n_fb.value))
-        if int(status.item()) & _ERROR_BITS:
+        if _read_status(status, "bwd:ttc_lqr_status") & _ERROR_BITS:
             raise RuntimeError(_BWD_MSG)
         out = (g[0][..., :d], g[1], g[2], g[3][..., :du], g[4], g[5], g[6][..., :du], g[7][..., :d],
                g[8][..., :d], g[9][:, :d, :du], g[10][:, :d, :d])
