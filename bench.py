@@ -82,6 +82,9 @@ def parse():
                          "TTCLayer(solver_impl='riccati') runs on CUDA tensors, with --stable-backward what 'kkt' runs")
     ap.add_argument("--stable-backward", action="store_true",
                     help="the stable backward for every problem (the 'kkt' key's backward)")
+    ap.add_argument("--status-check", default="sync", choices=["sync", "deferred"],
+                    help="hip_lqr_solve's status_check: 'deferred' takes the host synchronisation out of the "
+                         "forward (its status word is read by the backward)")
     ap.add_argument("--fwd-only", action="store_true",
                     help="profiling aid: time only the forward solve (the JSON value is then fwd solves/s)")
     ap.add_argument("--extra-configs", default="3,4,5,5b",
@@ -382,6 +385,8 @@ def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False, grad_lim
     torch.cuda.synchronize()
     res["step_ms"] = (time.perf_counter() - t0) / steps * 1e3
     res["peak_mem_bytes"] = max(0, torch.cuda.max_memory_allocated() - base)
+    from ttc.solvers.hip_lqr import check_deferred_status
+    check_deferred_status()  # forwards timed with a deferred status check (outside the timed regions)
     from ttc.solvers.hip_lqr import last_backward_stats
     res["bwd_fallback_problems"] = last_backward_stats["fallback"]
     return res
@@ -402,7 +407,7 @@ def sweep(args):
     `ref_metric` next to solves/s and the algorithmic FLOP/s."""
     import torch
     from oracle.inputs import bench_solver_inputs
-    from ttc.solvers.hip_lqr import hip_lqr_solve
+    from ttc.solvers.hip_lqr import check_deferred_status, hip_lqr_solve
     dev = torch.device("cuda:0")
     d = args.sweep_dim
     points = [(2 ** i, 1024) for i in range(4, 12)] if args.sweep == "horizon" else [(64, 2 ** i) for i in range(4, 14)]
@@ -412,11 +417,27 @@ def sweep(args):
         gr = torch.randn(batch, 1, d, device=dev, generator=torch.Generator(device=dev).manual_seed(1))
 
         def step():
-            u = hip_lqr_solve(*xs, T)
+            u = hip_lqr_solve(*xs, T, status_check=args.status_check)
             return torch.autograd.grad(u, xs, gr)
 
+        def fwd():
+            with torch.no_grad():
+                hip_lqr_solve(*ins, T, status_check=args.status_check)
+
         step()
+        fwd()
         torch.cuda.synchronize()
+        tf = []
+        for _ in range(5):  # one forward, waited for: its latency
+            t0 = time.perf_counter()
+            fwd()
+            torch.cuda.synchronize()
+            tf.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        for _ in range(5):  # five forwards back to back: with a deferred status they queue up
+            fwd()
+        torch.cuda.synchronize()
+        tf_pipe = (time.perf_counter() - t0) / 5
         ts, peaks = [], []
         for _ in range(5):
             torch.cuda.reset_peak_memory_stats()
@@ -427,7 +448,10 @@ def sweep(args):
             ts.append(time.perf_counter() - t0)
             peaks.append(torch.cuda.max_memory_allocated() - before)
         t = statistics.median(ts)
+        check_deferred_status()  # the deferred forwards' status words (outside the timed regions)
         print(json.dumps({"sweep": args.sweep, "T": T, "batch": batch, "heads": 1, "d": d,
+                          "status_check": args.status_check, "fwd_ms": statistics.median(tf) * 1e3,
+                          "fwd_back_to_back_ms": tf_pipe * 1e3,
                           "fwd_bwd_ms": t * 1e3, "solves_per_s": batch / t,
                           "tflops": batch * (flops_fwd(d, T) + flops_bwd(d, T)) / t / 1e12,
                           "ref_metric": 4 * batch * d ** 3 * T * 1e-9 / t,
@@ -479,6 +503,8 @@ def main():
         solver_kw["precision"] = args.precision
     if args.stable_backward:
         solver_kw["stable_backward"] = True
+    if args.status_check != "sync":
+        solver_kw["status_check"] = args.status_check
     r = time_solver(ins, d_u, T, args.steps, args.warmup, stash=args.stash, fwd_only=args.fwd_only,
                     grad_limit=c.get("grad_limit", 1e6), solver_kw=solver_kw)
     fwd_gpu_ms = r["fwd_ms"]
@@ -524,7 +550,8 @@ def main():
         "fwd_wall_ms": r["fwd_wall_ms"],
         "bwd_fallback_problems": r["bwd_fallback_problems"],
         "peak_mem_bytes_fwd_bwd": r["peak_mem_bytes"],
-        "solver": {"precision": args.precision, "stable_backward": args.stable_backward},
+        "solver": {"precision": args.precision, "stable_backward": args.stable_backward,
+                   "status_check": args.status_check},
         "tokens_per_s_fwd_bwd": N / step_s,
         "tokens_per_s_fwd": N / (fwd_gpu_ms * 1e-3),
         "fwd_bwd_tflops": (F_fwd + flops_bwd(d, T)) * P / step_s / 1e12,

@@ -645,6 +645,93 @@ def test_default_precision_on_config5_scales_below_fp64_horizon(T, seed):
     assert out["_fallback"] > 0  # the sample exercises the backward's fallback
 
 
+@pytest.mark.parametrize("cfg,n_tok,T,seed", [(2, 16, 64, 1), (5, 16, 64, 5), (5, 4, 1024, 5)])
+def test_deferred_status_equals_sync(cfg, n_tok, T, seed):
+    """status_check="deferred": the forward returns without reading its status word, the backward
+    reads it (and picks the backward's arithmetic from it, as the synchronous forward does);
+    u and the nine gradients bit for bit those of the default mode, on nominal inputs and on
+    config-5 scales whose forward rescues problems in fp64."""
+    from ttc.solvers.hip_lqr import _deferred, check_deferred_status
+    check_deferred_status()
+    ins = layer_solver_inputs(cfg, make_x(cfg, n_tokens=n_tok, seed=seed))
+    pb = LQRProblem(*ins, T)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(seed)).double().numpy()
+    a = run_hip(ins, T, dU, grad_limit=math.inf)
+    solve = _solver()
+    xs = [t.cuda().float().requires_grad_(True) for t in ins]
+    u = solve(*xs, T, grad_limit=math.inf, status_check="deferred")
+    assert len(_deferred) == 1
+    (u * torch.as_tensor(dU, device="cuda", dtype=u.dtype)).sum().backward()
+    assert len(_deferred) == 0  # the backward read it
+    assert torch.equal(u.detach().cpu().double(), torch.from_numpy(a["u"]))
+    for n, t in zip(NAMES, xs):
+        assert torch.equal(t.grad.cpu().double(), torch.from_numpy(a[n])), n
+
+
+def test_deferred_status_raises_later():
+    """A NaN input under status_check="deferred": the forward returns; check_deferred_status()
+    raises the reference's forward RuntimeError, and so does the backward of such a forward."""
+    from ttc.solvers.hip_lqr import check_deferred_status
+    ins = bench_solver_inputs(2, 8, 16, seed=1)
+    ins[8] = ins[8].clone()
+    ins[8][0, 0, 0] = float("nan")
+    solve = _solver()
+    check_deferred_status()
+    with torch.no_grad():
+        solve(*[t.cuda() for t in ins], 8, status_check="deferred")
+    with pytest.raises(RuntimeError, match="forward recurrence"):
+        check_deferred_status()
+    check_deferred_status()  # forgotten once read
+    xs = [t.cuda().requires_grad_(True) for t in ins]
+    u = solve(*xs, 8, status_check="deferred")
+    with pytest.raises(RuntimeError, match="forward recurrence"):
+        u.sum().backward()
+
+
+@pytest.mark.parametrize("cfg,T", [(2, 64), (5, 64)])
+def test_deferred_forward_in_a_hip_graph(cfg, T):
+    """With status_check="deferred" the forward makes no host synchronisation, so it can be
+    recorded by HIP graph capture (torch.cuda.graph): replayed on three inputs copied into the
+    captured input tensors, with eager work and synchronisations between the replays, each
+    replay's u equals the eager forward on the same inputs bit for bit, and its status word
+    (kept, re-read after each replay) reports the same rescue as the eager forward (config-5
+    scales: problems recomputed in fp64 inside the graph)."""
+    from ttc.solvers.hip_lqr import _deferred, check_deferred_status
+    solve = _solver()
+    draws = [layer_solver_inputs(cfg, make_x(cfg, n_tokens=16, seed=40 + k)) for k in range(4)]
+    static = [t.cuda().float().contiguous() for t in draws[0]]
+    check_deferred_status()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side), torch.no_grad():  # warm-up outside the capture
+        solve(*static, T, status_check="deferred")
+    torch.cuda.current_stream().wait_stream(side)
+    check_deferred_status()
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        u_graph = solve(*static, T, status_check="deferred")
+    assert len(_deferred) == 1
+    status_word = _deferred[0]
+    rescued = 0
+    for k in (1, 2, 3):
+        for dst, src in zip(static, draws[k]):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got, got_status = u_graph.clone(), int(status_word.item())
+        check_deferred_status(keep=True)
+        with torch.no_grad():
+            ref = solve(*[t.cuda().float() for t in draws[k]], T)  # eager, synchronous status
+        torch.cuda.synchronize()
+        print(f"[graph cfg{cfg} replay {k}] status {got_status}", flush=True)
+        assert torch.equal(got, ref), k
+        assert got_status & 3 == 0
+        rescued += got_status & 4
+    assert (rescued > 0) == (cfg == 5)
+    _deferred.clear()
+
+
 @pytest.mark.parametrize("factored", [False, True])
 def test_profiler_ranges_name_the_reference_stages(factored):
     """A torch.profiler trace of a forward + backward attributes the solver's time to ranges named
@@ -734,6 +821,13 @@ def test_layer_end_to_end_matches_oracle_layer():
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
+# Outputs on which a fixture's recorded tolerance (4 x the fp64 oracle's own error against the
+# higher-precision solve) lies far above what this solver achieves: bounds at about 2.5-3x the
+# achieved error, so that a regression of the solver fails even where the fixture allows more.
+# oracle_cfg5b_undiscounted: achieved 3.6e-4 (A_diag) and 2.1e-2 (B) with the fp64 Riccati
+# sweep on the matrix cores, against recorded tolerances of 3.5e-2 and 0.13.
+ACHIEVED_BOUNDS = {"oracle_cfg5b_undiscounted.npz": {"A_diag": 1e-3, "B": 5e-2}}
+
 
 @pytest.mark.parametrize("name", sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz")))
 def test_against_committed_golden(name):
@@ -750,6 +844,8 @@ def test_against_committed_golden(name):
     # (tests/test_oracle.py re-measures it); never a lifted (infinite) one
     tol = {k: float(z[f"tol_{k}"]) if f"tol_{k}" in z.files else TOL for k in errs}
     assert all(np.isfinite(t) and t >= TOL for t in tol.values()), tol
+    for k, b in ACHIEVED_BOUNDS.get(name, {}).items():
+        tol[k] = min(tol[k], b)
     print("   achieved rel err " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
     print("   tolerance        " + " ".join(f"{k}:{tol[k]:.1e}" for k in errs), flush=True)
     assert all(np.isfinite(out[k]).all() for k in errs), f"{name}: non-finite output"

@@ -42,6 +42,8 @@ in half of the device memory available at forward time (free on the device plus
 held unallocated by torch's caching allocator), capped by
 ``TTC_LQR_STASH_MAX_BYTES`` if set) | ``always`` | ``never`` (the backward then
 recomputes it with one forward sweep).
+``TTC_LQR_STATUS_CHECK`` = ``sync`` (default) | ``deferred``: the default of ``status_check``
+(see :func:`hip_lqr_solve`).
 ``TTC_LQR_WORKSPACE_BYTES``: backward workspace per call (default: 16 GiB or half of the
 memory available at backward time, whichever is smaller; the library splits the tokens
 into passes that fit, and one pass is fastest).
@@ -59,6 +61,7 @@ from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BW
     FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
+           "check_deferred_status",
            "SUPPORTED_DIMS", "last_backward_stats"]
 
 SUPPORTED_DIMS = (16, 32, 64)
@@ -204,12 +207,60 @@ def _read_status(status, name: str) -> int:
         return int(status.item())
 
 
+# Status words of forwards run with status_check="deferred" that nothing has read yet.
+_deferred: list = []
+_DEFERRED_MAX = 1024  # pending words that trigger a check of all of them
+
+
+def _deferred_mode(status_check: str | None) -> bool:
+    mode = status_check or os.environ.get("TTC_LQR_STATUS_CHECK", "sync")
+    assert mode in ("sync", "deferred"), f"unknown status_check {mode}"
+    return mode == "deferred"
+
+
+def _defer(status):
+    """Keep a forward's device status word for a later check (no host synchronisation now)."""
+    if len(_deferred) >= _DEFERRED_MAX:
+        check_deferred_status()
+    _deferred.append(status)
+
+
+def _take_deferred(status) -> int:
+    """Read one deferred status word (the backward's own forward), raising the forward's error."""
+    for i, t in enumerate(_deferred):
+        if t is status:
+            del _deferred[i]
+            break
+    fst = _read_status(status, "bwd:ttc_lqr_forward_status")
+    if fst & _ERROR_BITS:
+        raise RuntimeError(_FWD_MSG)
+    return fst
+
+
+def check_deferred_status(keep: bool = False) -> None:
+    """Read the status words of the forwards run with ``status_check="deferred"`` that no backward
+    has read yet (one synchronisation), forget them (unless ``keep``), and raise the reference's
+    forward ``RuntimeError`` (``fused_lqr.py:101``) if any of those forwards met a non-finite value.
+    A forward in deferred mode enqueues its kernels and returns without waiting for them, so it can
+    be recorded by HIP graph capture; its error surfaces here, or in its backward.  A forward
+    captured in a graph registers its status word once, when it is captured, and every replay
+    rewrites that word: ``keep=True`` checks it after each replay without dropping it."""
+    pending = list(_deferred)
+    if not keep:
+        _deferred.clear()
+    bad = False
+    for t in pending:
+        bad |= bool(_read_status(t, "fwd:ttc_lqr_status") & _ERROR_BITS)
+    if bad:
+        raise RuntimeError(_FWD_MSG)
+
+
 class HipLQRSolveFunc(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T: int,
                 grad_limit: float = 1e6, stash: str | None = None, precision: str = "auto",
-                stable_backward: bool = False):
+                stable_backward: bool = False, status_check: str | None = None):
         ins = [A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0]
         assert all(x.is_cuda for x in ins), "hip LQR solver inputs must be on a GPU"
         bs, nh, d = A_diag.shape
@@ -250,18 +301,26 @@ class HipLQRSolveFunc(torch.autograd.Function):
                                         None if fws is None else fws.data_ptr(), fws_bytes, status.data_ptr(),
                                         _stream_handle(dev))
         check(rc, "ttc_lqr_forward_ws")
-        fst = _read_status(status, "fwd:ttc_lqr_status")
-        if fst & _ERROR_BITS:
-            raise RuntimeError(_FWD_MSG)
+        ctx.fwd_status = None
+        if _deferred_mode(status_check):  # read by the backward or check_deferred_status()
+            _defer(status)
+            ctx.fwd_status = status
+        else:
+            fst = _read_status(status, "fwd:ttc_lqr_status")
+            if fst & _ERROR_BITS:
+                raise RuntimeError(_FWD_MSG)
+            flags = backward_flags(flags, fst)
         if need_grad:
             ctx.save_for_backward(*f32, u, *([st] if st is not None else []))
         ctx.meta = (bs, nh, d, du, Dp, T, float(grad_limit), st is not None, [x.dtype for x in ins],
-                    backward_flags(flags, fst) | (FLAG_STABLE_BWD if stable_backward else 0))
+                    flags | (FLAG_STABLE_BWD if stable_backward else 0))
         return u[..., :du].to(out_dtype)
 
     @staticmethod
     def backward(ctx, d_u):
         bs, nh, d, du, Dp, T, grad_limit, has_stash, dtypes, flags = ctx.meta
+        if ctx.fwd_status is not None:  # deferred: the forward's status word, read now
+            flags = backward_flags(flags, _take_deferred(ctx.fwd_status))
         saved = ctx.saved_tensors
         f32 = list(saved[:9])
         u = saved[9]
@@ -302,14 +361,14 @@ class HipLQRSolveFunc(torch.autograd.Function):
         out = (g["A"][..., :d], g["B"][:, :d, :du], g["Q"][:, :d, :d], g["R"][..., :du], g["Qf"][:, :, :d, :d],
                g["lA"], g["lB"][..., :du], g["lQ"][..., :d], g["h0"][..., :d])
         out = tuple(o.to(dt) if need else None for o, dt, need in zip(out, dtypes, ctx.needs_input_grad[:9]))
-        return out + (None, None, None, None, None)
+        return out + (None, None, None, None, None, None)
 
 
 def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_diag: torch.Tensor,
                   Q_f: torch.Tensor, log_gamma_A: torch.Tensor, log_gamma_B: torch.Tensor,
                   log_gamma_Q: torch.Tensor, h0: torch.Tensor, T: int, inv_guard: bool = False, *,
                   grad_limit: float = 1e6, stash: str | None = None, precision: str = "auto",
-                  stable_backward: bool = False) -> torch.Tensor:
+                  stable_backward: bool = False, status_check: str | None = None) -> torch.Tensor:
     """First optimal action ``u [N,H,du]`` of every (token, head) LQR problem.
 
     Drop-in for the reference ``fused_lqr_solve`` (``fused_lqr.py:294-304``): the same ten
@@ -326,9 +385,14 @@ def hip_lqr_solve(A_diag: torch.Tensor, B: torch.Tensor, Q: torch.Tensor, R_inv_
     sweep; see ``riccati_flags``.
     ``stable_backward``: skip the certified Hamiltonian rollout and compute every
     problem's gradients with the stable path.
+    ``status_check``: ``"sync"`` (default; ``TTC_LQR_STATUS_CHECK`` overrides it) reads the device
+    status word after the forward's kernels and raises at once, as the reference does
+    (``fused_lqr.py:99-110``); ``"deferred"`` returns without waiting for the kernels (no host
+    synchronisation in the forward, so it can be recorded by HIP graph capture) and raises the same
+    ``RuntimeError`` from the backward or from :func:`check_deferred_status`.
     """
     return HipLQRSolveFunc.apply(A_diag, B, Q, R_inv_diag, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, T,
-                                 grad_limit, stash, precision, stable_backward)
+                                 grad_limit, stash, precision, stable_backward, status_check)
 
 
 def _workspace_budget(dev) -> int:
@@ -370,7 +434,8 @@ class HipLQRFactoredFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0,
                 B_basis, Q_basis, T: int, grad_limit: float = 1e6, stash: str | None = None,
-                precision: str = "auto", stable_backward: bool = False, rescale: str = "none"):
+                precision: str = "auto", stable_backward: bool = False, rescale: str = "none",
+                status_check: str | None = None):
         ins = [A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q, h0,
                B_basis, Q_basis]
         assert rescale in _RESCALE_MODES, f"Unknown rescale method {rescale}"
@@ -440,18 +505,26 @@ class HipLQRFactoredFunc(torch.autograd.Function):
                 rc = lib.ttc_lqr_rescale(u.data_ptr(), xs[8].data_ptr(), bs, nh, Dp, Dp, mode, y.data_ptr(),
                                          _stream_handle(dev))
             check(rc, "ttc_lqr_rescale")
-        fst = _read_status(status, "fwd:ttc_lqr_status")
-        if fst & _ERROR_BITS:
-            raise RuntimeError(_FWD_MSG)
+        ctx.fwd_status = None
+        if _deferred_mode(status_check):  # read by the backward or check_deferred_status()
+            _defer(status)
+            ctx.fwd_status = status
+        else:
+            fst = _read_status(status, "fwd:ttc_lqr_status")
+            if fst & _ERROR_BITS:
+                raise RuntimeError(_FWD_MSG)
+            flags = backward_flags(flags, fst)
         if need_grad:
             ctx.save_for_backward(*xs, u, *([st] if st is not None else []))
         ctx.meta = (bs, nh, d, du, Dp, rb, rq, T, float(grad_limit), st is not None, [x.dtype for x in ins],
-                    backward_flags(flags, fst) | (FLAG_STABLE_BWD if stable_backward else 0), bf16, mode)
+                    flags | (FLAG_STABLE_BWD if stable_backward else 0), bf16, mode)
         return y[..., :du].to(out_dtype)
 
     @staticmethod
     def backward(ctx, d_u):
         bs, nh, d, du, Dp, rb, rq, T, grad_limit, has_stash, dtypes, flags, bf16, mode = ctx.meta
+        if ctx.fwd_status is not None:  # deferred: the forward's status word, read now
+            flags = backward_flags(flags, _take_deferred(ctx.fwd_status))
         saved = ctx.saved_tensors
         xs = list(saved[:11])
         u = saved[11]
@@ -492,16 +565,16 @@ class HipLQRFactoredFunc(torch.autograd.Function):
         out = (g[0][..., :d], g[1], g[2], g[3][..., :du], g[4], g[5], g[6][..., :du], g[7][..., :d],
                g[8][..., :d], g[9][:, :d, :du], g[10][:, :d, :d])
         out = tuple(o.to(dt) if need else None for o, dt, need in zip(out, dtypes, ctx.needs_input_grad[:11]))
-        return out + (None, None, None, None, None, None)
+        return out + (None, None, None, None, None, None, None)
 
 
 def hip_lqr_solve_factored(A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B, log_gamma_Q,
                            h0, B_basis, Q_basis, T: int, grad_limit: float = 1e6, stash: str | None = None,
                            precision: str = "auto", stable_backward: bool = False,
-                           rescale: str = "none") -> torch.Tensor:
+                           rescale: str = "none", status_check: str | None = None) -> torch.Tensor:
     """``hip_lqr_solve`` on the layer's low-rank factors (see :class:`HipLQRFactoredFunc`):
     equal to ``hip_lqr_solve(A_diag, einsum(coeff_B, B_basis), einsum(coeff_Q, Q_basis), R_inv,
     einsum(coeff_Qf, Q_basis), ...)`` with gradients for the coefficients and both bases."""
     return HipLQRFactoredFunc.apply(A_diag, coeff_B, coeff_Q, R_inv_diag, coeff_Qf, log_gamma_A, log_gamma_B,
                                     log_gamma_Q, h0, B_basis, Q_basis, T, grad_limit, stash, precision,
-                                    stable_backward, rescale)
+                                    stable_backward, rescale, status_check)
