@@ -65,9 +65,10 @@ int launch_gains64_d16(const float* A, const float* B, const float* Q, const flo
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* kst, float* q0s, int32_t* status, hipStream_t s) {
   if (P <= 0) return TTC_LQR_OK;
-  const int64_t batches = (P + 3) / 4;
+  // as many waves as fit at once, up to one per problem: the kernel then takes ceil(P / waves)
+  // problems per wave (at most four), so a pass shorter than four per wave runs fewer per wave
   const int64_t res = resident_waves64<STASH_GAINS, false, false>();
-  const int64_t waves = batches < res ? batches : res;
+  const int64_t waves = P < res ? P : res;
   hipLaunchKernelGGL((lqr_fwd64_mfma_kernel<STASH_GAINS, false, false>), dim3((unsigned)waves), dim3(64),
                      M64::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, nullptr, kst, q0s, status, nullptr);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
