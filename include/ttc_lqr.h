@@ -185,9 +185,12 @@ int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, cons
  * Fast path: a Hamiltonian rollout per problem (the reference's fused backward,
  * symplectic_iter.py:542-885) with a terminal certificate (TTC_LQR_CERT_TOL); problems
  * that fail it are recomputed by the stable path (gains stored per step in the
- * workspace, closed-loop costates).  *n_fallback (host, may be NULL) receives the
- * number of problems that took the stable path.  Reading that count synchronises
- * `stream` once per token chunk.
+ * workspace, closed-loop costates).  With heads % 8 == 0 the rollout runs over head
+ * groups of 8 in fp32; under TTC_LQR_FLAG_FP64_RICCATI / _FP64_RESCUE the problems of
+ * the groups it rejects are rolled again one by one in fp64 before any reaches the
+ * stable path.  *n_fallback (host, may be NULL) receives the number of problems that
+ * took the stable path.  Reading the rejected counts synchronises `stream` once per
+ * token chunk (twice with the fp64 second rollout).
  * grad_B / grad_Q are summed over heads (B and Q are head-shared).
  * workspace_bytes must be at least ttc_lqr_workspace_bytes(1, ...); larger workspaces
  * give fewer, larger passes.  grad_limit: |g| >= grad_limit sets TTC_LQR_STATUS_LARGE

@@ -290,6 +290,39 @@ def test_config5_stress(cfg, T, seed):
     check_case(f"cfg{cfg}", layer_solver_inputs(cfg, x), T, grad_limit=math.inf)
 
 
+@pytest.mark.parametrize("H", [8, 16])
+def test_long_horizon_two_tier_rollout(H, monkeypatch):
+    """T = 1024, heads % 8 == 0 (TTC_LQR_FLAG_FP64_RESCUE): the backward rolls head groups of 8
+    in fp32 on the matrix cores, rolls the problems of the groups that rejects again one by one
+    in fp64 on the row layout, and sends only what that rejects to the stable path.  The same
+    forward under TTC_LQR_FLAG_FP64_FALLBACK sends every rejected group whole to the stable path
+    (its count is 8 x the rejected groups), so the two-tier count lies strictly between 0 and it
+    when all three tiers run.  Both agree with the fp64 oracle: one group per token (H = 8, head
+    sums written directly) and two (H = 16: group sums from the per-problem partials of the second
+    tier and the stable path, then head sums)."""
+    import ttc.solvers.hip_lqr as hl
+    from ttc.solvers._lib import FLAG_FP64_FALLBACK
+    ins = layer_solver_inputs(5, make_x(5, n_tokens=16 * H // 8, seed=31))
+    if H != 8:
+        ins = _regroup_heads(ins, H)
+    T = 1024
+    pb = LQRProblem(*ins, T)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(9)).double().numpy()
+    ref = solve_grads(pb, dU)
+    print(f"[two-tier H={H}] N={pb.N} T={T}", flush=True)
+    tiers = run_hip(ins, T, dU, grad_limit=math.inf)
+    monkeypatch.setattr(hl, "riccati_flags", lambda precision, T_, Dp: FLAG_FP64_FALLBACK)
+    groups = run_hip(ins, T, dU, grad_limit=math.inf)
+    print(f"   stable path: two tiers {tiers['_fallback']}, whole groups {groups['_fallback']} of {pb.P}",
+          flush=True)
+    assert groups["_fallback"] % 8 == 0
+    assert 0 < tiers["_fallback"] < groups["_fallback"]
+    for label, out in (("two tiers", tiers), ("whole groups", groups)):
+        errs = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
+        print(f"   {label}: " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+        assert all(v <= TOL for v in errs.values()), (label, errs)
+
+
 @pytest.mark.parametrize("cfg,n_tok", [(5, 64), ("5b", 64)])
 def test_forward_workspace_packs_the_fp64_rescue(cfg, n_tok):
     """Long horizons (T = 1024, FP64_RESCUE): ttc_lqr_forward_ws lists the problems the

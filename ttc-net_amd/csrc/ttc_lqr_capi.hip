@@ -129,6 +129,39 @@ __global__ void scatter_group_kernel(const int* __restrict__ list, int64_t base,
   copy_span(gQg + o * d * d, c.gQ + i * d * d, d * d);
 }
 
+// Problems of the listed head groups (8 per group, chunk-local indices) for the second tier.
+__global__ void expand_groups_kernel(const int* __restrict__ glist, int64_t ngroups, int* __restrict__ plist) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < ngroups * 8) plist[e] = glist[e / 8] * 8 + (int)(e % 8);
+}
+
+// grad_B / grad_Q of the listed head groups as the sums of their eight problems' partials
+// (part, at the problems' own indices) into the group's slot of out -- the token's output when
+// H == 8, checked against the guard there (status non-null).
+__global__ void groupsum_kernel(const int* __restrict__ glist, int64_t ngroups, const float* __restrict__ part,
+                                int DD, float* __restrict__ out, float grad_limit, int* __restrict__ status) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= ngroups * DD) return;
+  const int64_t G = glist[e / DD];
+  const int r = (int)(e % DD);
+  float s = 0.f;
+  for (int k = 0; k < 8; ++k) s += part[(G * 8 + k) * DD + r];
+  out[G * DD + r] = s;
+  if (status != nullptr) {
+    if (!isfinite(s)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
+    else if (fabsf(s) >= grad_limit) atomicOr(status, TTC_LQR_STATUS_LARGE);
+  }
+}
+
+static int launch_groupsum(const int32_t* glist, int64_t ngroups, const float* part, int DD, float* out,
+                           float limit, int32_t* status, hipStream_t s) {
+  const int64_t total = ngroups * DD;
+  if (total <= 0) return TTC_LQR_OK;
+  hipLaunchKernelGGL(groupsum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, glist, ngroups, part,
+                     DD, out, limit, status);
+  return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+}
+
 static int launch_headsum(const float* part, int64_t N, int H, int DD, float* out, float limit, int32_t* status,
                           hipStream_t s) {
   const int64_t total = N * DD;
@@ -308,28 +341,32 @@ static int64_t fp64_round_problems(int d) {
 constexpr size_t kFallbackReserve = (size_t)256 << 20;
 
 struct FastLayout {
-  size_t v1, q0, gBp, gQp, list, cnt, fb, total;
+  size_t v1, q0, gBp, gQp, gBg, gQg, list, glist, plist, cnt, fb, total;
   int64_t F;  // fallback capacity within the reserve
 };
 
-// The fast path rolls head groups of 8 on the matrix cores (fp32, H % 8 == 0), else one
-// problem per row-layout pass (fp32 or, for the long-horizon flags, fp64).
+// The fast path rolls head groups of 8 on the matrix cores in fp32 (H % 8 == 0), else one
+// problem per row-layout rollout (fp32, or fp64 under the long-horizon flags).
 static bool head_group_path(int H, int flags, int d) {
-  return H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL) && !fp64_rollout(flags, d);
+  (void)d;
+  return H % 8 == 0 && !(flags & TTC_LQR_FLAG_ROW_KERNEL);
 }
 
-// Its partial grad_B / grad_Q sums per token, added up by the head sum: none when a head group
-// is the whole token (the group writes the outputs), one per head group, one per problem on
-// the row-layout path.
-static int64_t bq_parts_per_token(int H, int flags, int d) {
-  if (head_group_path(H, flags, d)) return H == 8 ? 0 : H / 8;
-  return H;
-}
+// Under the long-horizon flags the head-group rollout is the first of two tiers: the problems
+// of the groups it rejects are rolled again one by one in fp64 on the row layout, and only
+// those that rollout rejects take the stable path.
+static bool two_tier_path(int H, int flags, int d) { return head_group_path(H, flags, d) && fp64_rollout(flags, d); }
 
 static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash, int flags) {
   const bool fp64 = fp64_stable(flags, d);
+  const bool groups = head_group_path(H, flags, d);
+  const bool tiers = two_tier_path(H, flags, d);
   const size_t Pc = (size_t)chunk_tokens * (size_t)H;
-  const size_t parts = (size_t)chunk_tokens * (size_t)bq_parts_per_token(H, flags, d);
+  // partial grad_B / grad_Q sums, added up per token by the head sum: one per problem of the
+  // row-layout rollouts (per problem index; under two tiers for the second tier's problems),
+  // one per head group (none when a group is the whole token: it writes the outputs)
+  const size_t gparts = groups ? (size_t)chunk_tokens * (size_t)(H == 8 ? 0 : H / 8) : 0;
+  const size_t parts = (!groups || tiers) ? Pc : 0;
   FastLayout L{};
   size_t off = 0;
   L.v1 = off;
@@ -340,9 +377,17 @@ static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T,
   off += align256(parts * (size_t)d * du * sizeof(float));
   L.gQp = off;
   off += align256(parts * (size_t)d * d * sizeof(float));
+  L.gBg = off;
+  off += align256(gparts * (size_t)d * du * sizeof(float));
+  L.gQg = off;
+  off += align256(gparts * (size_t)d * d * sizeof(float));
   L.list = off;
   off += align256(Pc * sizeof(int32_t));
-  L.cnt = off;
+  L.glist = off;
+  off += tiers ? align256(Pc / 8 * sizeof(int32_t)) : 0;
+  L.plist = off;
+  off += tiers ? align256(Pc * sizeof(int32_t)) : 0;
+  L.cnt = off;  // [0]: rejected problems (or groups), [1]: the second tier's rejected problems
   off += 256;
   L.fb = off;
   const int64_t cap = fallback_capacity(kFallbackReserve, d, du, T, fp64);
@@ -438,39 +483,95 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
     hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
-    // long horizons in fp64 (fp64 flags): the rollout per problem in fp64 on the row layout, which
-    // accepts far more of their problems than the fp32 head-group rollout (a rejected group is
-    // recomputed whole by the stable path, each pass of which is a serial T-step sweep)
+    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt + 1, 0);
+    // a device count the host needs: one stream synchronisation
+    auto read_count = [&](const int32_t* c, int64_t cap, int32_t& v) -> int {
+      v = 0;
+      if (hipMemcpyAsync(&v, c, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;
+      if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
+      return (v < 0 || v > cap) ? TTC_LQR_ELAUNCH : TTC_LQR_OK;
+    };
+    // the listed problems (nfail) recomputed by the stable path in passes of Frun, their
+    // outputs and grad_B / grad_Q partials scattered to their own problem indices
+    auto stable_problems = [&](int32_t nfail) -> int {
+      const Compact c = compact_at(ws + L.fb, Frun, d, du);
+      for (int64_t f0 = 0; f0 < nfail; f0 += Frun) {
+        const int64_t fc = (f0 + Frun <= nfail) ? Frun : (nfail - f0);
+        hipLaunchKernelGGL(gather_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q, r, qf, la,
+                           lb, lq, hz, dz, c);
+        if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+        const int rs = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags,
+                                       c.gA, c.gB, c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable,
+                                       workspace_bytes - fb_stable, grad_limit, INFINITY, status,
+                                       s);  // per-problem partials
+        if (rs != TTC_LQR_OK) return rs;
+        hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
+                           glB, glQ, gh, gBp, gQp);
+        if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+      }
+      return TTC_LQR_OK;
+    };
     if (head_group_path(H, flags, d)) {
-      // head groups of 8 on the matrix cores: grad_B / grad_Q summed inside the kernel
+      // head groups of 8 on the matrix cores in fp32: grad_B / grad_Q summed inside the kernel
       // (straight into the outputs when a group is a token, H == 8)
       const bool direct = H == 8;
-      float* gBg = direct ? grad_B + n0 * dd : gBp;
-      float* gQg = direct ? grad_Q + n0 * dd : gQp;
+      const bool tiers = two_tier_path(H, flags, d);
+      float* gBg = direct ? grad_B + n0 * dd : reinterpret_cast<float*>(ws + L.gBg);
+      float* gQg = direct ? grad_Q + n0 * dd : reinterpret_cast<float*>(ws + L.gQg);
+      int32_t* glist = tiers ? reinterpret_cast<int32_t*>(ws + L.glist) : list;
       auto* launch = d == 16 ? launch_ham16_mfma : (d == 32 ? launch_ham32_mfma : launch_ham64_mfma);
       rc = launch(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, Pc, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBg,
-                  gQg, grad_limit, list, cnt, status, s);
+                  gQg, grad_limit, glist, cnt, status, s);
       if (rc != TTC_LQR_OK) return rc;
       int32_t nfail = 0;
-      if (hipMemcpyAsync(&nfail, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;
-      if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
-      if (nfail < 0 || nfail > Pc / 8) return TTC_LQR_ELAUNCH;
-      total_fb += 8 * (int64_t)nfail;
-      const Compact c = compact_at(ws + L.fb, Frun, d, du);
-      const int64_t Fg = Frun / 8;  // groups per fallback batch
-      for (int64_t f0 = 0; f0 < nfail; f0 += Fg) {
-        const int64_t fc = (f0 + Fg <= nfail) ? Fg : (nfail - f0);
-        hipLaunchKernelGGL(gather_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q,
-                           r, qf, la, lb, lq, hz, dz, c);
-        if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
-        // a group's sums are the token's head sums only when H == 8
-        rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 8, d, T, flags, c.gA, c.gB,
-                             c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable, workspace_bytes - fb_stable,
-                             grad_limit, direct ? grad_limit : INFINITY, status, s);
-        if (rc != TTC_LQR_OK) return rc;
-        hipLaunchKernelGGL(scatter_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, c, gA, gR,
-                           gQf, glA, glB, glQ, gh, gBg, gQg);
-        if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+      rc = read_count(cnt, Pc / 8, nfail);
+      if (rc != TTC_LQR_OK) return rc;
+      if (tiers) {
+        // long horizons: the problems of the rejected groups rolled again one by one in fp64 on
+        // the row layout (which accepts most of them), the rest by the stable path, and the
+        // groups' grad_B / grad_Q summed from the per-problem partials of the two
+        if (nfail > 0) {
+          int32_t* plist = reinterpret_cast<int32_t*>(ws + L.plist);
+          const int64_t np = 8 * (int64_t)nfail;
+          hipLaunchKernelGGL(expand_groups_kernel, dim3((unsigned)((np + 255) / 256)), dim3(256), 0, s, glist,
+                             (int64_t)nfail, plist);
+          if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+          switch (d) {
+            case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist); break;
+            case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist); break;
+            default: return TTC_LQR_EUNSUPPORTED;
+          }
+          if (rc != TTC_LQR_OK) return rc;
+          int32_t nfail2 = 0;
+          rc = read_count(cnt + 1, np, nfail2);
+          if (rc != TTC_LQR_OK) return rc;
+          total_fb += nfail2;
+          rc = stable_problems(nfail2);
+          if (rc != TTC_LQR_OK) return rc;
+          rc = launch_groupsum(glist, nfail, gBp, (int)(d * du), gBg, grad_limit, direct ? status : nullptr, s);
+          if (rc != TTC_LQR_OK) return rc;
+          rc = launch_groupsum(glist, nfail, gQp, (int)dd, gQg, grad_limit, direct ? status : nullptr, s);
+          if (rc != TTC_LQR_OK) return rc;
+        }
+      } else {
+        // a rejected group is recomputed whole by the stable path, gathered as a compact 8-head token
+        total_fb += 8 * (int64_t)nfail;
+        const Compact c = compact_at(ws + L.fb, Frun, d, du);
+        const int64_t Fg = Frun / 8;  // groups per fallback batch
+        for (int64_t f0 = 0; f0 < nfail; f0 += Fg) {
+          const int64_t fc = (f0 + Fg <= nfail) ? Fg : (nfail - f0);
+          hipLaunchKernelGGL(gather_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q,
+                             r, qf, la, lb, lq, hz, dz, c);
+          if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+          // a group's sums are the token's head sums only when H == 8
+          rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 8, d, T, flags, c.gA, c.gB,
+                               c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable,
+                               workspace_bytes - fb_stable, grad_limit, direct ? grad_limit : INFINITY, status, s);
+          if (rc != TTC_LQR_OK) return rc;
+          hipLaunchKernelGGL(scatter_group_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, c, gA,
+                             gR, gQf, glA, glB, glQ, gh, gBg, gQg);
+          if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+        }
       }
       if (!direct) {
         rc = launch_headsum(gBg, nc, H / 8, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
@@ -489,24 +590,11 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     if (rc != TTC_LQR_OK) return rc;
     // how many problems the certificate rejected (one stream synchronisation per chunk)
     int32_t nfail = 0;
-    if (hipMemcpyAsync(&nfail, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess) return TTC_LQR_ELAUNCH;
-    if (hipStreamSynchronize(s) != hipSuccess) return TTC_LQR_ELAUNCH;
-    if (nfail < 0 || nfail > Pc) return TTC_LQR_ELAUNCH;
+    rc = read_count(cnt, Pc, nfail);
+    if (rc != TTC_LQR_OK) return rc;
     total_fb += nfail;
-    const Compact c = compact_at(ws + L.fb, Frun, d, du);
-    for (int64_t f0 = 0; f0 < nfail; f0 += Frun) {
-      const int64_t fc = (f0 + Frun <= nfail) ? Frun : (nfail - f0);
-      hipLaunchKernelGGL(gather_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q, r, qf, la,
-                         lb, lq, hz, dz, c);
-      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
-      rc = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags, c.gA, c.gB,
-                           c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable,
-                           workspace_bytes - fb_stable, grad_limit, INFINITY, status, s);  // per-problem partials
-      if (rc != TTC_LQR_OK) return rc;
-      hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
-                         glB, glQ, gh, gBp, gQp);
-      if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
-    }
+    rc = stable_problems(nfail);
+    if (rc != TTC_LQR_OK) return rc;
     rc = launch_headsum(gBp, nc, H, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
     if (rc != TTC_LQR_OK) return rc;
     rc = launch_headsum(gQp, nc, H, (int)dd, grad_Q + n0 * dd, grad_limit, status, s);

@@ -45,12 +45,12 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s, bool fp64) {
+                  hipStream_t s, bool fp64, const int32_t* plist) {
   if (fp64)
     return launch_ham<16, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
-                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist);
   return launch_ham<16>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
-                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist);
 }
 
 }  // namespace ttc

@@ -31,10 +31,10 @@ int launch_ham_d64(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s, bool fp64) {
+                  hipStream_t s, bool fp64, const int32_t* plist) {
   if (fp64) return TTC_LQR_EUNSUPPORTED;  // no fp64 kernels at d = 64
   return launch_ham<64>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
-                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s);
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist);
 }
 
 }  // namespace ttc

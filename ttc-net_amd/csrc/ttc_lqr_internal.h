@@ -54,7 +54,7 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s, bool fp64);
+                  hipStream_t s, bool fp64, const int32_t* plist = nullptr);
 int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
@@ -69,7 +69,7 @@ int launch_ham_d32(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s, bool fp64);
+                  hipStream_t s, bool fp64, const int32_t* plist = nullptr);
 int launch_fwd_d64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
@@ -84,7 +84,7 @@ int launch_ham_d64(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s, bool fp64);
+                  hipStream_t s, bool fp64, const int32_t* plist = nullptr);
 // d = 16 Hamiltonian backward on the matrix cores over head groups of 8 (H % 8 == 0):
 // writes the group sums of grad_B / grad_Q to gBg / gQg ([P/8, 16, 16]; when H == 8 a group
 // is a token and gBg / gQg may be the final outputs) and lists rejected groups.

@@ -847,11 +847,15 @@ __device__ __forceinline__ double rcpr(double x) { return 1.0 / x; }
 // appended to fail_list (chunk-local index); the caller recomputes it with the
 // stable path (stored gains, closed-loop costates).  grad_B / grad_Q partials go to
 // gBp / gQp for headsum_kernel, as in lqr_bwd_kernel.
+// LISTED == false: problems 0..P-1; LISTED: the P chunk-local problem indices plist[0..P-1] (the
+// problems of head groups another rollout rejected).  Every output, partial and fail_list
+// entry is then at the listed problem's own index, and each problem reads its token's B
+// from global memory instead of the block's LDS copy.
 // ---------------------------------------------------------------------------
 #ifndef TTC_HAM64_WAVES
 #define TTC_HAM64_WAVES 2  // waves per SIMD of the fp64 rollout (registers capped; its loop keeps them all)
 #endif
-template <int D, typename R = float>
+template <int D, typename R = float, bool LISTED = false>
 __global__ __launch_bounds__(Geo<D>::THREADS)
 __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WAVES : 1))) void lqr_ham_bwd_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
@@ -861,19 +865,22 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
     const float* __restrict__ q0s, int64_t P, int H, int T, int ntok_lds, float tau, float* __restrict__ gA,
     float* __restrict__ gRinv, float* __restrict__ gQf, float* __restrict__ glgA, float* __restrict__ glgB,
     float* __restrict__ glgQ, float* __restrict__ gh0, float* __restrict__ gBp, float* __restrict__ gQp,
-    float grad_limit, int* __restrict__ fail_list, int* __restrict__ fail_count, int* __restrict__ status) {
+    float grad_limit, int* __restrict__ fail_list, int* __restrict__ fail_count, int* __restrict__ status,
+    const int* __restrict__ plist) {
   using G = Geo<D>;
   extern __shared__ __align__(16) float smem_f[];
   R* const smem = reinterpret_cast<R*>(smem_f);
   const int li = threadIdx.x % D;
   const int pb = threadIdx.x / D;
   const int64_t p0 = (int64_t)blockIdx.x * G::PPB;
-  int64_t p = p0 + pb;
-  const bool valid = p < P;
-  if (!valid) p = P - 1;  // idle lanes recompute a real problem, never store
+  const int64_t slot = p0 + pb;
+  const bool valid = slot < P;
+  // idle lanes recompute a real problem, never store
+  int64_t p = valid ? slot : P - 1;
+  if constexpr (LISTED) p = plist[p];
   const int64_t n = p / H;
   const int64_t n0 = p0 / H;
-  {
+  if constexpr (!LISTED) {
     const int64_t plast = (p0 + G::PPB - 1 < P) ? (p0 + G::PPB - 1) : (P - 1);
     const int ntok = (int)(plast / H - n0 + 1);
     for (int e = threadIdx.x; e < ntok * D * D; e += G::THREADS) {
@@ -882,7 +889,6 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
     }
   }
   __syncthreads();
-  const R* Bs = smem + (int)(n - n0) * G::MAT;
   R* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
   R* v0 = S + G::MAT;  // 6 vectors of D floats, then the pivot row
   R* v1 = v0 + D;
@@ -904,12 +910,23 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
   R Brow[D], Bcol[D], Qrow[D];
   {
     const float* qg = Qg + n * D * D;
+    if constexpr (!LISTED) {
+      const R* Bs = smem + (int)(n - n0) * G::MAT;
 #pragma unroll
-    for (int c = 0; c < D; ++c) {
-      Brow[c] = Bs[li * G::LDM + c];
-      Bcol[c] = Bs[c * G::LDM + li];
-      Qrow[c] = R(0.5) * (qg[li * D + c] + qg[c * D + li]);
+      for (int c = 0; c < D; ++c) {
+        Brow[c] = Bs[li * G::LDM + c];
+        Bcol[c] = Bs[c * G::LDM + li];
+      }
+    } else {
+      const float* bg = Bg + n * D * D;
+#pragma unroll
+      for (int c = 0; c < D; ++c) {
+        Brow[c] = bg[li * D + c];
+        Bcol[c] = bg[c * D + li];
+      }
     }
+#pragma unroll
+    for (int c = 0; c < D; ++c) Qrow[c] = R(0.5) * (qg[li * D + c] + qg[c * D + li]);
   }
 
   // t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (pivoted elimination)
@@ -1388,13 +1405,17 @@ inline int launch_ham(const float* A, const float* B, const float* Q, const floa
                       const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                       float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                       float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                      hipStream_t s) {
+                      hipStream_t s, const int32_t* plist = nullptr) {
   if (P <= 0) return TTC_LQR_OK;
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
-  hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf, lA, lB,
-                     lQ, h0, u0,
-                     dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB, glQ, gh0, gBp, gQp,
-                     limit, fail_list, fail_count, status);
+  if (plist != nullptr)
+    hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT, true>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf,
+                       lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB, glQ,
+                       gh0, gBp, gQp, limit, fail_list, fail_count, status, plist);
+  else
+    hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT, false>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R,
+                       Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB,
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, plist);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
