@@ -20,7 +20,7 @@
  *     unchanged).  Anything else returns TTC_LQR_EUNSUPPORTED.
  *   - Nothing here allocates device memory or throws.  All work is enqueued on
  *     `stream` (a hipStream_t, NULL = default stream); only ttc_lqr_backward
- *     synchronises it (once per token chunk, to size its fallback).
+ *     synchronises it (once or twice per token chunk, to size its fallback).
  *   - `status` (device int32, caller-zeroed, may be NULL) receives bit flags:
  *     TTC_LQR_STATUS_NONFINITE if any output is NaN/Inf, TTC_LQR_STATUS_LARGE if
  *     a gradient has |g| >= grad_limit.  The caller reads it after the stream
