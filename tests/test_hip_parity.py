@@ -290,8 +290,8 @@ def test_config5_stress(cfg, T, seed):
     check_case(f"cfg{cfg}", layer_solver_inputs(cfg, x), T, grad_limit=math.inf)
 
 
-@pytest.mark.parametrize("H", [8, 16])
-def test_long_horizon_two_tier_rollout(H, monkeypatch):
+@pytest.mark.parametrize("d,H", [(16, 8), (16, 16), (32, 8)])
+def test_long_horizon_two_tier_rollout(d, H, monkeypatch):
     """T = 1024, heads % 8 == 0 (TTC_LQR_FLAG_FP64_RESCUE): the backward rolls head groups of 8
     in fp32 on the matrix cores, rolls the problems of the groups that rejects again one by one
     in fp64 on the row layout, and sends only what that rejects to the stable path.  The same
@@ -299,17 +299,20 @@ def test_long_horizon_two_tier_rollout(H, monkeypatch):
     (its count is 8 x the rejected groups), so the two-tier count lies strictly between 0 and it
     when all three tiers run.  Both agree with the fp64 oracle: one group per token (H = 8, head
     sums written directly) and two (H = 16: group sums from the per-problem partials of the second
-    tier and the stable path, then head sums)."""
+    tier and the stable path, then head sums).  d = 32: the config-5 problems zero-padded to
+    d = 24 (an equivalent problem; the solver pads it to its d = 32 kernels)."""
     import ttc.solvers.hip_lqr as hl
     from ttc.solvers._lib import FLAG_FP64_FALLBACK
     ins = layer_solver_inputs(5, make_x(5, n_tokens=16 * H // 8, seed=31))
     if H != 8:
         ins = _regroup_heads(ins, H)
+    if d != 16:
+        ins = [t.float() for t in hl._pad_inputs([t.double() for t in ins], 16, 16, 24)]
     T = 1024
     pb = LQRProblem(*ins, T)
     dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(9)).double().numpy()
     ref = solve_grads(pb, dU)
-    print(f"[two-tier H={H}] N={pb.N} T={T}", flush=True)
+    print(f"[two-tier d={d} H={H}] N={pb.N} T={T}", flush=True)
     tiers = run_hip(ins, T, dU, grad_limit=math.inf)
     monkeypatch.setattr(hl, "riccati_flags", lambda precision, T_, Dp: FLAG_FP64_FALLBACK)
     groups = run_hip(ins, T, dU, grad_limit=math.inf)
