@@ -402,9 +402,14 @@ def _workspace_budget(dev) -> int:
 def _workspace_bytes(full: int, floor: int, dev) -> int:
     """Bytes of a call's workspace: ``full`` (one pass) when the budget allows, else the budget,
     at least ``floor`` (one token's worth).  The default budget is never below 1 GiB, so a
-    smaller ``full`` skips the device memory query."""
-    if full <= 1 << 30 and not os.environ.get("TTC_LQR_WORKSPACE_BYTES"):
-        return max(full, floor, 256)
+    smaller ``full`` skips the device memory query; up to 16 GiB and half the device's free
+    memory (one driver query) ``full`` is within the budget too, which then need not read
+    torch's allocator counters (hundreds of microseconds per call)."""
+    if not os.environ.get("TTC_LQR_WORKSPACE_BYTES"):
+        if full <= 1 << 30:
+            return max(full, floor, 256)
+        if full <= 16 << 30 and full <= torch.cuda.mem_get_info(dev)[0] // 2:
+            return max(full, floor, 256)
     return max(min(full, _workspace_budget(dev)), floor, 256)
 
 
