@@ -338,6 +338,32 @@ def _note(msg):
         print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def einsum_step_ms(ins_f, d_u, T, steps, warmup, grad_limit=1e6):
+    """fwd+bwd wall time of the layer's other route from the same eleven factored inputs: B, Q and
+    Q_f materialised by torch einsums (as the reference layer does, `ttc_layer.py:117-123`) and
+    solved on them, gradients through the einsums by autograd."""
+    import torch
+    from ttc.solvers.hip_lqr import hip_lqr_solve
+    xs = [t.clone().requires_grad_(True) for t in ins_f]
+
+    def step():
+        A, cB, cQ, R, cQf, lA, lB, lQ, h0, Bb, Qb = xs
+        B = torch.einsum("nr,rij->nij", cB, Bb)
+        Q = torch.einsum("nr,rij->nij", cQ, Qb)
+        Qf = torch.einsum("nhr,rij->nhij", cQf, Qb)
+        u = hip_lqr_solve(A, B, Q, R, Qf, lA, lB, lQ, h0, T, grad_limit=grad_limit)
+        return torch.autograd.grad(u, xs, d_u)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
 def time_solver(ins, d_u, T, steps, warmup, stash=None, fwd_only=False, grad_limit=1e6, solver_kw=None):
     """Forward: mean per-call GPU time from HIP events on the launch stream.  fwd+bwd: wall
     time of `steps` steps between two device synchronisations, and the peak device memory the
@@ -583,7 +609,10 @@ def main():
         out["factored"] = {"fwd_ms": rf["fwd_ms"], "fwd_bwd_ms": rf["step_ms"],
                            "fwd_bwd_solves_per_s": P / (rf["step_ms"] * 1e-3),
                            "peak_mem_bytes_fwd_bwd": rf["peak_mem_bytes"],
-                           "input_bytes_per_problem": 4 * (5 * d + 1 + (c["b_rank"] + c["q_rank"]) / H + c["q_rank"])}
+                           "input_bytes_per_problem": 4 * (5 * d + 1 + (c["b_rank"] + c["q_rank"]) / H + c["q_rank"]),
+                           # the same step with B / Q / Q_f materialised by torch einsums instead
+                           "torch_einsum_materialised_fwd_bwd_ms": einsum_step_ms(
+                               ins_f, du_f, T, 3, 1, grad_limit=c.get("grad_limit", 1e6))}
         del ins_f, du_f
         torch.cuda.empty_cache()
     if args.config == "2" and not args.no_full_size:

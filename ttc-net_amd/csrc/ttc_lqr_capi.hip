@@ -907,13 +907,11 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
     if (rc != TTC_LQR_OK) return rc;
     total_fb += nfb;
     // chain rule of the expansion: coefficient gradients, then the basis sums
-    rc = launch_project(gB, nc, Eb, Bs, rb, gcB, s);
-    if (rc == TTC_LQR_OK) rc = launch_project(gQ, nc, Eq, Gs, rq, gcQ, s);
-    if (rc == TTC_LQR_OK) rc = launch_project(gQf, Pc, Eq, Gs, rq, gcQf, s);
+    // (each gradient read once where launch_project_reduce fuses the two)
     const int first = n0 == 0 ? 0 : 1;
-    if (rc == TTC_LQR_OK) rc = launch_reduce(cB, nc, rb, gB, Eb, part, gBs, first, s);
-    if (rc == TTC_LQR_OK) rc = launch_reduce(cQ, nc, rq, gQ, Eq, part, gGs, first, s);
-    if (rc == TTC_LQR_OK) rc = launch_reduce(cQf, Pc, rq, gQf, Eq, part, gGs, 1, s);
+    rc = launch_project_reduce(cB, nc, rb, gB, Eb, Bs, gcB, part, gBs, first, s);
+    if (rc == TTC_LQR_OK) rc = launch_project_reduce(cQ, nc, rq, gQ, Eq, Gs, gcQ, part, gGs, first, s);
+    if (rc == TTC_LQR_OK) rc = launch_project_reduce(cQf, Pc, rq, gQf, Eq, Gs, gcQf, part, gGs, 1, s);
     St::flush(grad_A_diag, p0 * d, n[0], gA, s, rc);
     St::flush(grad_coeff_B, n0 * rb, n[1], gcB, s, rc);
     St::flush(grad_coeff_Q, n0 * rq, n[2], gcQ, s, rc);

@@ -214,6 +214,81 @@ __global__ __launch_bounds__(64) void reduce_kernel(const float* __restrict__ co
     }
 }
 
+// project_kernel<1> and reduce_kernel<1, 16> of one X in a single pass over it, for E == 256 and
+// R <= 16: one wave per slab of rows_per rows (the slabs of reduce_kernel), every row read from
+// HBM once.  Each 16-row block is loaded in reduce_kernel's operand layout (lane (g, c): X[m0 + 4g +
+// si][16 et + c]) and feeds its MFMAs from registers; the block also goes to an LDS tile (rows
+// padded to kPRLd floats: 16-byte aligned, lanes of a store on distinct banks) and comes back in
+// project_kernel's layout (lane (g, c): X[m0 + c][16 j + 4g .. + 3]) for the projection against
+// basis row c, held in registers for the whole slab.  Same products in the same order as the two
+// kernels, so the same results.
+constexpr int kPRLd = 260;
+__global__ __launch_bounds__(64) void project_reduce_kernel(const float* __restrict__ coeff, int64_t M, int R,
+                                                            const float* __restrict__ X, int64_t rows_per,
+                                                            const float* __restrict__ basis,
+                                                            float* __restrict__ proj,
+                                                            float* __restrict__ partial) {
+  constexpr int E = 256;
+  __shared__ __align__(16) float tile[16 * kPRLd];
+  const int lane = threadIdx.x, g = lane >> 4, c = lane & 15;
+  const int64_t s = blockIdx.x;
+  const int64_t m_begin = s * rows_per;
+  const int64_t m_end = (m_begin + rows_per < M) ? (m_begin + rows_per) : M;
+  const bool cv = c < R;
+  float4 bas[16];  // basis[c][16 j + 4g .. + 3]
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    bas[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (cv) bas[j] = *reinterpret_cast<const float4*>(basis + (int64_t)c * E + 16 * j + 4 * g);
+  }
+  v4f acc[16];
+#pragma unroll
+  for (int et = 0; et < 16; ++et) acc[et] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int64_t m0 = m_begin; m0 < m_end; m0 += 16) {
+    float a[4], b[4][16];
+#pragma unroll
+    for (int si = 0; si < 4; ++si) {
+      const int64_t m = m0 + 4 * g + si;
+      const bool mv = m < m_end;
+      a[si] = (mv && cv) ? coeff[m * R + c] : 0.f;
+#pragma unroll
+      for (int et = 0; et < 16; ++et) b[si][et] = mv ? X[m * E + 16 * et + c] : 0.f;
+    }
+#pragma unroll
+    for (int si = 0; si < 4; ++si) {
+#pragma unroll
+      for (int et = 0; et < 16; ++et) tile[(4 * g + si) * kPRLd + 16 * et + c] = b[si][et];
+#pragma unroll
+      for (int et = 0; et < 16; ++et) acc[et] = mfma4(a[si], b[si][et], acc[et]);
+    }
+    __syncthreads();  // the block's tile is written (one wave: orders its LDS accesses)
+    v4f p = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const float4 x = *reinterpret_cast<const float4*>(tile + c * kPRLd + 16 * j + 4 * g);
+      p = mfma4(x.x, bas[j].x, p);
+      p = mfma4(x.y, bas[j].y, p);
+      p = mfma4(x.z, bas[j].z, p);
+      p = mfma4(x.w, bas[j].w, p);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t m = m0 + 4 * g + i;
+      if (m < m_end && cv) proj[m * R + c] = p[i];
+    }
+    __syncthreads();  // the tile is read before the next block overwrites it
+  }
+  float* ps = partial + s * (int64_t)R * E;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * g + i;
+    if (r < R) {
+#pragma unroll
+      for (int et = 0; et < 16; ++et) ps[(int64_t)r * E + 16 * et + c] = acc[et][i];
+    }
+  }
+}
+
 // out[j][i] = (accumulate ? out[j][i] : 0) + sum_{k in [j G, min(S, (j+1) G))} in[k][i], in the
 // order of k.  Grid: (ceil(n / 256), ceil(S / G)).
 __global__ __launch_bounds__(256) void sum_slabs_kernel(const float* __restrict__ in, int64_t S, int64_t n,
@@ -323,6 +398,19 @@ int launch_project(const float* X, int64_t M, int E, const float* basis, int R, 
   return launched() ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
+// out = (accumulate ? out : 0) + the sum of the S slab partials of R x E values (sum_slabs_kernel
+// twice: groups of kSlabGroup slabs, then the groups).
+static int launch_sum_slabs(float* partial, int64_t S, int64_t n, float* out, int accumulate, hipStream_t s) {
+  const int64_t S2 = (S + kSlabGroup - 1) / kSlabGroup;
+  float* level2 = partial + S * n;
+  const unsigned bx = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(sum_slabs_kernel, dim3(bx, (unsigned)S2), dim3(256), 0, s, partial, S, n, (int64_t)kSlabGroup,
+                     level2, 0);
+  if (!launched()) return TTC_LQR_ELAUNCH;
+  hipLaunchKernelGGL(sum_slabs_kernel, dim3(bx, 1u), dim3(256), 0, s, level2, S2, n, S2, out, accumulate);
+  return launched() ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+}
+
 int launch_reduce(const float* coeff, int64_t M, int R, const float* X, int E, float* partial, float* out,
                   int accumulate, hipStream_t s) {
   const int64_t n = (int64_t)R * E;
@@ -343,14 +431,23 @@ int launch_reduce(const float* coeff, int64_t M, int R, const float* X, int E, f
   else hipLaunchKernelGGL((reduce_kernel<4, 8>), grid, block, 0, s, coeff, M, R, X, E, rows_per, partial);
   if (!launched()) return TTC_LQR_ELAUNCH;
   // slabs whose row range is empty (rows_per * S > rows) hold zeros: reduce_kernel wrote them
-  const int64_t S2 = (S + kSlabGroup - 1) / kSlabGroup;
-  float* level2 = partial + S * n;
-  const unsigned bx = (unsigned)((n + 255) / 256);
-  hipLaunchKernelGGL(sum_slabs_kernel, dim3(bx, (unsigned)S2), dim3(256), 0, s, partial, S, n, (int64_t)kSlabGroup,
-                     level2, 0);
+  return launch_sum_slabs(partial, S, n, out, accumulate, s);
+}
+
+int launch_project_reduce(const float* coeff, int64_t M, int R, const float* X, int E, const float* basis,
+                          float* proj, float* partial, float* out, int accumulate, hipStream_t s) {
+  if (E != 256 || R > 16 || M <= 0) {
+    int rc = launch_project(X, M, E, basis, R, proj, s);
+    if (rc == TTC_LQR_OK) rc = launch_reduce(coeff, M, R, X, E, partial, out, accumulate, s);
+    return rc;
+  }
+  const int64_t S = factor_slabs(M, R, E);  // reduce_kernel<1, 16>'s slabs: one group of columns
+  const int64_t tiles = (M + 15) / 16;
+  const int64_t rows_per = 16 * ((tiles + S - 1) / S);
+  hipLaunchKernelGGL(project_reduce_kernel, dim3((unsigned)S), dim3(64), 0, s, coeff, M, R, X, rows_per, basis, proj,
+                     partial);
   if (!launched()) return TTC_LQR_ELAUNCH;
-  hipLaunchKernelGGL(sum_slabs_kernel, dim3(bx, 1u), dim3(256), 0, s, level2, S2, n, S2, out, accumulate);
-  return launched() ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
+  return launch_sum_slabs(partial, S, (int64_t)R * E, out, accumulate, s);
 }
 
 }  // namespace ttc

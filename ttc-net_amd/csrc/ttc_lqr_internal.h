@@ -115,6 +115,10 @@ int launch_expand(const uint16_t* coeff, int64_t M, int R, const float* basis, i
 int launch_project(const float* X, int64_t M, int E, const float* basis, int R, float* out, hipStream_t s);
 int launch_reduce(const float* coeff, int64_t M, int R, const float* X, int E, float* partial, float* out,
                   int accumulate, hipStream_t s);
+// launch_project(X, M, E, basis, R, proj) and launch_reduce(coeff, M, R, X, E, partial, out,
+// accumulate) with the same results, in one pass over X when E == 256 and R <= 16.
+int launch_project_reduce(const float* coeff, int64_t M, int R, const float* X, int E, const float* basis,
+                          float* proj, float* partial, float* out, int accumulate, hipStream_t s);
 int64_t factor_slabs(int64_t M, int R, int E);
 int launch_pack_upper(const float* in, int64_t P, int D, float* out, hipStream_t s);
 int launch_unpack_quu0(const float* packed, const float* B, const float* lgB, const float* Rinv, int64_t P, int H,
