@@ -104,6 +104,15 @@ extern "C" {
  * backward: the rejected problems of a batch whose sweep certified every problem are accurate on
  * the fp32 stable path, which is cheaper. */
 #define TTC_LQR_FLAG_FP64_FALLBACK 64
+/* TTC_LQR_FLAG_KEEP_EXPANDED (factored entry points only, with a stash): the forward expands
+ * B, Q and Q_f into the stash buffer instead of its workspace, and the backward reads them from
+ * there instead of expanding them again -- what the reference's layer does by keeping its
+ * einsums' outputs for autograd.  The stash buffer is then align256(ttc_lqr_stash_bytes, or
+ * ttc_lqr_compact_stash_bytes with TTC_LQR_FLAG_COMPACT_STASH) + ttc_lqr_expanded_bytes bytes:
+ * after the V_1 stash, at 256-byte boundaries, B [N,d,du], Q [N,d,d] and Q_f [N,H,d,d] in fp32.
+ * Pass the same flag and buffer to both calls; NULL stash with this flag: TTC_LQR_EINVAL.  The
+ * other entry points ignore it.  Same results. */
+#define TTC_LQR_FLAG_KEEP_EXPANDED 128
 
 /* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
  * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds
@@ -130,6 +139,10 @@ size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t d
 
 /* Bytes of the compact stash (TTC_LQR_FLAG_COMPACT_STASH): 4 * N * H * d(d+1)/2. */
 size_t ttc_lqr_compact_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du);
+
+/* Bytes of the expanded B, Q and Q_f that TTC_LQR_FLAG_KEEP_EXPANDED keeps after the stash:
+ * align256(4 N d du) + align256(4 N d d) + align256(4 N H d d). */
+size_t ttc_lqr_expanded_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du);
 
 /* Workspace bytes ttc_lqr_backward needs to process `chunk_tokens` tokens per pass
  * (it loops over the tokens in chunks of that size) with these `flags` (the stable path's

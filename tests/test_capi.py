@@ -31,7 +31,7 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
         "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes",
-        "ttc_lqr_compact_stash_bytes",
+        "ttc_lqr_compact_stash_bytes", "ttc_lqr_expanded_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
         "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host", "ttc_lqr_fallback_bytes",
@@ -65,7 +65,8 @@ def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 8) == 1 and L.ttc_lqr_supported_flags(32, 32, 8 | 4) == 1
-    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 128) == 0
+    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 256) == 0
+    assert L.ttc_lqr_supported_flags(64, 64, 128 | 16) == 1  # TTC_LQR_FLAG_KEEP_EXPANDED, any d
     # TTC_LQR_FLAG_FP64_FALLBACK (64) needs the fp64 kernels: d <= 32
     assert L.ttc_lqr_supported_flags(16, 16, 64) == 1 and L.ttc_lqr_supported_flags(32, 32, 64) == 1
     assert L.ttc_lqr_supported_flags(64, 64, 64) == 0
@@ -197,6 +198,25 @@ def test_factored_argument_validation(L):
     assert bwd(rb=70) == (1, 0)
     assert bwd(basis=odd) == (1, 0)
     assert bwd(work=64) == (1, 0)
+
+
+def test_keep_expanded_sizing_and_validation(L):
+    """TTC_LQR_FLAG_KEEP_EXPANDED (128): the expanded B, Q, Q_f after the stash take
+    align256 of each array; the factored workspaces then hold no expansion of their own; and
+    the flag without a stash is rejected before any device work."""
+    a = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    assert L.ttc_lqr_expanded_bytes(10, 8, 16, 16) == a(4 * 10 * 256) + a(4 * 10 * 256) + a(4 * 80 * 256)
+    assert L.ttc_lqr_expanded_bytes(3, 2, 32, 32) == a(4 * 3 * 1024) * 2 + a(4 * 6 * 1024)
+    for backward in (0, 1):
+        plain = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 1, backward, 0, 0)
+        kept = L.ttc_lqr_factored_workspace_bytes(100, 8, 16, 16, 16, 16, 64, 1, backward, 0, 128)
+        assert plain - kept == a(4 * 100 * 256) * 2 + a(4 * 800 * 256)
+    p = ctypes.c_void_p(16)
+    assert L.ttc_lqr_forward_factored(*([p] * 11), 1, 1, 16, 16, 16, 16, 4, 128, p, None, p, 1 << 30,
+                                      None, None) == 1
+    n_fb = ctypes.c_int64(-3)
+    assert L.ttc_lqr_backward_factored(*([p] * 11), p, p, 1, 1, 16, 16, 16, 16, 4, 128, None, *([p] * 11), p,
+                                       1 << 30, float("inf"), None, ctypes.byref(n_fb), None) == 1
 
 
 def test_rescale_argument_validation(L):

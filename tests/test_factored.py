@@ -154,6 +154,29 @@ def test_factored_token_chunks_match_single_pass(monkeypatch):
         assert _relerr(many[k], ref[k]) <= TOL, k
 
 
+@pytest.mark.parametrize("cfg,n_tok,T,stash", [(2, 24, 64, "always"), (5, 8, 1024, "always"),
+                                              (4, 2, 256, "always"), (2, 24, 64, "compact")])
+def test_kept_expansion_equals_reexpansion(cfg, n_tok, T, stash, monkeypatch):
+    """TTC_LQR_FLAG_KEEP_EXPANDED: the forward expands B, Q, Q_f into the stash buffer and the
+    backward reads them there instead of expanding again.  The same values reach the same kernels,
+    so u and all eleven gradients are bitwise those of the run that expands twice -- with the full
+    and the compact stash, and at T = 1024 (fp64 rescue, two rollout tiers, stable path); the
+    keep decision is forced both ways and recorded, so both branches run."""
+    import ttc.solvers.hip_lqr as hl
+    ins = factored_inputs(cfg, n_tok, seed=2)
+    N, H, d = ins[0].shape
+    dU = torch.randn(N, H, ins[3].shape[-1], generator=torch.Generator().manual_seed(5)).double().numpy()
+    decided, outs = [], []
+    for keep in (False, True):
+        monkeypatch.setattr(hl, "_keep_expanded", lambda *a, keep=keep: decided.append(keep) or keep)
+        print(f"[keep-expanded cfg{cfg} T={T} stash={stash} keep={keep}]", flush=True)
+        outs.append(run_factored(ins, T, dU, stash=stash, grad_limit=math.inf))
+    assert decided == [False, True]
+    for k in ["u"] + NAMES11:
+        assert np.array_equal(outs[0][k], outs[1][k]), k
+    assert outs[0]["_fallback"] == outs[1]["_fallback"]
+
+
 def test_factored_equals_materialised_hip_solver():
     """Same HIP kernels on both sides: the factored entry points against hip_lqr_solve on
     torch-expanded B, Q, Q_f with torch's chain rule of the einsums."""

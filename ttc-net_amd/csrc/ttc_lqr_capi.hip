@@ -616,6 +616,39 @@ struct FactLayout {
   size_t bas, gbas, Bx, Qx, Qfx, gB, gQ, gQf, part, cin[10], cg[9], v1t, q0t, rlist, inner, total;
 };
 
+// TTC_LQR_FLAG_KEEP_EXPANDED: byte offsets of the expanded B [N,d,du], Q [N,d,d], Q_f [N,H,d,d]
+// after the V_1 stash (which is align256 of the full or compact stash bytes).
+struct KeptLayout {
+  size_t B, Q, Qf, total;
+};
+
+static KeptLayout kept_layout(int64_t N, int H, int d, int du) {
+  KeptLayout K{};
+  size_t off = 0;
+  K.B = off;
+  off += align256((size_t)N * d * du * sizeof(float));
+  K.Q = off;
+  off += align256((size_t)N * d * d * sizeof(float));
+  K.Qf = off;
+  off += align256((size_t)N * H * d * d * sizeof(float));
+  K.total = off;
+  return K;
+}
+
+// The expanded arrays of a KEEP_EXPANDED stash buffer.
+struct Kept {
+  float *B, *Q, *Qf;
+};
+
+static Kept kept_arrays(const float* stash, int64_t N, int H, int d, int du, bool compact) {
+  const size_t v1 = compact ? (size_t)N * H * ((size_t)d * (d + 1) / 2) * sizeof(float)
+                            : (size_t)N * H * ((size_t)d * d + (size_t)du * du) * sizeof(float);
+  char* base = reinterpret_cast<char*>(const_cast<float*>(stash)) + align256(v1);
+  const KeptLayout K = kept_layout(N, H, d, du);
+  return Kept{reinterpret_cast<float*>(base + K.B), reinterpret_cast<float*>(base + K.Q),
+              reinterpret_cast<float*>(base + K.Qf)};
+}
+
 // Elements of the per-problem / per-token arrays of a chunk, in argument order:
 // A_diag, coeff_B, coeff_Q, R_inv, coeff_Qf, lgA, lgB, lgQ, h0 (and d_u).
 static void io_counts(int64_t nc, int H, int d, int du, int rb, int rq, size_t (&n)[10]) {
@@ -630,6 +663,7 @@ static void io_counts(int64_t nc, int H, int d, int du, int rb, int rq, size_t (
 static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, int T, bool with_stash,
                               bool backward, bool bf16, bool compact, int flags) {
   const bool fp64 = fp64_stable(flags, d);
+  const bool kept = (flags & TTC_LQR_FLAG_KEEP_EXPANDED) != 0;  // B, Q, Q_f live in the stash buffer
   const size_t N = (size_t)nc, P = (size_t)nc * (size_t)H, Eb = (size_t)d * du, Eq = (size_t)d * d;
   const size_t nbas = (size_t)rb * Eb + (size_t)rq * Eq;
   FactLayout L{};
@@ -639,11 +673,11 @@ static FactLayout fact_layout(int64_t nc, int H, int d, int du, int rb, int rq, 
   L.gbas = off;
   off += (bf16 && backward) ? align256(nbas * sizeof(float)) : 0;
   L.Bx = off;
-  off += align256(N * Eb * sizeof(float));
+  off += kept ? 0 : align256(N * Eb * sizeof(float));
   L.Qx = off;
-  off += align256(N * Eq * sizeof(float));
+  off += kept ? 0 : align256(N * Eq * sizeof(float));
   L.Qfx = off;
-  off += align256(P * Eq * sizeof(float));
+  off += kept ? 0 : align256(P * Eq * sizeof(float));
   if (backward) {
     L.gB = off;
     off += align256(N * Eb * sizeof(float));
@@ -770,6 +804,8 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
   using St = Store<TS>;
   const bool compact = stash != nullptr && (flags & TTC_LQR_FLAG_COMPACT_STASH);
   const bool fp64 = fp64_stable(flags, d);
+  const bool kept = stash != nullptr && (flags & TTC_LQR_FLAG_KEEP_EXPANDED);
+  const Kept K = kept ? kept_arrays(stash, n_tokens, H, d, du, compact) : Kept{};
   const int64_t chunk = fact_chunk(n_tokens, H, d, du, rb, rq, T, stash != nullptr, false, St::BF16, compact, flags,
                                    ws_bytes);
   if (chunk == 0) return TTC_LQR_EINVAL;
@@ -797,6 +833,11 @@ static int forward_factored(const TS* A_diag, const TS* coeff_B, const TS* coeff
     float* Bx = reinterpret_cast<float*>(ws + L.Bx);
     float* Qx = reinterpret_cast<float*>(ws + L.Qx);
     float* Qfx = reinterpret_cast<float*>(ws + L.Qfx);
+    if (kept) {  // into the stash buffer, where the backward reads them
+      Bx = K.B + n0 * d * du;
+      Qx = K.Q + n0 * dd;
+      Qfx = K.Qf + p0 * dd;
+    }
     // the expansion reads the coefficients as stored (bf16: widened in registers)
     rc = expand_chunk(coeff_B + n0 * rb, coeff_Q + n0 * rq, coeff_Qf + p0 * rq, Bs, Gs, nc, H, d, du, rb, rq, Bx, Qx,
                       Qfx, s);
@@ -830,6 +871,8 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
   const bool with_stash = stash != nullptr && !stable;
   const bool compact = with_stash && (flags & TTC_LQR_FLAG_COMPACT_STASH);
   const bool fp64 = fp64_stable(flags, d);
+  const bool kept = stash != nullptr && (flags & TTC_LQR_FLAG_KEEP_EXPANDED);
+  const Kept K = kept ? kept_arrays(stash, n_tokens, H, d, du, (flags & TTC_LQR_FLAG_COMPACT_STASH) != 0) : Kept{};
   flags &= ~TTC_LQR_FLAG_COMPACT_STASH;
   const int Eb = d * du, Eq = d * d;
   const size_t nb = (size_t)rb * Eb, nq = (size_t)rq * Eq;
@@ -888,8 +931,14 @@ static int backward_factored(const TS* A_diag, const TS* coeff_B, const TS* coef
     float* gQ = reinterpret_cast<float*>(ws + L.gQ);
     float* gQf = reinterpret_cast<float*>(ws + L.gQf);
     float* part = reinterpret_cast<float*>(ws + L.part);
-    rc = expand_chunk(cB, cQ, cQf, Bs, Gs, nc, H, d, du, rb, rq, Bx, Qx, Qfx, s);
-    if (rc != TTC_LQR_OK) return rc;
+    if (kept) {  // expanded by the forward
+      Bx = K.B + n0 * d * du;
+      Qx = K.Q + n0 * dd;
+      Qfx = K.Qf + p0 * dd;
+    } else {
+      rc = expand_chunk(cB, cQ, cQf, Bs, Gs, nc, H, d, du, rb, rq, Bx, Qx, Qfx, s);
+      if (rc != TTC_LQR_OK) return rc;
+    }
     const float* v1 = with_stash ? stash + p0 * dd : nullptr;
     const float* q0 = with_stash ? stash + P * dd + p0 * (int64_t)du * du : nullptr;
     if (compact) {  // V_1 from its upper triangle, Quu_0 = R + B_0' V_1 B_0 recomputed
@@ -937,6 +986,7 @@ static int forward_factored_entry(const TS* A_diag, const TS* coeff_B, const TS*
                                   void* stream) {
   if (!fact_args_ok(n_tokens, heads, d, du, rb, rq, T)) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  if ((flags & TTC_LQR_FLAG_KEEP_EXPANDED) && !stash) return TTC_LQR_EINVAL;
   if (n_tokens == 0) return TTC_LQR_OK;
   if (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !lgA || !lgB || !lgQ || !h0 || !B_basis ||
       !Q_basis || !u || !workspace)
@@ -959,6 +1009,7 @@ static int backward_factored_entry(const TS* A_diag, const TS* coeff_B, const TS
   if (n_fallback) *n_fallback = 0;
   if (!fact_args_ok(n_tokens, heads, d, du, rb, rq, T)) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
+  if ((flags & TTC_LQR_FLAG_KEEP_EXPANDED) && !stash) return TTC_LQR_EINVAL;
   const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
   if (!gBs || !gQs || !workspace) return TTC_LQR_EINVAL;
   if (n_tokens > 0 &&
@@ -1001,13 +1052,18 @@ int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
     return 0;
   const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD |
                         TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH | TTC_LQR_FLAG_FP64_RESCUE |
-                        TTC_LQR_FLAG_FP64_FALLBACK;
+                        TTC_LQR_FLAG_FP64_FALLBACK | TTC_LQR_FLAG_KEEP_EXPANDED;
   return (flags & ~known) ? 0 : 1;
 }
 
 size_t ttc_lqr_compact_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du) {
   if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0) return 0;
   return sizeof(float) * (size_t)n_tokens * (size_t)heads * ((size_t)d * (d + 1) / 2);
+}
+
+size_t ttc_lqr_expanded_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du) {
+  if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0) return 0;
+  return kept_layout(n_tokens, heads, d, du).total;
 }
 
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {

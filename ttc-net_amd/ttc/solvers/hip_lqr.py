@@ -58,7 +58,7 @@ import os
 import torch
 
 from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS, \
-    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK
+    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK, FLAG_KEEP_EXPANDED
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
            "check_deferred_status",
@@ -399,6 +399,18 @@ def _workspace_budget(dev) -> int:
     return _env_bytes("TTC_LQR_WORKSPACE_BYTES", min(16 << 30, max(1 << 30, _stash_budget(dev))))
 
 
+def _align256(n: int) -> int:
+    return (n + 255) // 256 * 256
+
+
+def _keep_expanded(dev, kind: str, stash_bytes: int, expanded_bytes: int) -> bool:
+    """Whether the factored forward keeps its expansion of B, Q and Q_f for the backward
+    (``TTC_LQR_FLAG_KEEP_EXPANDED``: the backward then does not expand them again): with the full
+    stash, when the stash and the expansion fit the stash budget together; never beside a compact
+    stash, which is chosen when memory is short."""
+    return kind == "full" and _stash_fits(dev, _align256(stash_bytes) + expanded_bytes)
+
+
 def _workspace_bytes(full: int, floor: int, dev) -> int:
     """Bytes of a call's workspace: ``full`` (one pass) when the budget allows, else the budget,
     at least ``floor`` (one token's worth).  The default budget is never below 1 GiB, so a
@@ -415,7 +427,7 @@ def _workspace_bytes(full: int, floor: int, dev) -> int:
 
 class HipLQRFactoredFunc(torch.autograd.Function):
     """The solve on the layer's low-rank factors (``ttc_layer.py:117-123``): ``B``, ``Q`` and
-    ``Q_f`` are never materialised in full; the library expands them per token chunk.
+    ``Q_f`` are expanded by the library per token chunk (in full only in the stash, see below).
 
     Inputs: ``A_diag [N,H,d]``, ``coeff_B [N,rb]``, ``coeff_Q [N,rq]``, ``R_inv [N,H,du]``,
     ``coeff_Qf [N,H,rq]``, ``log_gamma_A [N,H]``, ``log_gamma_B [N,H,du]``,
@@ -430,7 +442,10 @@ class HipLQRFactoredFunc(torch.autograd.Function):
     Stash: as :class:`HipLQRSolveFunc`; when the full stash does not fit the budget (``"auto"``)
     or ``stash="compact"``, only the upper triangles of ``V_1`` are kept
     (``TTC_LQR_FLAG_COMPACT_STASH``: 4x smaller at d = 64) and the backward recomputes
-    ``Quu_0`` from them instead of re-running the forward sweep.
+    ``Quu_0`` from them instead of re-running the forward sweep.  With the full stash, when the
+    budget also holds the forward's expansion of ``B``, ``Q`` and ``Q_f`` (2.7 GB at config 2),
+    the stash keeps it and the backward reads it instead of expanding again
+    (``TTC_LQR_FLAG_KEEP_EXPANDED``; what the reference's layer keeps for autograd).
     ``rescale`` (``"none" | "l2_norm" | "h0_norm"``, fp32 storage): the layer's rescale of
     ``u`` (``ttc_layer.py:142-147``) fused into the call -- the result is the rescaled output
     and the backward takes its gradient (``ttc_lqr_rescale`` / ``ttc_lqr_rescale_backward``).
@@ -490,8 +505,11 @@ class HipLQRFactoredFunc(torch.autograd.Function):
                 kind = "compact"
         if kind == "compact":
             flags |= FLAG_COMPACT_STASH
-        st = None if kind is None else torch.empty((stash_bytes if kind == "full" else compact_bytes) // 4,
-                                                   device=dev, dtype=torch.float32)
+        st_bytes = stash_bytes if kind == "full" else compact_bytes
+        if kind is not None and _keep_expanded(dev, kind, st_bytes, lib.ttc_lqr_expanded_bytes(bs, nh, Dp, Dp)):
+            flags |= FLAG_KEEP_EXPANDED
+            st_bytes = _align256(st_bytes) + lib.ttc_lqr_expanded_bytes(bs, nh, Dp, Dp)
+        st = None if kind is None else torch.empty(st_bytes // 4, device=dev, dtype=torch.float32)
         ws_stash = {None: 0, "full": 1, "compact": 2}[kind]
         full = lib.ttc_lqr_factored_workspace_bytes(max(bs, 1), nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16), flags)
         one = lib.ttc_lqr_factored_workspace_bytes(1, nh, Dp, Dp, rb, rq, T, ws_stash, 0, int(bf16), flags)
