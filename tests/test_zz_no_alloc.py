@@ -5,7 +5,9 @@ with a caller-allocated workspace, bit for bit (the same kernels on independent 
 token chunks and fallback passes the scratch imposes do not change any problem's arithmetic or
 the order of a token's head sums).  Cases: a config-2 slice (one chunk), a batch that the
 256 MiB scratch splits into several token chunks, and config-5 stress inputs whose rejected
-problems take the stable path inside the scratch (asserted: the fallback count is positive)."""
+problems take the stable path inside the scratch (asserted: the fallback count is positive), at
+T = 64 and at T = 1024 under TTC_LQR_FLAG_FP64_RESCUE (the fp32 head-group rollout, the fp64
+second rollout tier and the fp64 stable path, all inside the scratch)."""
 import ctypes
 import math
 
@@ -30,7 +32,7 @@ def _grads_like(ins):
     return [torch.empty_like(t) for t in (A, B, Q, R, Qf, lA, lB, lQ, h0)]
 
 
-def _backward(ins, T, noalloc, stash):
+def _backward(ins, T, noalloc, stash, flags=0):
     from ttc.solvers._lib import lib
     N, H, d = ins[0].shape
     dev = ins[0].device
@@ -38,19 +40,19 @@ def _backward(ins, T, noalloc, stash):
     st = torch.empty(lib.ttc_lqr_stash_bytes(N, H, d, d, T) // 4, device=dev) if stash else None
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     s = torch.cuda.current_stream().cuda_stream
-    rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in ins], N, H, d, d, T, 0, u.data_ptr(),
+    rc = lib.ttc_lqr_forward(*[t.data_ptr() for t in ins], N, H, d, d, T, flags, u.data_ptr(),
                              None if st is None else st.data_ptr(), status.data_ptr(), s)
     assert rc == 0
     dU = torch.randn(N, H, d, generator=torch.Generator(device=dev).manual_seed(N + T), device=dev)
     g = _grads_like(ins)
     status.zero_()
     n_fb = ctypes.c_int64(-1)
-    common = [*[t.data_ptr() for t in ins], u.data_ptr(), dU.data_ptr(), N, H, d, d, T, 0,
+    common = [*[t.data_ptr() for t in ins], u.data_ptr(), dU.data_ptr(), N, H, d, d, T, flags,
               None if st is None else st.data_ptr(), *[t.data_ptr() for t in g]]
     if noalloc:
         rc = lib.ttc_lqr_backward_noalloc(*common, math.inf, status.data_ptr(), ctypes.byref(n_fb), s)
     else:
-        ws_bytes = lib.ttc_lqr_workspace_bytes(N, H, d, d, T, int(stash), 0)
+        ws_bytes = lib.ttc_lqr_workspace_bytes(N, H, d, d, T, int(stash), flags)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
         rc = lib.ttc_lqr_backward(*common, ws.data_ptr(), ws.numel(), math.inf, status.data_ptr(),
                                   ctypes.byref(n_fb), s)
@@ -59,13 +61,14 @@ def _backward(ins, T, noalloc, stash):
     return [t.cpu() for t in g], int(status.item()), int(n_fb.value)
 
 
-@pytest.mark.parametrize("cfg,n1,n2,T,stash", [(2, 256, 40, 64, True), (2, 1200, 300, 64, False),
-                                               (5, 64, 16, 64, True)])
-def test_noalloc_backward_equals_workspace_backward(cfg, n1, n2, T, stash):
+@pytest.mark.parametrize("cfg,n1,n2,T,stash,flags", [(2, 256, 40, 64, True, 0), (2, 1200, 300, 64, False, 0),
+                                                     (5, 64, 16, 64, True, 0), (5, 32, 8, 1024, True, 32)])
+def test_noalloc_backward_equals_workspace_backward(cfg, n1, n2, T, stash, flags):
     for n_tok in (n1, n2):  # two calls in a row, the second smaller
         ins = _inputs(cfg, n_tok, seed=n_tok + cfg)
-        ref, st_ref, fb_ref = _backward(ins, T, noalloc=False, stash=stash)
-        out, st_out, fb_out = _backward(ins, T, noalloc=True, stash=stash)
+        print(f"[noalloc cfg{cfg} tokens={n_tok} T={T} stash={stash} flags={flags}]", flush=True)
+        ref, st_ref, fb_ref = _backward(ins, T, noalloc=False, stash=stash, flags=flags)
+        out, st_out, fb_out = _backward(ins, T, noalloc=True, stash=stash, flags=flags)
         errs = {n: float((a.double() - b.double()).abs().max() / max(b.double().abs().max(), 1e-30))
                 for n, a, b in zip(NAMES, out, ref)}
         same = all(torch.equal(a, b) for a, b in zip(out, ref))
