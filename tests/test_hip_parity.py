@@ -282,10 +282,11 @@ def test_wide_symplectic_stress(d, H, T):
                precision="fp32")
 
 
-@pytest.mark.parametrize("cfg,T,seed", [(5, 64, 5), (5, 1024, 5), ("5b", 1024, 55)])
+@pytest.mark.parametrize("cfg,T,seed", [(5, 64, 5), (5, 1024, 5), ("5b", 1024, 55), (5, 2048, 7), ("5b", 2048, 57)])
 def test_config5_stress(cfg, T, seed):
     """Config 5 / 5b share the layer and the log-normal token scales; 5b draws its own tokens
-    (another seed), so the two cases cover different problems."""
+    (another seed), so the two cases cover different problems.  T = 2048 is the longest horizon
+    of the reference bench's sweep (bench_lqr_solvers.py:30-37)."""
     x = make_x(cfg, n_tokens=4, seed=seed)
     check_case(f"cfg{cfg}", layer_solver_inputs(cfg, x), T, grad_limit=math.inf)
 
