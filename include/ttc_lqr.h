@@ -113,6 +113,16 @@ extern "C" {
  * Pass the same flag and buffer to both calls; NULL stash with this flag: TTC_LQR_EINVAL.  The
  * other entry points ignore it.  Same results. */
 #define TTC_LQR_FLAG_KEEP_EXPANDED 128
+/* TTC_LQR_FLAG_RESCUE_V1 (d = du = 16, with TTC_LQR_FLAG_FP64_RESCUE, ttc_lqr_forward_ws /
+ * ttc_lqr_backward / ttc_lqr_backward_noalloc, with a stash): the forward's fp64 rescue also keeps
+ * the fp64 V_1 and Quu_0 of up to max(64, P/8) of the problems it recomputes (P = N * H), after
+ * the stash, and the backward's fp64 second rollout tier starts those problems from them instead
+ * of the stash's fp32 roundings, so more of them pass its certificate and fewer take the stable
+ * path.  The stash buffer is then align256(ttc_lqr_stash_bytes) + ttc_lqr_rescue_stash_bytes
+ * bytes: a slot index per problem (int32, -1 = none), then the slots (fp64 V_1 then Quu_0).
+ * Pass the same flag and buffer to both calls; NULL stash with this flag: TTC_LQR_EINVAL.  Same
+ * results to the certificate's tolerance. */
+#define TTC_LQR_FLAG_RESCUE_V1 256
 
 /* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
  * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds
@@ -143,6 +153,10 @@ size_t ttc_lqr_compact_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, i
 /* Bytes of the expanded B, Q and Q_f that TTC_LQR_FLAG_KEEP_EXPANDED keeps after the stash:
  * align256(4 N d du) + align256(4 N d d) + align256(4 N H d d). */
 size_t ttc_lqr_expanded_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du);
+
+/* Bytes that TTC_LQR_FLAG_RESCUE_V1 keeps after the stash: align256(4 P) + align256(8 S (d d +
+ * du du)) for P = N * H problems and S = min(P, max(64, P / 8)) slots. */
+size_t ttc_lqr_rescue_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du);
 
 /* Workspace bytes ttc_lqr_backward needs to process `chunk_tokens` tokens per pass
  * (it loops over the tokens in chunks of that size) with these `flags` (the stable path's

@@ -31,7 +31,7 @@ def test_header_declares_expected_entry_points():
     assert declared_functions() == sorted([
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
         "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes",
-        "ttc_lqr_compact_stash_bytes", "ttc_lqr_expanded_bytes",
+        "ttc_lqr_compact_stash_bytes", "ttc_lqr_expanded_bytes", "ttc_lqr_rescue_stash_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
         "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host", "ttc_lqr_fallback_bytes",
@@ -65,7 +65,7 @@ def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 8) == 1 and L.ttc_lqr_supported_flags(32, 32, 8 | 4) == 1
-    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 256) == 0
+    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 512) == 0
     assert L.ttc_lqr_supported_flags(64, 64, 128 | 16) == 1  # TTC_LQR_FLAG_KEEP_EXPANDED, any d
     # TTC_LQR_FLAG_FP64_FALLBACK (64) needs the fp64 kernels: d <= 32
     assert L.ttc_lqr_supported_flags(16, 16, 64) == 1 and L.ttc_lqr_supported_flags(32, 32, 64) == 1
@@ -217,6 +217,26 @@ def test_keep_expanded_sizing_and_validation(L):
     n_fb = ctypes.c_int64(-3)
     assert L.ttc_lqr_backward_factored(*([p] * 11), p, p, 1, 1, 16, 16, 16, 16, 4, 128, None, *([p] * 11), p,
                                        1 << 30, float("inf"), None, ctypes.byref(n_fb), None) == 1
+
+
+def test_rescue_v1_sizing_and_validation(L):
+    """TTC_LQR_FLAG_RESCUE_V1 (256): d = du = 16 only; after the stash a slot index per problem and
+    min(P, max(64, P / 8)) slots of 2 x 256 doubles, each region 256-byte aligned; the flag without
+    a stash is rejected, and the factored entry points do not take it."""
+    a = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    assert L.ttc_lqr_supported_flags(16, 16, 256 | 32) == 1
+    assert L.ttc_lqr_supported_flags(32, 32, 256 | 32) == 0 and L.ttc_lqr_supported_flags(64, 64, 256) == 0
+    for n, h in ((1000, 8), (3, 2), (20, 8)):
+        P = n * h
+        slots = min(P, max(64, P // 8))
+        assert L.ttc_lqr_rescue_stash_bytes(n, h, 16, 16) == a(4 * P) + a(8 * slots * 512)
+    p = ctypes.c_void_p(16)
+    assert _fwd(L, flags=256 | 32) == 1                      # no stash
+    n_fb = ctypes.c_int64(-3)
+    assert L.ttc_lqr_backward(*([p] * 11), 1, 1, 16, 16, 4, 256 | 32, None, *([p] * 9), p, 1 << 30,
+                              float("inf"), None, ctypes.byref(n_fb), None) == 1
+    assert L.ttc_lqr_forward_factored(*([p] * 11), 1, 1, 16, 16, 16, 16, 4, 256 | 32, p, p, p, 1 << 30,
+                                      None, None) == 2
 
 
 def test_rescale_argument_validation(L):

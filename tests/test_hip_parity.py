@@ -327,6 +327,48 @@ def test_long_horizon_two_tier_rollout(d, H, monkeypatch):
         assert all(v <= TOL for v in errs.values()), (label, errs)
 
 
+def test_rescue_v1_slots_cut_the_stable_path(monkeypatch):
+    """TTC_LQR_FLAG_RESCUE_V1 at T = 1024 on config-5b token scales: the forward's fp64 rescue keeps
+    the fp64 V_1 / Quu_0 of the problems it recomputes, and the backward's fp64 second rollout tier
+    starts those problems from them instead of their fp32 roundings.  Some then pass its
+    certificate and skip the stable path: fewer problems take it than without the slots, and both
+    runs agree with the fp64 oracle."""
+    import ttc.solvers.hip_lqr as hl
+    ins = layer_solver_inputs("5b", make_x("5b", n_tokens=64, seed=3))
+    T = 1024
+    pb = LQRProblem(*ins, T)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(8)).double().numpy()
+    ref = solve_grads(pb, dU)
+    orig = hl._rescue_v1
+    outs = {}
+    for on in (False, True):
+        monkeypatch.setattr(hl, "_rescue_v1", lambda flags, Dp, on=on: on and orig(flags, Dp))
+        print(f"[rescue-v1 cfg5b T={T} slots={on}]", flush=True)
+        outs[on] = run_hip(ins, T, dU, grad_limit=math.inf)
+        errs = {k: _relerr(outs[on][k], ref[k]) for k in ["u"] + NAMES}
+        print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()) + f"  fallback={outs[on]['_fallback']}",
+              flush=True)
+        assert all(v <= TOL for v in errs.values()), errs
+    assert outs[True]["_fallback"] < outs[False]["_fallback"]
+
+
+@pytest.mark.parametrize("slots", [False, True])
+def test_certificate_rejects_trajectories_beyond_fp32(slots, monkeypatch):
+    """Config-5b token 29207 (of the 32,768-token sample, seed 3), T = 1024: started from the
+    forward's fp64 V_1, head 3's fp64 Hamiltonian rollout grows to |lambda| ~ 1e52 -- finite in fp64,
+    beyond the fp32 range -- while its gradient sums stay below 1e34.  The certificate compares
+    residual and magnitude as fp32 values, where both are +inf; it must reject such a problem
+    (inf <= tau * inf holds) and leave it to the stable path.  Every output within 1e-4 of the fp64
+    oracle, with and without the rescue's fp64 slots."""
+    import ttc.solvers.hip_lqr as hl
+    full = layer_solver_inputs("5b", make_x("5b", n_tokens=32768, seed=3))
+    ins = [t[29207:29208].clone() for t in full]
+    del full
+    orig = hl._rescue_v1
+    monkeypatch.setattr(hl, "_rescue_v1", lambda flags, Dp: slots and orig(flags, Dp))
+    check_case(f"cfg5b token 29207 slots={slots}", ins, 1024, seed=4, grad_limit=math.inf)
+
+
 @pytest.mark.parametrize("cfg,n_tok", [(5, 64), ("5b", 64)])
 def test_forward_workspace_packs_the_fp64_rescue(cfg, n_tok):
     """Long horizons (T = 1024, FP64_RESCUE): ttc_lqr_forward_ws lists the problems the

@@ -223,11 +223,12 @@ static StableLayout stable_layout(int64_t chunk_tokens, int H, int d, int T, boo
 static int fwd_d(int d, const float* a, const float* b, const float* q, const float* r, const float* qf,
                  const float* la, const float* lb, const float* lq, const float* hz, int64_t P, int H, int T, float* u,
                  float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
-                 int32_t* rescue_ws = nullptr) {
+                 int32_t* rescue_ws = nullptr, RescueSlots rs = RescueSlots{}) {
   flags = forward_flags(flags, d, H, sm);
   switch (d) {
     case 16:
-      return launch_fwd_d16(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags, rescue_ws);
+      return launch_fwd_d16(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags, rescue_ws,
+                            rs);
     case 32:
       return launch_fwd_d32(a, b, q, r, qf, la, lb, lq, hz, P, H, T, u, st_a, st_b, sm, status, s, flags, rescue_ws);
     case 64:
@@ -424,7 +425,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
                          float* grad_Q, float* grad_R_inv, float* grad_Q_f, float* grad_log_gamma_A,
                          float* grad_log_gamma_B, float* grad_log_gamma_Q, float* grad_h0, char* ws,
                          size_t workspace_bytes, float grad_limit, int32_t* status, int64_t* n_fallback,
-                         hipStream_t s) {
+                         hipStream_t s, RescueSlots rs = RescueSlots{}) {
   const bool fp64 = fp64_stable(flags, d);
   if (flags & TTC_LQR_FLAG_STABLE_BWD) {
     if (n_fallback) *n_fallback = n_tokens * H;
@@ -537,7 +538,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
                              (int64_t)nfail, plist);
           if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
           switch (d) {
-            case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist); break;
+            case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist, rs.slot_of ? rs.slot_of + p0 : nullptr, rs.slots); break;
             case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist); break;
             default: return TTC_LQR_EUNSUPPORTED;
           }
@@ -633,6 +634,33 @@ static KeptLayout kept_layout(int64_t N, int H, int d, int du) {
   off += align256((size_t)N * H * d * d * sizeof(float));
   K.total = off;
   return K;
+}
+
+// TTC_LQR_FLAG_RESCUE_V1: after the stash (align256 of its bytes), a slot index per problem
+// (int32, -1 = none) and min(P, max(64, P / 8)) slots of the fp64 V_1 and Quu_0 (d = du = 16).
+static int64_t rescue_nslot(int64_t P) {
+  const int64_t s = P / 8 > 64 ? P / 8 : 64;
+  return s < P ? s : P;
+}
+
+static size_t rescue_record_bytes(int64_t P, int d, int du) {
+  return align256((size_t)P * sizeof(int32_t)) +
+         align256((size_t)rescue_nslot(P) * ((size_t)d * d + (size_t)du * du) * sizeof(double));
+}
+
+static RescueSlots rescue_slots(const float* stash, int64_t P, int d, int du) {
+  char* base = reinterpret_cast<char*>(const_cast<float*>(stash)) +
+               align256((size_t)P * ((size_t)d * d + (size_t)du * du) * sizeof(float));
+  RescueSlots rs;
+  rs.slot_of = reinterpret_cast<int32_t*>(base);
+  rs.slots = reinterpret_cast<double*>(base + align256((size_t)P * sizeof(int32_t)));
+  rs.nslot = rescue_nslot(P);
+  return rs;
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
 }
 
 // The expanded arrays of a KEEP_EXPANDED stash buffer.
@@ -987,6 +1015,7 @@ static int forward_factored_entry(const TS* A_diag, const TS* coeff_B, const TS*
   if (!fact_args_ok(n_tokens, heads, d, du, rb, rq, T)) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
   if ((flags & TTC_LQR_FLAG_KEEP_EXPANDED) && !stash) return TTC_LQR_EINVAL;
+  if (flags & TTC_LQR_FLAG_RESCUE_V1) return TTC_LQR_EUNSUPPORTED;  // materialised entry points only
   if (n_tokens == 0) return TTC_LQR_OK;
   if (!A_diag || !coeff_B || !coeff_Q || !R_inv || !coeff_Qf || !lgA || !lgB || !lgQ || !h0 || !B_basis ||
       !Q_basis || !u || !workspace)
@@ -1010,6 +1039,7 @@ static int backward_factored_entry(const TS* A_diag, const TS* coeff_B, const TS
   if (!fact_args_ok(n_tokens, heads, d, du, rb, rq, T)) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
   if ((flags & TTC_LQR_FLAG_KEEP_EXPANDED) && !stash) return TTC_LQR_EINVAL;
+  if (flags & TTC_LQR_FLAG_RESCUE_V1) return TTC_LQR_EUNSUPPORTED;  // materialised entry points only
   const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
   if (!gBs || !gQs || !workspace) return TTC_LQR_EINVAL;
   if (n_tokens > 0 &&
@@ -1050,9 +1080,10 @@ int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if (!ttc_lqr_supported(d, du)) return 0;
   if ((flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE | TTC_LQR_FLAG_FP64_FALLBACK)) && d > 32)
     return 0;
+  if ((flags & TTC_LQR_FLAG_RESCUE_V1) && (d != 16 || du != 16)) return 0;  // the d = 16 fp64 rescue keeps them
   const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD |
                         TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH | TTC_LQR_FLAG_FP64_RESCUE |
-                        TTC_LQR_FLAG_FP64_FALLBACK | TTC_LQR_FLAG_KEEP_EXPANDED;
+                        TTC_LQR_FLAG_FP64_FALLBACK | TTC_LQR_FLAG_KEEP_EXPANDED | TTC_LQR_FLAG_RESCUE_V1;
   return (flags & ~known) ? 0 : 1;
 }
 
@@ -1064,6 +1095,11 @@ size_t ttc_lqr_compact_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, i
 size_t ttc_lqr_expanded_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du) {
   if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0) return 0;
   return kept_layout(n_tokens, heads, d, du).total;
+}
+
+size_t ttc_lqr_rescue_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du) {
+  if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0) return 0;
+  return rescue_record_bytes(n_tokens * heads, d, du);
 }
 
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {
@@ -1108,6 +1144,7 @@ int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, cons
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
   if (flags & TTC_LQR_FLAG_COMPACT_STASH) return TTC_LQR_EUNSUPPORTED;  // factored entry points only
+  if ((flags & TTC_LQR_FLAG_RESCUE_V1) && !stash) return TTC_LQR_EINVAL;
   if (n_tokens == 0) return TTC_LQR_OK;
   if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !u)
     return TTC_LQR_EINVAL;
@@ -1124,8 +1161,16 @@ int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, cons
     hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, rws, 0);
     if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
   }
+  // TTC_LQR_FLAG_RESCUE_V1: no problem has a slot until the listed fp64 rescue gives it one
+  RescueSlots rs{};
+  if (flags & TTC_LQR_FLAG_RESCUE_V1) {
+    rs = rescue_slots(stash, P, d, du);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, rs.slot_of, P, -1);
+    if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+    if (rws == nullptr) rs = RescueSlots{};
+  }
   return fwd_d(d, A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, P, heads, T, u, v1, q0,
-               stash ? kStashV1 : 0, status, s, flags, rws);
+               stash ? kStashV1 : 0, status, s, flags, rws, rs);
 }
 
 int ttc_lqr_backward(const float* A_diag, const float* B, const float* Q, const float* R_inv, const float* Q_f,
@@ -1156,6 +1201,7 @@ int backward_entry(const float* A_diag, const float* B, const float* Q, const fl
   if (n_tokens < 0 || heads <= 0 || T <= 0 || d <= 0 || du <= 0) return TTC_LQR_EINVAL;
   if (!ttc_lqr_supported_flags(d, du, flags)) return TTC_LQR_EUNSUPPORTED;
   if (flags & TTC_LQR_FLAG_COMPACT_STASH) return TTC_LQR_EUNSUPPORTED;  // factored entry points only
+  if ((flags & TTC_LQR_FLAG_RESCUE_V1) && !stash) return TTC_LQR_EINVAL;
   if (n_tokens == 0) return TTC_LQR_OK;
   const bool stable = (flags & TTC_LQR_FLAG_STABLE_BWD) != 0;
   if (!A_diag || !B || !Q || !R_inv || !Q_f || !log_gamma_A || !log_gamma_B || !log_gamma_Q || !h0 || !d_u ||
@@ -1164,11 +1210,13 @@ int backward_entry(const float* A_diag, const float* B, const float* Q, const fl
     return TTC_LQR_EINVAL;
   const float* v1s = stash;
   const float* q0s = stash ? stash + n_tokens * heads * (int64_t)d * d : nullptr;
+  const RescueSlots rs = (flags & TTC_LQR_FLAG_RESCUE_V1) ? rescue_slots(stash, n_tokens * heads, d, du)
+                                                          : RescueSlots{};
   return backward_core(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, u, d_u, n_tokens, heads,
                        d, du, T, flags, v1s, q0s, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f,
                        grad_log_gamma_A, grad_log_gamma_B, grad_log_gamma_Q, grad_h0,
                        static_cast<char*>(workspace), workspace_bytes, grad_limit, status, n_fallback,
-                       reinterpret_cast<hipStream_t>(stream));
+                       reinterpret_cast<hipStream_t>(stream), rs);
 }
 
 }  // namespace ttc

@@ -6,7 +6,7 @@ namespace ttc {
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
-                  int32_t* rescue_ws) {
+                  int32_t* rescue_ws, RescueSlots rs) {
   // the stable backward's gains at long horizons: fp64 on the matrix cores
   if (sm == STASH_GAINS && (flags & TTC_LQR_FLAG_FP64_RESCUE) &&
       !(flags & (TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_FP64_RICCATI)))
@@ -22,7 +22,7 @@ int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* 
   if (!(flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL))) {
     if (sm != STASH_GAINS && !(flags & TTC_LQR_FLAG_RICCATI_STEPS))
       return launch_fwd_d16_sym(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s,
-                                (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0, rescue_ws);
+                                (flags & TTC_LQR_FLAG_FP64_RESCUE) != 0, rescue_ws, rs);
     return launch_fwd_d16_mfma(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s);
   }
   return launch_fwd<16, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, sm, status, s, flags);
@@ -45,10 +45,11 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s, bool fp64, const int32_t* plist) {
+                  hipStream_t s, bool fp64, const int32_t* plist,
+                  const int32_t* slot_of, const double* slots) {
   if (fp64)
     return launch_ham<16, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
-                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist);
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist, slot_of, slots);
   return launch_ham<16>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
                        glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist);
 }

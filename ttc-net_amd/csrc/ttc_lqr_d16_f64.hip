@@ -27,7 +27,8 @@ int64_t resident_waves64() {
 template <int SM, bool WU>
 static int rescue64(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                     const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
-                    float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, int32_t* rescue_ws) {
+                    float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, int32_t* rescue_ws,
+                    const RescueSlots& rs) {
   if (device_cus() <= 0 || P >= ((int64_t)1 << 31)) return TTC_LQR_EUNSUPPORTED;
   const float* mark = WU ? u : st_b;
   const int64_t mstride = WU ? 16 : 256;
@@ -36,25 +37,27 @@ static int rescue64(const float* A, const float* B, const float* Q, const float*
                      rescue_ws, status);
   const int64_t waves = resident_waves64<SM, WU, true>();
   hipLaunchKernelGGL((lqr_fwd64_mfma_kernel<SM, WU, true>), dim3((unsigned)waves), dim3(64), M64::LDS_BYTES, s, A,
-                     B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, rescue_ws);
+                     B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, rescue_ws, rs.slot_of, rs.slots,
+                     rs.nslot);
   return TTC_LQR_OK;  // launch errors are the caller's to collect (hipGetLastError)
 }
 
 int launch_rescue64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                        int32_t* rescue_ws) {
+                        int32_t* rescue_ws, RescueSlots rs) {
   if (P <= 0) return TTC_LQR_OK;
   if (rescue_ws == nullptr) return TTC_LQR_EINVAL;
   switch (sm) {
     case STASH_NONE:
-      return rescue64<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, rescue_ws);
+      return rescue64<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, rescue_ws,
+                                        RescueSlots{});
     case STASH_V1:
       if (u != nullptr)
         return rescue64<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s,
-                                        rescue_ws);
+                                        rescue_ws, rs);
       return rescue64<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s,
-                                       rescue_ws);
+                                       rescue_ws, rs);
   }
   return TTC_LQR_EINVAL;
 }

@@ -9,7 +9,7 @@ template <int SM, bool WU>
 static void launch_s16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* u, float* st_a, float* st_b, int32_t* status, hipStream_t s, bool fp64_rescue,
-                       int32_t* rescue_ws) {
+                       int32_t* rescue_ws, RescueSlots rs) {
   using G = MB<16, 4, 1, true>;
   using GT = MB<16, 4, 1, true, true>;
   const dim3 grid((unsigned)((P + G::PPW - 1) / G::PPW)), block(G::THREADS);
@@ -25,7 +25,7 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
     // listed, on the matrix cores (the LU row-layout sweep finishing any whose Cholesky breaks
     // down); without a list workspace by the row-layout sweep alone
     if (rescue_ws != nullptr && launch_rescue64_d16(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, SM,
-                                                    status, s, rescue_ws) != TTC_LQR_EUNSUPPORTED)
+                                                    status, s, rescue_ws, rs) != TTC_LQR_EUNSUPPORTED)
       return;
     launch_rescue_k<16, SM, WU, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s,
                                         rescue_ws);
@@ -44,20 +44,20 @@ static void launch_s16(const float* A, const float* B, const float* Q, const flo
 int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                       bool fp64_rescue, int32_t* rescue_ws) {
+                       bool fp64_rescue, int32_t* rescue_ws, RescueSlots rs) {
   if (P <= 0) return TTC_LQR_OK;
   switch (sm) {
     case STASH_NONE:
       launch_s16<STASH_NONE, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue,
-                                   rescue_ws);
+                                   rescue_ws, rs);
       break;
     case STASH_V1:
       if (u != nullptr)
         launch_s16<STASH_V1, true>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue,
-                                   rescue_ws);
+                                   rescue_ws, rs);
       else
         launch_s16<STASH_V1, false>(A, B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, s, fp64_rescue,
-                                    rescue_ws);
+                                    rescue_ws, rs);
       break;
     default:
       return TTC_LQR_EINVAL;

@@ -425,7 +425,8 @@ __global__ __launch_bounds__(Ham16::THREADS) __attribute__((amdgpu_waves_per_eu(
     const float E2 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(lamb - fhb))));
     const float M1 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(fh) + fabsf(lam))));
     const float M2 = __uint_as_float(group_max_u32<16>(__float_as_uint(fabsf(fhb) + fabsf(lamb))));
-    if (!(E1 <= tau * M1 && E2 <= tau * M2)) bad = 1u;
+    // an infinite magnitude (a trajectory beyond the fp32 range) fails: inf <= tau * inf would pass
+    if (!(E1 <= tau * M1 && E2 <= tau * M2 && isfinite(M1) && isfinite(M2))) bad = 1u;
   }
 
   // finish the per-problem sums: primal + adjoint lanes, then glgA over the 16 rows

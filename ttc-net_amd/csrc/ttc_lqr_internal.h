@@ -12,6 +12,14 @@ namespace ttc {
 // word 0), then one index per problem.
 inline size_t rescue_ws_bytes(int64_t P) { return (size_t)(64 + (P > 0 ? P : 0)) * sizeof(int32_t); }
 
+// TTC_LQR_FLAG_RESCUE_V1: where the d = 16 fp64 rescue keeps the fp64 V_1 and Quu_0 of list positions
+// below nslot (slots[k]: 256 doubles of V_1, then 256 of Quu_0; slot_of[problem] = k).
+struct RescueSlots {
+  int32_t* slot_of = nullptr;
+  double* slots = nullptr;
+  int64_t nslot = 0;
+};
+
 int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s);
@@ -20,14 +28,14 @@ int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const fl
 int launch_fwd_d16_sym(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                        int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                       bool fp64_rescue, int32_t* rescue_ws = nullptr);
+                       bool fp64_rescue, int32_t* rescue_ws = nullptr, RescueSlots rs = RescueSlots{});
 // d = 16, fp64 on the matrix cores (ttc_lqr_d16_f64.hip): the rescue of the problems a symplectic
 // sweep marked (sm = STASH_NONE / STASH_V1; rescue_ws of rescue_ws_bytes(P)), and every gain
 // K_t plus Quu_0 of P problems in fp64 (the stable backward).
 int launch_rescue64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,
-                        int32_t* rescue_ws);
+                        int32_t* rescue_ws, RescueSlots rs = RescueSlots{});
 int launch_gains64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* kst, float* q0s, int32_t* status, hipStream_t s);
@@ -42,7 +50,7 @@ int launch_fwd_d64_mfma(const float* A, const float* B, const float* Q, const fl
 int launch_fwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,
-                  int32_t* rescue_ws = nullptr);
+                  int32_t* rescue_ws = nullptr, RescueSlots rs = RescueSlots{});
 int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
@@ -54,7 +62,8 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                  hipStream_t s, bool fp64, const int32_t* plist = nullptr);
+                  hipStream_t s, bool fp64, const int32_t* plist = nullptr, const int32_t* slot_of = nullptr,
+                  const double* slots = nullptr);
 int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,

@@ -848,7 +848,9 @@ __device__ __forceinline__ double rcpr(double x) { return 1.0 / x; }
 // stable path (stored gains, closed-loop costates).  grad_B / grad_Q partials go to
 // gBp / gQp for headsum_kernel, as in lqr_bwd_kernel.
 // LISTED == false: problems 0..P-1; LISTED: the P chunk-local problem indices plist[0..P-1] (the
-// problems of head groups another rollout rejected).  Every output, partial and fail_list
+// problems of head groups another rollout rejected).  fp64 and listed: a problem p with
+// slot_of[p] >= 0 reads V_1 and Quu_0 in fp64 from slots[slot_of[p]] (256 doubles each, kept by
+// the forward's fp64 rescue) instead of the fp32 v1s / q0s.  Every output, partial and fail_list
 // entry is then at the listed problem's own index, and each problem reads its token's B
 // from global memory instead of the block's LDS copy.
 // ---------------------------------------------------------------------------
@@ -866,7 +868,7 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
     float* __restrict__ gRinv, float* __restrict__ gQf, float* __restrict__ glgA, float* __restrict__ glgB,
     float* __restrict__ glgQ, float* __restrict__ gh0, float* __restrict__ gBp, float* __restrict__ gQp,
     float grad_limit, int* __restrict__ fail_list, int* __restrict__ fail_count, int* __restrict__ status,
-    const int* __restrict__ plist) {
+    const int* __restrict__ plist, const int32_t* __restrict__ slot_of, const double* __restrict__ slots) {
   using G = Geo<D>;
   extern __shared__ __align__(16) float smem_f[];
   R* const smem = reinterpret_cast<R*>(smem_f);
@@ -929,11 +931,22 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
     for (int c = 0; c < D; ++c) Qrow[c] = R(0.5) * (qg[li * D + c] + qg[c * D + li]);
   }
 
+  // the forward's fp64 V_1 / Quu_0 of this problem, where it kept them
+  int kslot = -1;
+  if constexpr (LISTED && std::is_same<R, double>::value) {
+    if (slot_of != nullptr) kslot = slot_of[p];
+  }
   // t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (pivoted elimination)
   R w_i;
   {
     R aug[D + 4];
-    ld_global_row<D>(q0s + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
+    if constexpr (LISTED && std::is_same<R, double>::value) {
+      if (kslot >= 0) ld_global_row<D>(slots + (int64_t)kslot * (2 * D * D) + D * D + li * D,
+                                      *reinterpret_cast<R(*)[D]>(aug));
+      else ld_global_row<D>(q0s + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
+    } else {
+      ld_global_row<D>(q0s + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
+    }
     aug[D] = dU[p * D + li];
     aug[D + 1] = aug[D + 2] = aug[D + 3] = R(0);
     R piv;
@@ -971,7 +984,12 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
     R hv[D], hbv[D], vrow[D];
     ld_row<D>(v0, hv);
     ld_row<D>(v1, hbv);
-    ld_global_row<D>(v1s + (p * D + li) * D, vrow);
+    if constexpr (LISTED && std::is_same<R, double>::value) {
+      if (kslot >= 0) ld_global_row<D>(slots + (int64_t)kslot * (2 * D * D) + li * D, vrow);
+      else ld_global_row<D>(v1s + (p * D + li) * D, vrow);
+    } else {
+      ld_global_row<D>(v1s + (p * D + li) * D, vrow);
+    }
     R lam = R(0), lamb = R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
@@ -1114,7 +1132,10 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
   m4 = __uint_as_float(group_max_u32<D>(__float_as_uint((float)m2)));
   // finite as stored (fp32): an fp64 rollout can leave the fp32 range while staying finite
   const unsigned bad_lane = isfinite((float)fin) ? 0u : 1u;
-  const bool ok = group_max_u32<D>(bad_lane) == 0u && E1 <= tau * m3 && E2 <= tau * m4;
+  // magnitudes beyond the fp32 range fail: an fp64 trajectory can stay finite there while both
+  // sides of the comparison round to +inf, and inf <= tau * inf would pass
+  const bool ok = group_max_u32<D>(bad_lane) == 0u && E1 <= tau * m3 && E2 <= tau * m4 && isfinite(m3) &&
+                  isfinite(m4);
   if (!valid) return;
   if (!ok) {
     if (li == 0) fail_list[atomicAdd(fail_count, 1)] = (int)p;
@@ -1405,17 +1426,18 @@ inline int launch_ham(const float* A, const float* B, const float* Q, const floa
                       const float* dU, const float* v1s, const float* q0s, int64_t P, int H, int T, float tau,
                       float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                       float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
-                      hipStream_t s, const int32_t* plist = nullptr) {
+                      hipStream_t s, const int32_t* plist = nullptr, const int32_t* slot_of = nullptr,
+                      const double* slots = nullptr) {
   if (P <= 0) return TTC_LQR_OK;
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
   if (plist != nullptr)
     hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT, true>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf,
                        lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB, glQ,
-                       gh0, gBp, gQp, limit, fail_list, fail_count, status, plist);
+                       gh0, gBp, gQp, limit, fail_list, fail_count, status, plist, slot_of, slots);
   else
     hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT, false>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R,
                        Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB,
-                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, plist);
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, plist, nullptr, nullptr);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 

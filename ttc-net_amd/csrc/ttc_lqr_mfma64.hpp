@@ -118,14 +118,20 @@ __device__ __forceinline__ double rsqrt64(double d) {
 // K_t and Quu_0 in fp64 into kstash / q0stash, no u).  LISTED: the problems are list[64 ..
 // 64 + list[0]) (the rescue list; the grid loops over it, and returns at once unless `status`
 // carries TTC_LQR_STATUS_RESCUED), else 0 .. P-1, four to a wave.
+// slots (LISTED, STASH_V1; null otherwise): list position k < nslot also keeps the problem's
+// fp64 V_1 and Quu_0 in slots[k] (2 x 256 doubles) and k in slot_of[problem], for a later
+// fp64 rollout to start from.
 template <int SM, bool WRITE_U, bool LISTED>
 __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0, int64_t P,
     int H, int T, float* __restrict__ u_out, float* __restrict__ kstash, float* __restrict__ q0stash,
-    int* __restrict__ status, const int32_t* __restrict__ list) {
+    int* __restrict__ status, const int32_t* __restrict__ list, int32_t* __restrict__ slot_of = nullptr,
+    double* __restrict__ slots = nullptr, int64_t nslot = 0) {
   constexpr int LDG = M64::LDG;
+  constexpr bool KEEP64 = LISTED && SM == STASH_V1;  // the fp64 V_1 / Quu_0 slots may be written
+  const bool keep64 = KEEP64 && slots != nullptr;
   extern __shared__ __align__(16) double sm64[];
   const int lane = threadIdx.x;
   const int g = lane >> 4, c = lane & 15;
@@ -214,9 +220,18 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
       if (SM == STASH_V1 && t == 0) {  // V_1 = -N (fp32 rows)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (vq[q])
+          if (vq[q]) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) kstash[(pq[q] * 16 + g + 4 * r) * 16 + c] = (float)(-N[q][r]);
+            if constexpr (KEEP64) {
+              if (keep64 && b0 + q < nslot) {  // and in fp64 (list position b0 + q)
+                double* sl = slots + (b0 + q) * 512;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sl[(g + 4 * r) * 16 + c] = -N[q][r];
+                if (lane == 0) slot_of[pq[q]] = (int32_t)(b0 + q);
+              }
+            }
+          }
       }
       wave_sync();
       // -W = N B_k and -Quu = B_k'(-W) - R; rows of -Quu -> T0 and T2, -W -> T1 (columns in perm4
@@ -251,6 +266,13 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
             const int64_t e = (pq[q] * 16 + g + 4 * r) * 16 + c;
             if constexpr (SM == STASH_GAINS) reinterpret_cast<double*>(q0stash)[e] = -nQ[r];
             else q0stash[e] = (float)(-nQ[r]);
+          }
+          if constexpr (KEEP64) {
+            if (keep64 && b0 + q < nslot) {
+              double* sl = slots + (b0 + q) * 512 + 256;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) sl[(g + 4 * r) * 16 + c] = -nQ[r];
+            }
           }
         }
       }

@@ -58,7 +58,7 @@ import os
 import torch
 
 from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS, \
-    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK, FLAG_KEEP_EXPANDED
+    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK, FLAG_KEEP_EXPANDED, FLAG_RESCUE_V1
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
            "check_deferred_status",
@@ -291,7 +291,11 @@ class HipLQRSolveFunc(torch.autograd.Function):
         stash_bytes = lib.ttc_lqr_stash_bytes(bs, nh, Dp, Dp, T)
         keep = (need_grad and bs > 0 and not stable_backward
                 and (policy == "always" or (policy == "auto" and _stash_fits(dev, stash_bytes))))
-        st = torch.empty(stash_bytes // 4, device=dev, dtype=torch.float32) if keep else None
+        st_bytes = stash_bytes
+        if keep and _rescue_v1(flags, Dp):  # the rescue's fp64 V_1 / Quu_0 after the stash
+            flags |= FLAG_RESCUE_V1
+            st_bytes = _align256(stash_bytes) + lib.ttc_lqr_rescue_stash_bytes(bs, nh, Dp, Dp)
+        st = torch.empty(st_bytes // 4, device=dev, dtype=torch.float32) if keep else None
         # the fp64 rescue's problem list (4 bytes a problem; long horizons only)
         fws_bytes = lib.ttc_lqr_forward_workspace_bytes(bs, nh, Dp, Dp, T, flags)
         fws = torch.empty(fws_bytes, device=dev, dtype=torch.uint8) if fws_bytes > 0 else None
@@ -401,6 +405,14 @@ def _workspace_budget(dev) -> int:
 
 def _align256(n: int) -> int:
     return (n + 255) // 256 * 256
+
+
+def _rescue_v1(flags: int, Dp: int) -> bool:
+    """Whether a forward with a stash keeps the fp64 V_1 / Quu_0 of the problems its fp64 rescue
+    recomputes (``TTC_LQR_FLAG_RESCUE_V1``, d = 16, under ``TTC_LQR_FLAG_FP64_RESCUE``): the
+    backward's fp64 second rollout tier then starts them from those instead of their fp32
+    roundings, and more of them pass its certificate (each that does skips a stable-path sweep)."""
+    return bool(flags & FLAG_FP64_RESCUE) and Dp == 16
 
 
 def _keep_expanded(dev, kind: str, stash_bytes: int, expanded_bytes: int) -> bool:
