@@ -275,9 +275,20 @@ def test_fallback_and_precision_sizing(L):
     # the backward's workspace: the main layout (with the stash: two d x d partials and a list
     # entry per problem) plus a fallback reserve of at most 256 MiB, fp32 or fp64
     P = 8000
+    # (under RESCUE at d = 16 with head groups of 8, also the third rollout tier: a list, a slot
+    # index per problem and the fp64 V_1 / Quu_0 of up to one problem in eight)
     for flags in (0, RESCUE):
         w = L.ttc_lqr_workspace_bytes(1000, 8, d, d, 64, 1, flags)
-        assert 4 * P * (2 * d * d + 1) <= w <= 4 * P * (2 * d * d + 1) + (256 << 20) + (1 << 16)
+        main = 4 * P * (2 * d * d + 1)
+        if flags == RESCUE:
+            main += 4 * P + 8 * (P // 8) * 2 * d * d
+        assert main <= w <= main + (256 << 20) + (1 << 16)
+    # the third tier needs d = du = 16 and head groups of 8
+    t3 = 4 * P + 8 * (P // 8) * 2 * d * d
+    assert (L.ttc_lqr_workspace_bytes(1000, 8, d, d, 64, 1, RESCUE) - L.ttc_lqr_workspace_bytes(1000, 8, d, d, 64, 1, 0)
+            >= t3)
+    assert (L.ttc_lqr_workspace_bytes(1000, 4, d, d, 64, 1, RESCUE) - L.ttc_lqr_workspace_bytes(1000, 4, d, d, 64, 1, 0)
+            < t3 // 2)
     # stable-path-only workspace: the stable layout for the chunk
     ws = L.ttc_lqr_workspace_bytes(10, 8, d, d, 64, 0, STABLE | FP64)
     assert ws >= 8 * 80 * 64 * (d * d + 4 * d)

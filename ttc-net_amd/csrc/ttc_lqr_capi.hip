@@ -35,6 +35,36 @@ __global__ void headsum_kernel(const float* __restrict__ part, int64_t N, int H,
 
 __global__ void set_i32_kernel(int* p, int v) { *p = v; }
 
+__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// Third rollout tier: of the n problems the fp64 tier rejected (list), those without an fp64 V_1
+// of the forward's (slot_of null, or slot_of[p] < 0) go to list3[64 + k] for k < n3 (count in
+// c3, may exceed n3), the rest to the stable path's list (count in cs).
+__global__ void tier3_split_kernel(const int* __restrict__ list, int64_t n, const int32_t* __restrict__ slot_of,
+                                   int32_t* __restrict__ list3, int64_t n3, int32_t* c3, int32_t* __restrict__ stable,
+                                   int32_t* cs) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int32_t p = list[e];
+  if (slot_of == nullptr || slot_of[p] < 0) {
+    const int32_t k = atomicAdd(c3, 1);
+    if (k < n3) {
+      list3[64 + k] = p;
+      return;
+    }
+  }
+  stable[atomicAdd(cs, 1)] = p;
+}
+
+// list3[0] = the third tier's problem count, min(c3, n3)
+__global__ void tier3_close_kernel(const int32_t* c3, int64_t n3, int32_t* list3) {
+  const int32_t c = *c3;
+  list3[0] = c < n3 ? c : (int32_t)n3;
+}
+
 // The nine inputs and d_u of the listed problems (chunk-local indices), gathered into
 // contiguous arrays of `cnt` one-head problems (the head-shared B and Q are copied per
 // problem), so the stable path can recompute them as cnt tokens with H = 1.
@@ -342,8 +372,9 @@ static int64_t fp64_round_problems(int d) {
 constexpr size_t kFallbackReserve = (size_t)256 << 20;
 
 struct FastLayout {
-  size_t v1, q0, gBp, gQp, gBg, gQg, list, glist, plist, cnt, fb, total;
-  int64_t F;  // fallback capacity within the reserve
+  size_t v1, q0, gBp, gQp, gBg, gQg, list, glist, plist, cnt, l3, so3, sl3, fb, total;
+  int64_t F;   // fallback capacity within the reserve
+  int64_t n3;  // problems the third rollout tier can take (0: no third tier)
 };
 
 // The fast path rolls head groups of 8 on the matrix cores in fp32 (H % 8 == 0), else one
@@ -357,6 +388,16 @@ static bool head_group_path(int H, int flags, int d) {
 // of the groups it rejects are rolled again one by one in fp64 on the row layout, and only
 // those that rollout rejects take the stable path.
 static bool two_tier_path(int H, int flags, int d) { return head_group_path(H, flags, d) && fp64_rollout(flags, d); }
+
+// At d = du = 16 a third tier follows: the problems the fp64 rollout rejects that started from
+// the fp32 stash's V_1 get an fp64 V_1 / Quu_0 from an fp64 sweep on the matrix cores and are
+// rolled once more from it, up to one problem in eight of the chunk (the rest of them, and
+// whatever that rollout rejects, take the stable path).
+static int64_t tier3_problems(int64_t Pc, int H, int flags, int d, int du) {
+  if (!two_tier_path(H, flags, d) || d != 16 || du != 16) return 0;
+  const int64_t s = Pc / 8 > 64 ? Pc / 8 : 64;
+  return s < Pc ? s : Pc;
+}
 
 static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T, bool with_stash, int flags) {
   const bool fp64 = fp64_stable(flags, d);
@@ -388,8 +429,15 @@ static FastLayout fast_layout(int64_t chunk_tokens, int H, int d, int du, int T,
   off += tiers ? align256(Pc / 8 * sizeof(int32_t)) : 0;
   L.plist = off;
   off += tiers ? align256(Pc * sizeof(int32_t)) : 0;
-  L.cnt = off;  // [0]: rejected problems (or groups), [1]: the second tier's rejected problems
-  off += 256;
+  L.cnt = off;  // [0]: rejected problems (or groups), [1] / [2]: the second / third tier's,
+  off += 256;   // [3]: the stable path's problems after the third tier
+  L.n3 = tier3_problems((int64_t)Pc, H, flags, d, du);
+  L.l3 = off;   // the third tier's list: count, then its problems from index 64
+  off += L.n3 > 0 ? align256((size_t)(64 + L.n3) * sizeof(int32_t)) : 0;
+  L.so3 = off;  // slot per chunk problem (-1: none)
+  off += L.n3 > 0 ? align256(Pc * sizeof(int32_t)) : 0;
+  L.sl3 = off;  // fp64 V_1 / Quu_0 per slot
+  off += align256((size_t)L.n3 * ((size_t)d * d + (size_t)du * du) * sizeof(double));
   L.fb = off;
   const int64_t cap = fallback_capacity(kFallbackReserve, d, du, T, fp64);
   L.F = (int64_t)Pc < cap ? (int64_t)Pc : cap;
@@ -483,8 +531,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     float* gQp = reinterpret_cast<float*>(ws + L.gQp);
     int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
-    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt, 0);
-    hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, s, cnt + 1, 0);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, cnt, (int64_t)4, 0);
     // a device count the host needs: one stream synchronisation
     auto read_count = [&](const int32_t* c, int64_t cap, int32_t& v) -> int {
       v = 0;
@@ -494,7 +541,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     };
     // the listed problems (nfail) recomputed by the stable path in passes of Frun, their
     // outputs and grad_B / grad_Q partials scattered to their own problem indices
-    auto stable_problems = [&](int32_t nfail) -> int {
+    auto stable_problems = [&](const int32_t* list, int32_t nfail) -> int {
       const Compact c = compact_at(ws + L.fb, Frun, d, du);
       for (int64_t f0 = 0; f0 < nfail; f0 += Frun) {
         const int64_t fc = (f0 + Frun <= nfail) ? Frun : (nfail - f0);
@@ -546,8 +593,38 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
           int32_t nfail2 = 0;
           rc = read_count(cnt + 1, np, nfail2);
           if (rc != TTC_LQR_OK) return rc;
-          total_fb += nfail2;
-          rc = stable_problems(nfail2);
+          const int32_t* slist = list;  // the stable path's problems
+          int32_t nstable = nfail2;
+          if (L.n3 > 0 && nfail2 > 0) {
+            // third tier: those that started from the fp32 V_1 get an fp64 one and roll again;
+            // the stable path's list goes to plist (free once the second tier has run)
+            int32_t* list3 = reinterpret_cast<int32_t*>(ws + L.l3);
+            int32_t* so3 = reinterpret_cast<int32_t*>(ws + L.so3);
+            double* sl3 = reinterpret_cast<double*>(ws + L.sl3);
+            hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((Pc + 255) / 256)), dim3(256), 0, s, so3, Pc, -1);
+            hipLaunchKernelGGL(tier3_split_kernel, dim3((unsigned)((nfail2 + 255) / 256)), dim3(256), 0, s, list,
+                               (int64_t)nfail2, rs.slot_of ? rs.slot_of + p0 : nullptr, list3, L.n3, cnt + 2, plist,
+                               cnt + 3);
+            hipLaunchKernelGGL(tier3_close_kernel, dim3(1), dim3(1), 0, s, cnt + 2, L.n3, list3);
+            if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+            rc = launch_v1slots64_d16(a, b, q, r, qf, la, lb, lq, hz, H, T, list3,
+                                      nfail2 < L.n3 ? (int64_t)nfail2 : L.n3, so3, sl3, L.n3, s);
+            if (rc != TTC_LQR_OK) return rc;
+            int32_t n3 = 0;
+            rc = read_count(list3, L.n3, n3);
+            if (rc != TTC_LQR_OK) return rc;
+            if (n3 > 0) {
+              rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, n3, H, T, tau, gA, gR, gQf, glA,
+                                  glB, glQ, gh, gBp, gQp, grad_limit, plist, cnt + 3, status, s, true, list3 + 64, so3,
+                                  sl3);
+              if (rc != TTC_LQR_OK) return rc;
+            }
+            rc = read_count(cnt + 3, nfail2, nstable);
+            if (rc != TTC_LQR_OK) return rc;
+            slist = plist;
+          }
+          total_fb += nstable;
+          rc = stable_problems(slist, nstable);
           if (rc != TTC_LQR_OK) return rc;
           rc = launch_groupsum(glist, nfail, gBp, (int)(d * du), gBg, grad_limit, direct ? status : nullptr, s);
           if (rc != TTC_LQR_OK) return rc;
@@ -594,7 +671,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     rc = read_count(cnt, Pc, nfail);
     if (rc != TTC_LQR_OK) return rc;
     total_fb += nfail;
-    rc = stable_problems(nfail);
+    rc = stable_problems(list, nfail);
     if (rc != TTC_LQR_OK) return rc;
     rc = launch_headsum(gBp, nc, H, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
     if (rc != TTC_LQR_OK) return rc;
@@ -656,11 +733,6 @@ static RescueSlots rescue_slots(const float* stash, int64_t P, int d, int du) {
   rs.slots = reinterpret_cast<double*>(base + align256((size_t)P * sizeof(int32_t)));
   rs.nslot = rescue_nslot(P);
   return rs;
-}
-
-__global__ void fill_i32_kernel(int32_t* p, int64_t n, int32_t v) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
 }
 
 // The expanded arrays of a KEEP_EXPANDED stash buffer.

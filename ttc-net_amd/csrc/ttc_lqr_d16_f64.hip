@@ -8,11 +8,11 @@ namespace ttc {
 namespace {
 
 // Waves of the fp64 matrix-core kernel resident on the device (one per block).
-template <int SM, bool WU, bool LISTED>
+template <int SM, bool WU, bool LISTED, bool SYMP = false>
 int64_t resident_waves64() {
   const int cus = device_cus();
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, lqr_fwd64_mfma_kernel<SM, WU, LISTED>, 64,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, lqr_fwd64_mfma_kernel<SM, WU, LISTED, SYMP>, 64,
                                                    M64::LDS_BYTES) != hipSuccess ||
       per_cu <= 0)
     per_cu = 4;
@@ -60,6 +60,26 @@ int launch_rescue64_d16(const float* A, const float* B, const float* Q, const fl
                                        rescue_ws, rs);
   }
   return TTC_LQR_EINVAL;
+}
+
+// fp64 V_1 and Quu_0 of listed problems by the fp64 symplectic sweep on the matrix cores: list[0]
+// (on the device) is their count, at most max_list, and list[64 + k] problem k; the values of a
+// problem that passes the sweep's certificate go to slots[k] (2 x 256 doubles) and k to
+// slot_of[problem] (the others keep slot_of -1).  Nothing else is written.  The backward's third
+// rollout tier.
+int launch_v1slots64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                         const float* lA, const float* lB, const float* lQ, const float* h0, int H, int T,
+                         const int32_t* list, int64_t max_list, int32_t* slot_of, double* slots, int64_t nslot,
+                         hipStream_t s) {
+  if (max_list <= 0) return TTC_LQR_OK;
+  if (device_cus() <= 0) return TTC_LQR_EUNSUPPORTED;
+  // the kernel takes ceil(count / waves) problems per wave (at most four)
+  const int64_t res = resident_waves64<STASH_V1, false, true, true>();
+  const int64_t waves = max_list < res ? max_list : res;
+  hipLaunchKernelGGL((lqr_fwd64_mfma_kernel<STASH_V1, false, true, true>), dim3((unsigned)waves), dim3(64),
+                     M64::LDS_BYTES, s, A, B, Q, R, Qf, lA, lB, lQ, h0, max_list, H, T, nullptr, nullptr, nullptr,
+                     nullptr, list, slot_of, slots, nslot);
+  return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
 // Every gain K_t [P,T,16,16] and Quu_0 [P,16,16] in fp64 (the stable backward), on the matrix

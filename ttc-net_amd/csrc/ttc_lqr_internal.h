@@ -39,6 +39,12 @@ int launch_rescue64_d16(const float* A, const float* B, const float* Q, const fl
 int launch_gains64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                        const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                        float* kst, float* q0s, int32_t* status, hipStream_t s);
+// the fp64 V_1 / Quu_0 of listed problems into slots (list[0] their count, list[64 + k] the
+// problems; the backward's third rollout tier)
+int launch_v1slots64_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
+                         const float* lA, const float* lB, const float* lQ, const float* h0, int H, int T,
+                         const int32_t* list, int64_t max_list, int32_t* slot_of, double* slots, int64_t nslot,
+                         hipStream_t s);
 int launch_fwd_d32_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                         const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H,
                         int T, float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s,

@@ -114,14 +114,35 @@ __device__ __forceinline__ double rsqrt64(double d) {
   return rs;
 }
 
+// max over the 16 lanes of a problem's row group (non-negative values)
+__device__ __forceinline__ double gmax16d(double v) {
+  v = fmax(v, __shfl_xor(v, 8, 64));
+  v = fmax(v, __shfl_xor(v, 4, 64));
+  v = fmax(v, __shfl_xor(v, 2, 64));
+  return fmax(v, __shfl_xor(v, 1, 64));
+}
+
+// Certificate of the fp64 symplectic sweep (SYMP): V_1 = Y1^{-1} Y2 is accepted when the pivot
+// estimate ||Y1||_inf / min|u_kk| of cond(Y1) (LU with partial pivoting) is at most
+// kSym64CondMax and max|V_1 - V_1'| <= kSym64AsymMax max|V_1|.  In an fp64 emulation of 5b-scale
+// problems (T = 1,024) the accepted ones (estimates up to 2e8, asymmetries up to 1.3e-13) had V_1
+// within 1.2e-13 of the fp64 Riccati sweep's; every inaccurate one had an estimate of 8e11 or
+// more and an asymmetry of 2.5e-9 or more.
+constexpr double kSym64CondMax = 1.0e10;
+constexpr double kSym64AsymMax = 1.0e-11;
+
 // SM: STASH_NONE (u), STASH_V1 (V_1 and Quu_0 in fp32, u when WRITE_U) or STASH_GAINS (every
 // K_t and Quu_0 in fp64 into kstash / q0stash, no u).  LISTED: the problems are list[64 ..
 // 64 + list[0]) (the rescue list; the grid loops over it, and returns at once unless `status`
 // carries TTC_LQR_STATUS_RESCUED), else 0 .. P-1, four to a wave.
 // slots (LISTED, STASH_V1; null otherwise): list position k < nslot also keeps the problem's
 // fp64 V_1 and Quu_0 in slots[k] (2 x 256 doubles) and k in slot_of[problem], for a later
-// fp64 rollout to start from.
-template <int SM, bool WRITE_U, bool LISTED>
+// fp64 rollout to start from.  Under STASH_V1 a null kstash / q0stash skips the fp32 copies (the
+// backward's sweep for its own slots, which leaves the forward's stash as it is).
+// SYMP: steps T-1 .. 1 as the symplectic sweep in fp64 instead (below), its certificate per
+// problem, then step 0 as above from V_1; a problem that misses the certificate stores nothing
+// (no u, stash or slot).
+template <int SM, bool WRITE_U, bool LISTED, bool SYMP = false>
 __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
     const float* __restrict__ A_diag, const float* __restrict__ Bg, const float* __restrict__ Qg,
     const float* __restrict__ Rinv, const float* __restrict__ Qf, const float* __restrict__ lgA,
@@ -199,11 +220,168 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
       nR[q] = -1.0 / (double)Rinv[pq[q] * 16 + c];
     }
 
+    // SYMP: steps T-1 .. 1 by the symplectic recursion (the reference's symplectic_iter.py:226-251,
+    // here in fp64 on the matrix cores), V_t = Y1^{-1} Y2 with Y1_T = I, Y2_T = Q_f.  The registers
+    // hold Y-hat = Y' in the C layout: Y1' in Y1, Y2' as -N.  With B_k = B diag(beta_t), per step
+    //   M = R^{-1} B_k' Y2'            4 MFMA (B' N, rows scaled by -beta^2 R_inv)
+    //   Y1' <- A^{-1} (Y1' + B_k M)    4 MFMA
+    //   Y2' <- A Y2' + Qc Y1'          4 MFMA
+    // and every 8 steps each column of Y-hat (a row of Y, which leaves Y1^{-1} Y2 unchanged) is
+    // rescaled by a power of 2.  Then V_1 from the rows [Y1 | -Y2] by LU with partial pivoting,
+    // its certificate, and N = sym(-V_1) for step 0.
+    bool acc[4] = {true, true, true, true};
+    if constexpr (SYMP) {
+      if (T > 1) {
+        double Bt[4][4];  // B[c][g + 4s]: the A operand of B_k M
+        v4d Y1[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float* bq = Bg + (pq[q] / H) * 256;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) Bt[q][s] = bq[c * 16 + g + 4 * s];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Y1[q][r] = (g + 4 * r == c) ? 1.0 : 0.0;
+        }
+        const double rinv_c = (double)Rinv[pg * 16 + c];
+        for (int t = T - 1; t >= 1; --t) {
+          {
+            const double tp1 = (double)(t + 1);
+            const double al = fma(a_c, exp(lgA_g * tp1), 1.0);
+            const double be = exp(lgB_c * tp1);
+            const double qv = exp(lgQ_c * (double)t);
+            double* v = VV(g);
+            v[pc] = al;
+            v[16 + pc] = 1.0 / al;
+            v[32 + c] = qv;
+            v[48 + pc] = qv;
+            v[64 + pc] = -(be * be) * rinv_c;
+          }
+          wave_sync();
+          const bool renorm = (T - 1 - t) % 8 == 7;
+          // phase by phase over the wave's problems: each phase's products are independent of
+          // one another, so the matrix core runs one problem's while the next is scaled
+          v4d M[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {  // B' N: A operand B'[c][g + 4s] = B[g + 4s][c] (Bo)
+            if (q >= ppw) break;  // uniform
+            M[q] = v4d{0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) M[q] = mfma64(Bo[q][s], N[q][s], M[q]);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {  // M = R^{-1} B_k' Y2' (rows g + 4r); Y1' += B M
+            if (q >= ppw) break;  // uniform
+            double nbr[4];
+            ld_row<4>(VV(q) + 64 + 4 * g, nbr);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) M[q][r] *= nbr[r];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) Y1[q] = mfma64(Bt[q][s], M[q][s], Y1[q]);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {  // Y1' <- A^{-1} Y1'; -Y2' <- A (-Y2') - Qc Y1'
+            if (q >= ppw) break;  // uniform
+            const double* v = VV(q);
+            double alr[4], iar[4], qr[4];
+            ld_row<4>(v + 4 * g, alr);
+            ld_row<4>(v + 16 + 4 * g, iar);
+            ld_row<4>(v + 48 + 4 * g, qr);
+            const double q_c = v[32 + c];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              Y1[q][r] *= iar[r];
+              N[q][r] *= alr[r];
+            }
+            // A operand -Qc[c][g + 4s] = q_c (-sym Q)[g + 4s][c] q_{g + 4s}
+            double op[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) op[s] = Qo[q][s] * (q_c * qr[s]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) N[q] = mfma64(op[s], Y1[q][s], N[q]);
+          }
+          if (renorm) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if (q >= ppw) break;  // uniform
+              double mk = 0.0;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) mk = fmax(mk, fmax(fabs(Y1[q][r]), fabs(N[q][r])));
+              mk = fmax(mk, __shfl_xor(mk, 16, 64));
+              mk = fmax(mk, __shfl_xor(mk, 32, 64));
+              const int e = 1 - __builtin_amdgcn_frexp_exp(mk);  // mk 2^e in [1, 2)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                Y1[q][r] = __builtin_amdgcn_ldexp(Y1[q][r], e);
+                N[q][r] = __builtin_amdgcn_ldexp(N[q][r], e);
+              }
+            }
+          }
+          wave_sync();
+        }
+        // rows of Y1 (columns of Y1') -> T0, of -Y2 -> T1; group g solves its problem's rows
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            T0(q)[c * LDG + g + 4 * r] = Y1[q][r];
+            T1(q)[c * LDG + g + 4 * r] = N[q][r];
+          }
+        wave_sync();
+        double aug[32];
+        {
+          double y1r[16], y2r[16];
+          ld_row<16>(T0(g) + c * LDG, y1r);
+          ld_row<16>(T1(g) + c * LDG, y2r);
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            aug[k] = y1r[k];
+            aug[16 + k] = y2r[k];
+          }
+        }
+        double rs = 0.0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) rs += fabs(aug[k]);
+        const double n1 = gmax16d(rs);  // ||Y1||_inf
+        double piv;
+        int pos;
+        solve_rows<16, 32>(aug, c, T2(g), piv, pos);  // row pos of Y1^{-1}(-Y2) = -V_1
+        double ukk = 0.0;  // U[pos][pos], left in place by the back substitution
+#pragma unroll
+        for (int k = 0; k < 16; ++k) ukk = (pos == k) ? aug[k] : ukk;
+        const double n2 = gmax16d(fabs(1.0 / ukk));
+        double xr[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) xr[k] = aug[16 + k];
+        wave_sync();
+        st_row<16>(T0(g) + pos * LDG, xr);
+        wave_sync();
+        double da = 0.0, mx = 0.0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          da = fmax(da, fabs(xr[k] - T0(g)[k * LDG + pos]));
+          mx = fmax(mx, fabs(xr[k]));
+        }
+        da = gmax16d(da);
+        mx = gmax16d(mx);
+        // false on NaN; fmax drops NaN operands, so the finiteness of the magnitudes is tested too
+        const bool ok = n1 * n2 <= kSym64CondMax && da <= kSym64AsymMax * mx && isfinite(mx) && isfinite(n1);
+        const unsigned long long bal = __ballot(ok);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          acc[q] = ((bal >> (16 * q)) & 1ull) != 0ull;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) N[q][r] = 0.5 * (T0(q)[(g + 4 * r) * LDG + c] + T0(q)[c * LDG + g + 4 * r]);
+        }
+        wave_sync();
+      }
+    }
+    const bool accg = g == 0 ? acc[0] : (g == 1 ? acc[1] : (g == 2 ? acc[2] : acc[3]));
+
     // The discounts are exact exponentials at every step.  (By one-step multiplications with an
     // exact refresh every 8 steps -- ~1e-15 relative -- the undiscounted config-5b fixture's
     // A_diag / B gradients moved from 3.6e-4 / 2.1e-2 to 8.2e-3 / 6.5e-2 against its 40-digit
     // answer: those problems amplify the discounts' last bits.)
-    for (int t = T - 1; t >= 0; --t) {
+    for (int t = SYMP ? 0 : T - 1; t >= 0; --t) {
       {
         const double tp1 = (double)(t + 1);
         const double eA = exp(lgA_g * tp1);
@@ -217,12 +395,14 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
         v[48 + pc] = qv;
         v[64 + c] = be;
       }
-      if (SM == STASH_V1 && t == 0) {  // V_1 = -N (fp32 rows)
+      if (SM == STASH_V1 && t == 0) {  // V_1 = -N (fp32 rows, unless kstash is null)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-          if (vq[q]) {
+          if (vq[q] && acc[q]) {
+            if (kstash != nullptr) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) kstash[(pq[q] * 16 + g + 4 * r) * 16 + c] = (float)(-N[q][r]);
+              for (int r = 0; r < 4; ++r) kstash[(pq[q] * 16 + g + 4 * r) * 16 + c] = (float)(-N[q][r]);
+            }
             if constexpr (KEEP64) {
               if (keep64 && b0 + q < nslot) {  // and in fp64 (list position b0 + q)
                 double* sl = slots + (b0 + q) * 512;
@@ -260,12 +440,12 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
           t2[c * LDG + g + 4 * r] = nQ[r];
           t1[(g + 4 * r) * LDG + pc] = nW[r];
         }
-        if (SM != STASH_NONE && t == 0 && vq[q]) {  // Quu_0
+        if (SM != STASH_NONE && t == 0 && vq[q] && acc[q]) {  // Quu_0
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int64_t e = (pq[q] * 16 + g + 4 * r) * 16 + c;
             if constexpr (SM == STASH_GAINS) reinterpret_cast<double*>(q0stash)[e] = -nQ[r];
-            else q0stash[e] = (float)(-nQ[r]);
+            else if (q0stash != nullptr) q0stash[e] = (float)(-nQ[r]);
           }
           if constexpr (KEEP64) {
             if (keep64 && b0 + q < nslot) {
@@ -447,8 +627,8 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
 #pragma unroll
       for (int j = 0; j < 16; ++j) sacc = fma(xr[j], hv[j], sacc);
       const float u0 = (float)(-sacc);
-      if (vg) u_out[pg * 16 + c] = u0;
-      if (status != nullptr && vg && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
+      if (vg && accg) u_out[pg * 16 + c] = u0;
+      if (status != nullptr && vg && accg && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
     }
     wave_sync();  // the next batch rewrites the tiles
   }
