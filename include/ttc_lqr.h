@@ -123,6 +123,14 @@ extern "C" {
  * Pass the same flag and buffer to both calls; NULL stash with this flag: TTC_LQR_EINVAL.  Same
  * results to the certificate's tolerance. */
 #define TTC_LQR_FLAG_RESCUE_V1 256
+/* TTC_LQR_FLAG_RESCUE_GAINS (with TTC_LQR_FLAG_RESCUE_V1): the forward's fp64 rescue also keeps
+ * every gain K_t (fp64) of the problems in its first G = min(S, max(64, P / 16)) slots (S as
+ * below), after the TTC_LQR_FLAG_RESCUE_V1 record, and the backward's stable path reads them
+ * instead of sweeping those problems again.  The stash buffer is then
+ * align256(ttc_lqr_stash_bytes) + ttc_lqr_rescue_stash_bytes + ttc_lqr_rescue_gains_bytes bytes
+ * (2 MB per kept problem at d = 16, T = 1024).  Pass the same flag and buffer to both calls.
+ * Same results to the rounding of the fp64 sweep (the same kernel). */
+#define TTC_LQR_FLAG_RESCUE_GAINS 512
 
 /* Relative tolerance of the backward's certificate: a problem's Hamiltonian rollout is
  * accepted when |lambda_T - Q_f h_T| <= TOL * (|Q_f h_T| + |lambda_T|) (max norms) holds
@@ -157,6 +165,10 @@ size_t ttc_lqr_expanded_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_
 /* Bytes that TTC_LQR_FLAG_RESCUE_V1 keeps after the stash: align256(4 P) + align256(8 S (d d +
  * du du)) for P = N * H problems and S = min(P, max(64, P / 8)) slots. */
 size_t ttc_lqr_rescue_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du);
+
+/* Bytes that TTC_LQR_FLAG_RESCUE_GAINS keeps after that record: align256(8 G T du d) with
+ * G = min(S, max(64, P / 16)). */
+size_t ttc_lqr_rescue_gains_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T);
 
 /* Workspace bytes ttc_lqr_backward needs to process `chunk_tokens` tokens per pass
  * (it loops over the tokens in chunks of that size) with these `flags` (the stable path's

@@ -32,6 +32,7 @@ def test_header_declares_expected_entry_points():
         "ttc_lqr_backward", "ttc_lqr_forward", "ttc_lqr_stash_bytes", "ttc_lqr_strerror",
         "ttc_lqr_supported", "ttc_lqr_supported_flags", "ttc_lqr_version", "ttc_lqr_workspace_bytes",
         "ttc_lqr_compact_stash_bytes", "ttc_lqr_expanded_bytes", "ttc_lqr_rescue_stash_bytes",
+        "ttc_lqr_rescue_gains_bytes",
         "ttc_lqr_factored_workspace_bytes", "ttc_lqr_forward_factored", "ttc_lqr_backward_factored",
         "ttc_lqr_forward_factored_bf16", "ttc_lqr_backward_factored_bf16", "ttc_lqr_rescale",
         "ttc_lqr_rescale_backward", "ttc_lqr_forward_host", "ttc_lqr_backward_host", "ttc_lqr_fallback_bytes",
@@ -65,7 +66,7 @@ def test_supported_flags(L):
     assert L.ttc_lqr_supported_flags(64, 64, 1) == 0 and L.ttc_lqr_supported_flags(64, 64, 0) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 4) == 1 and L.ttc_lqr_supported_flags(64, 64, 4 | 2) == 1
     assert L.ttc_lqr_supported_flags(16, 16, 8) == 1 and L.ttc_lqr_supported_flags(32, 32, 8 | 4) == 1
-    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 512) == 0
+    assert L.ttc_lqr_supported_flags(64, 64, 16) == 1 and L.ttc_lqr_supported_flags(16, 16, 1024) == 0
     assert L.ttc_lqr_supported_flags(64, 64, 128 | 16) == 1  # TTC_LQR_FLAG_KEEP_EXPANDED, any d
     # TTC_LQR_FLAG_FP64_FALLBACK (64) needs the fp64 kernels: d <= 32
     assert L.ttc_lqr_supported_flags(16, 16, 64) == 1 and L.ttc_lqr_supported_flags(32, 32, 64) == 1
@@ -236,6 +237,29 @@ def test_rescue_v1_sizing_and_validation(L):
     assert L.ttc_lqr_backward(*([p] * 11), 1, 1, 16, 16, 4, 256 | 32, None, *([p] * 9), p, 1 << 30,
                               float("inf"), None, ctypes.byref(n_fb), None) == 1
     assert L.ttc_lqr_forward_factored(*([p] * 11), 1, 1, 16, 16, 16, 16, 4, 256 | 32, p, p, p, 1 << 30,
+                                      None, None) == 2
+
+
+def test_rescue_gains_sizing_and_validation(L):
+    """TTC_LQR_FLAG_RESCUE_GAINS (512): only with TTC_LQR_FLAG_RESCUE_V1 (so d = du = 16); after
+    that record every gain K_t of G = min(S, max(64, P / 16)) slots in fp64, T x du x d each,
+    256-byte aligned; the factored entry points do not take it."""
+    a = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    assert L.ttc_lqr_supported_flags(16, 16, 512 | 256 | 32) == 1
+    assert L.ttc_lqr_supported_flags(16, 16, 512 | 32) == 0          # without the slots
+    assert L.ttc_lqr_supported_flags(32, 32, 512 | 256 | 32) == 0
+    for n, h, T in ((1000, 8, 1024), (3, 2, 5), (20, 8, 64), (32768, 8, 1024)):
+        P = n * h
+        S = min(P, max(64, P // 8))
+        G = min(S, max(64, P // 16))
+        assert L.ttc_lqr_rescue_gains_bytes(n, h, 16, 16, T) == a(8 * G * T * 256)
+    # config 5b: 16,384 kept problems of 2 MB each
+    assert L.ttc_lqr_rescue_gains_bytes(32768, 8, 16, 16, 1024) == 16384 * 1024 * 256 * 8
+    assert L.ttc_lqr_rescue_gains_bytes(-1, 8, 16, 16, 4) == 0 and L.ttc_lqr_rescue_gains_bytes(1, 8, 16, 16, 0) == 0
+    p = ctypes.c_void_p(16)
+    assert _fwd(L, flags=512 | 32) == 2                       # unsupported without 256
+    assert _fwd(L, flags=512 | 256 | 32) == 1                 # no stash
+    assert L.ttc_lqr_forward_factored(*([p] * 11), 1, 1, 16, 16, 16, 16, 4, 512 | 256 | 32, p, p, p, 1 << 30,
                                       None, None) == 2
 
 

@@ -352,6 +352,77 @@ def test_rescue_v1_slots_cut_the_stable_path(monkeypatch):
     assert outs[True]["_fallback"] < outs[False]["_fallback"]
 
 
+def test_rescue_gains_are_the_oracle_gains():
+    """TTC_LQR_FLAG_RESCUE_GAINS (with _RESCUE_V1, _FP64_RESCUE) at T = 1024 on config-5b token
+    scales, through the C ABI: the forward's fp64 rescue keeps every gain K_t of the problems in
+    its first slots, after the fp64 V_1 / Quu_0 record.  Each kept problem's gains are the fp64
+    oracle's (the Riccati sweep, lin_solver_lqr.py:155-185) to 1e-6 of its largest gain, at every
+    step; problems without a slot are the ones the symplectic sweep accepted."""
+    from ttc.solvers._lib import FLAG_FP64_RESCUE, FLAG_RESCUE_GAINS, FLAG_RESCUE_V1, lib
+    from oracle.lqr64 import _riccati
+    ins = [t.float().contiguous() for t in layer_solver_inputs("5b", make_x("5b", n_tokens=32, seed=3))]
+    N, H, d = ins[0].shape
+    T, P = 1024, N * H
+    flags = FLAG_FP64_RESCUE | FLAG_RESCUE_V1 | FLAG_RESCUE_GAINS
+    a256 = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    sb = lib.ttc_lqr_stash_bytes(N, H, d, d, T)
+    rec = lib.ttc_lqr_rescue_stash_bytes(N, H, d, d)
+    gb = lib.ttc_lqr_rescue_gains_bytes(N, H, d, d, T)
+    nslot = min(P, max(64, P // 8))
+    ngslot = min(nslot, max(64, P // 16))
+    assert gb == a256(8 * ngslot * T * 256)
+    dev = torch.device("cuda:0")
+    xs = [t.to(dev) for t in ins]
+    u = torch.empty(N, H, d, device=dev)
+    st = torch.zeros((a256(sb) + rec + gb) // 4, device=dev)
+    nws = lib.ttc_lqr_forward_workspace_bytes(N, H, d, d, T, flags)
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    print(f"[rescue-gains cfg5b] N={N} H={H} T={T} slots={nslot} gain slots={ngslot}", flush=True)
+    rc = lib.ttc_lqr_forward_ws(*[t.data_ptr() for t in xs], N, H, d, d, T, flags, u.data_ptr(), st.data_ptr(),
+                                ws.data_ptr(), nws, status.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0 and int(status.item()) & 4, (rc, int(status.item()))
+    raw = st.view(torch.uint8)
+    slot_of = raw[a256(sb):a256(sb) + 4 * P].view(torch.int32).cpu().numpy()
+    gains = raw[a256(sb) + rec:a256(sb) + rec + 8 * ngslot * T * 256].view(torch.float64)
+    kept = [(p, int(k)) for p, k in enumerate(slot_of) if 0 <= k < ngslot]
+    assert kept and all(k < nslot for _, k in kept) and len({k for _, k in kept}) == len(kept)
+    assert np.all((slot_of == -1) | ((slot_of >= 0) & (slot_of < nslot)))
+    K, _ = _riccati(LQRProblem(*ins, T), keep_gains=True)  # [T, P, du, d]
+    worst = 0.0
+    for p, k in kept:
+        g = gains[k * T * 256:(k + 1) * T * 256].view(T, 16, 16).cpu().numpy()
+        ref = K[:, p]
+        worst = max(worst, float(np.abs(g - ref).max() / np.abs(ref).max()))
+    print(f"   kept {len(kept)} problems: worst gain error {worst:.1e}", flush=True)
+    assert worst <= 1e-6
+
+
+def test_rescue_gains_read_by_the_stable_path(monkeypatch):
+    """Config-5b token scales, T = 1024, 64 tokens: with and without the forward's kept fp64 gains
+    (TTC_LQR_FLAG_RESCUE_GAINS), u and all nine gradients agree with the fp64 oracle, and the same
+    number of problems takes the stable path (the gains change how it gets them, not who needs
+    them; the rescue list's atomic order may move one or two)."""
+    import ttc.solvers.hip_lqr as hl
+    ins = layer_solver_inputs("5b", make_x("5b", n_tokens=64, seed=3))
+    T = 1024
+    pb = LQRProblem(*ins, T)
+    dU = torch.randn(pb.N, pb.H, pb.du, generator=torch.Generator().manual_seed(8)).double().numpy()
+    ref = solve_grads(pb, dU)
+    fb = {}
+    for on in (False, True):
+        monkeypatch.setattr(hl, "_keep_rescue_gains", lambda dev, policy, nbytes, on=on: on)
+        print(f"[rescue-gains cfg5b T={T} kept={on}]", flush=True)
+        out = run_hip(ins, T, dU, grad_limit=math.inf)
+        errs = {k: _relerr(out[k], ref[k]) for k in ["u"] + NAMES}
+        print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()) + f"  fallback={out['_fallback']}",
+              flush=True)
+        assert all(v <= TOL for v in errs.values()), errs
+        fb[on] = out["_fallback"]
+    assert fb[True] > 0 and abs(fb[True] - fb[False]) <= 2, fb
+
+
 @pytest.mark.parametrize("slots", [False, True])
 def test_certificate_rejects_trajectories_beyond_fp32(slots, monkeypatch):
     """Config-5b token 29207 (of the 32,768-token sample, seed 3), T = 1024: started from the

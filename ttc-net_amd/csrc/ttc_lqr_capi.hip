@@ -65,12 +65,33 @@ __global__ void tier3_close_kernel(const int32_t* c3, int64_t n3, int32_t* list3
   list3[0] = c < n3 ? c : (int32_t)n3;
 }
 
+// The stable path's n problems (list) reordered into out[0 .. n): first those whose gains the
+// forward did not keep (count in cr), then those it kept, with a slot below ngslot (count in ck).
+__global__ void kept_split_kernel(const int* __restrict__ list, int64_t n, const int32_t* __restrict__ slot_of,
+                                  int64_t ngslot, int32_t* __restrict__ out, int32_t* ck, int32_t* cr) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int32_t p = list[e];
+  const int32_t k = slot_of[p];
+  if (k >= 0 && k < ngslot) out[n - 1 - atomicAdd(ck, 1)] = p;
+  else out[atomicAdd(cr, 1)] = p;
+}
+
+// Slots of the listed problems list[base + i], i < n, whose gains are kept: -1 for the first
+// nrest of the list (swept), slot_of[problem] for the others.
+__global__ void gather_slot_kernel(const int* __restrict__ list, int64_t base, int64_t n, int64_t nrest,
+                                   const int32_t* __restrict__ slot_of, int32_t* __restrict__ gi) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) gi[i] = (base + i < nrest) ? -1 : slot_of[list[base + i]];
+}
+
 // The nine inputs and d_u of the listed problems (chunk-local indices), gathered into
 // contiguous arrays of `cnt` one-head problems (the head-shared B and Q are copied per
 // problem), so the stable path can recompute them as cnt tokens with H = 1.
 struct Compact {
   float *A, *B, *Q, *R, *Qf, *lA, *lB, *lQ, *h0, *dU;               // inputs
   float *gA, *gB, *gQ, *gR, *gQf, *glA, *glB, *glQ, *gh0;            // gradients
+  int32_t* gi;  // TTC_LQR_FLAG_RESCUE_GAINS: each problem's slot of kept gains
 };
 
 __device__ __forceinline__ void copy_span(float* __restrict__ dst, const float* __restrict__ src, int n) {
@@ -274,8 +295,14 @@ static int stable_backward(const float* A, const float* B, const float* Q, const
                            const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                            int64_t n_tokens, int H, int d, int T, int flags, float* gA, float* gB, float* gQ,
                            float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, char* ws,
-                           size_t ws_bytes, float limit, float sum_limit, int32_t* status, hipStream_t s) {
+                           size_t ws_bytes, float limit, float sum_limit, int32_t* status, hipStream_t s,
+                           const int32_t* gidx = nullptr, const double* gsl = nullptr,
+                           const double* q0sl = nullptr, int64_t nsweep = -1) {
+  // gidx (d = 16, fp64): a problem p with gidx[p] >= 0 has the gains and Quu_0 the forward
+  // rescue kept in slot gidx[p] (gsl, q0sl); the sweep then runs over the first nsweep problems
+  // only (the others must all have one)
   const bool fp64 = fp64_stable(flags, d);
+  if (gidx != nullptr && (d != 16 || !fp64)) return TTC_LQR_EINVAL;
   if (ws_bytes < stable_layout(1, H, d, T, fp64).total) return TTC_LQR_EINVAL;
   int64_t chunk = 1, hi = n_tokens;  // largest token chunk whose layout fits
   while (chunk < hi) {
@@ -292,13 +319,18 @@ static int stable_backward(const float* A, const float* B, const float* Q, const
     const float *la = lA + p0, *lb = lB + p0 * d, *lq = lQ + p0 * d, *hz = h0 + p0 * d, *dz = dU + p0 * d;
     float* kst = reinterpret_cast<float*>(ws + L.kst);
     float* q0s = reinterpret_cast<float*>(ws + L.q0s);
-    int rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, Pc, H, T, nullptr, kst, q0s, kStashGains, nullptr, s, flags);
-    if (rc != TTC_LQR_OK) return rc;
+    int rc = TTC_LQR_OK;
+    int64_t sw = Pc;  // problems of this chunk that the sweep takes (the leading ones)
+    if (gidx != nullptr && nsweep >= 0) sw = nsweep <= p0 ? 0 : (nsweep - p0 < Pc ? nsweep - p0 : Pc);
+    if (sw > 0) {
+      rc = fwd_d(d, a, b, q, r, qf, la, lb, lq, hz, sw, H, T, nullptr, kst, q0s, kStashGains, nullptr, s, flags);
+      if (rc != TTC_LQR_OK) return rc;
+    }
     void* traj = ws + L.traj;
     float* gBp = reinterpret_cast<float*>(ws + L.gBp);
     float* gQp = reinterpret_cast<float*>(ws + L.gQp);
     switch (d) {
-      case 16: rc = launch_bwd_d16(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, fp64, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
+      case 16: rc = launch_bwd_d16(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, fp64, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s, gidx ? gidx + p0 : nullptr, gsl, q0sl); break;
       case 32: rc = launch_bwd_d32(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, fp64, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
       case 64: rc = launch_bwd_d64(a, b, q, r, qf, la, lb, lq, hz, dz, kst, q0s, Pc, H, T, traj, fp64, gA + p0 * d, gR + p0 * d, gQf + p0 * dd, glA + p0, glB + p0 * d, glQ + p0 * d, gh0 + p0 * d, gBp, gQp, limit, status, s); break;
       default: return TTC_LQR_EUNSUPPORTED;
@@ -319,7 +351,7 @@ static size_t compact_floats(int d, int du) {  // inputs + gradients of one prob
   return in + out;
 }
 
-// The 19 compact arrays (inputs and gradients) of F gathered problems.
+// The 19 compact arrays (inputs and gradients) of F gathered problems, then a slot index each.
 static size_t compact_sizes(int64_t F64, int d, int du, size_t (&sizes)[19]) {
   const size_t F = (size_t)F64;
   const size_t v[19] = {F * d, F * d * du, F * d * d, F * du, F * d * d, F, F * du, F * d, F * d, F * du,
@@ -329,7 +361,7 @@ static size_t compact_sizes(int64_t F64, int d, int du, size_t (&sizes)[19]) {
     sizes[k] = v[k];
     total += align256(v[k] * sizeof(float));
   }
-  return total;
+  return total + align256(F * sizeof(int32_t));
 }
 
 // Bytes of the fallback region for F rejected problems: their compact inputs and gradients,
@@ -459,6 +491,7 @@ static Compact compact_at(char* base, int64_t F64, int d, int du) {
   c.lQ = ptr[7]; c.h0 = ptr[8]; c.dU = ptr[9];
   c.gA = ptr[10]; c.gB = ptr[11]; c.gQ = ptr[12]; c.gR = ptr[13]; c.gQf = ptr[14]; c.glA = ptr[15];
   c.glB = ptr[16]; c.glQ = ptr[17]; c.gh0 = ptr[18];
+  c.gi = reinterpret_cast<int32_t*>(base + off);
   return c;
 }
 
@@ -531,7 +564,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     float* gQp = reinterpret_cast<float*>(ws + L.gQp);
     int32_t* list = reinterpret_cast<int32_t*>(ws + L.list);
     int32_t* cnt = reinterpret_cast<int32_t*>(ws + L.cnt);
-    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, cnt, (int64_t)4, 0);
+    hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, s, cnt, (int64_t)6, 0);
     // a device count the host needs: one stream synchronisation
     auto read_count = [&](const int32_t* c, int64_t cap, int32_t& v) -> int {
       v = 0;
@@ -540,19 +573,29 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
       return (v < 0 || v > cap) ? TTC_LQR_ELAUNCH : TTC_LQR_OK;
     };
     // the listed problems (nfail) recomputed by the stable path in passes of Frun, their
-    // outputs and grad_B / grad_Q partials scattered to their own problem indices
-    auto stable_problems = [&](const int32_t* list, int32_t nfail) -> int {
+    // outputs and grad_B / grad_Q partials scattered to their own problem indices; kept: each
+    // has gains the forward's fp64 rescue kept (TTC_LQR_FLAG_RESCUE_GAINS), read instead of swept
+    auto stable_problems = [&](const int32_t* list, int32_t nfail, int32_t nrest) -> int {
+      // nrest >= 0: only the first nrest listed problems are swept; the others have gains the
+      // forward's fp64 rescue kept (TTC_LQR_FLAG_RESCUE_GAINS), read by the same gradient pass
+      const bool kept = nrest >= 0;
       const Compact c = compact_at(ws + L.fb, Frun, d, du);
       for (int64_t f0 = 0; f0 < nfail; f0 += Frun) {
         const int64_t fc = (f0 + Frun <= nfail) ? Frun : (nfail - f0);
         hipLaunchKernelGGL(gather_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, H, d, du, a, b, q, r, qf, la,
                            lb, lq, hz, dz, c);
+        if (kept)
+          hipLaunchKernelGGL(gather_slot_kernel, dim3((unsigned)((fc + 255) / 256)), dim3(256), 0, s, list, f0, fc,
+                             (int64_t)nrest, rs.slot_of + p0, c.gi);
         if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
-        const int rs = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags,
-                                       c.gA, c.gB, c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable,
-                                       workspace_bytes - fb_stable, grad_limit, INFINITY, status,
-                                       s);  // per-problem partials
-        if (rs != TTC_LQR_OK) return rs;
+        const int64_t sweep = !kept ? -1 : (nrest <= f0 ? 0 : (nrest - f0 < fc ? nrest - f0 : fc));
+        const int rcs = stable_backward(c.A, c.B, c.Q, c.R, c.Qf, c.lA, c.lB, c.lQ, c.h0, c.dU, fc, 1, d, T, flags,
+                                        c.gA, c.gB, c.gQ, c.gR, c.gQf, c.glA, c.glB, c.glQ, c.gh0, ws + fb_stable,
+                                        workspace_bytes - fb_stable, grad_limit, INFINITY, status,
+                                        s,  // per-problem partials
+                                        kept ? c.gi : nullptr, kept ? rs.gains : nullptr, kept ? rs.slots : nullptr,
+                                        sweep);
+        if (rcs != TTC_LQR_OK) return rcs;
         hipLaunchKernelGGL(scatter_kernel, dim3((unsigned)fc), dim3(256), 0, s, list, f0, d, du, c, gA, gR, gQf, glA,
                            glB, glQ, gh, gBp, gQp);
         if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
@@ -624,7 +667,19 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
             slist = plist;
           }
           total_fb += nstable;
-          rc = stable_problems(slist, nstable);
+          if (rs.gains != nullptr && slist == plist && nstable > 0) {
+            // the problems whose gains the forward kept skip the sweep: the list reordered into
+            // list (free once the third tier has split it), those without first
+            hipLaunchKernelGGL(kept_split_kernel, dim3((unsigned)((nstable + 255) / 256)), dim3(256), 0, s, plist,
+                               (int64_t)nstable, rs.slot_of + p0, rs.ngslot, list, cnt + 4, cnt + 5);
+            if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
+            int32_t nrest = 0;
+            rc = read_count(cnt + 5, nstable, nrest);
+            if (rc != TTC_LQR_OK) return rc;
+            rc = stable_problems(list, nstable, nrest);
+          } else {
+            rc = stable_problems(slist, nstable, -1);
+          }
           if (rc != TTC_LQR_OK) return rc;
           rc = launch_groupsum(glist, nfail, gBp, (int)(d * du), gBg, grad_limit, direct ? status : nullptr, s);
           if (rc != TTC_LQR_OK) return rc;
@@ -671,7 +726,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
     rc = read_count(cnt, Pc, nfail);
     if (rc != TTC_LQR_OK) return rc;
     total_fb += nfail;
-    rc = stable_problems(list, nfail);
+    rc = stable_problems(list, nfail, -1);
     if (rc != TTC_LQR_OK) return rc;
     rc = launch_headsum(gBp, nc, H, (int)(d * du), grad_B + n0 * d * du, grad_limit, status, s);
     if (rc != TTC_LQR_OK) return rc;
@@ -725,13 +780,29 @@ static size_t rescue_record_bytes(int64_t P, int d, int du) {
          align256((size_t)rescue_nslot(P) * ((size_t)d * d + (size_t)du * du) * sizeof(double));
 }
 
-static RescueSlots rescue_slots(const float* stash, int64_t P, int d, int du) {
+// TTC_LQR_FLAG_RESCUE_GAINS: after that record, every gain K_t [T][du][d] (fp64) of the first
+// min(S, max(64, P / 16)) slots.
+static int64_t rescue_gains_nslot(int64_t P) {
+  const int64_t g = P / 16 > 64 ? P / 16 : 64;
+  const int64_t s = rescue_nslot(P);
+  return g < s ? g : s;
+}
+
+static size_t rescue_gains_bytes(int64_t P, int d, int du, int T) {
+  return align256((size_t)rescue_gains_nslot(P) * (size_t)T * (size_t)d * du * sizeof(double));
+}
+
+static RescueSlots rescue_slots(const float* stash, int64_t P, int d, int du, int T, bool gains) {
   char* base = reinterpret_cast<char*>(const_cast<float*>(stash)) +
                align256((size_t)P * ((size_t)d * d + (size_t)du * du) * sizeof(float));
   RescueSlots rs;
   rs.slot_of = reinterpret_cast<int32_t*>(base);
   rs.slots = reinterpret_cast<double*>(base + align256((size_t)P * sizeof(int32_t)));
   rs.nslot = rescue_nslot(P);
+  if (gains) {
+    rs.gains = reinterpret_cast<double*>(base + rescue_record_bytes(P, d, du));
+    rs.ngslot = rescue_gains_nslot(P);
+  }
   return rs;
 }
 
@@ -1153,9 +1224,11 @@ int ttc_lqr_supported_flags(int32_t d, int32_t du, int32_t flags) {
   if ((flags & (TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_FP64_RESCUE | TTC_LQR_FLAG_FP64_FALLBACK)) && d > 32)
     return 0;
   if ((flags & TTC_LQR_FLAG_RESCUE_V1) && (d != 16 || du != 16)) return 0;  // the d = 16 fp64 rescue keeps them
+  if ((flags & TTC_LQR_FLAG_RESCUE_GAINS) && !(flags & TTC_LQR_FLAG_RESCUE_V1)) return 0;  // in its slots
   const int32_t known = TTC_LQR_FLAG_FP64_RICCATI | TTC_LQR_FLAG_ROW_KERNEL | TTC_LQR_FLAG_STABLE_BWD |
                         TTC_LQR_FLAG_RICCATI_STEPS | TTC_LQR_FLAG_COMPACT_STASH | TTC_LQR_FLAG_FP64_RESCUE |
-                        TTC_LQR_FLAG_FP64_FALLBACK | TTC_LQR_FLAG_KEEP_EXPANDED | TTC_LQR_FLAG_RESCUE_V1;
+                        TTC_LQR_FLAG_FP64_FALLBACK | TTC_LQR_FLAG_KEEP_EXPANDED | TTC_LQR_FLAG_RESCUE_V1 |
+                        TTC_LQR_FLAG_RESCUE_GAINS;
   return (flags & ~known) ? 0 : 1;
 }
 
@@ -1172,6 +1245,11 @@ size_t ttc_lqr_expanded_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_
 size_t ttc_lqr_rescue_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du) {
   if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0) return 0;
   return rescue_record_bytes(n_tokens * heads, d, du);
+}
+
+size_t ttc_lqr_rescue_gains_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {
+  if (n_tokens < 0 || heads <= 0 || d <= 0 || du <= 0 || T <= 0) return 0;
+  return rescue_gains_bytes(n_tokens * heads, d, du, T);
 }
 
 size_t ttc_lqr_stash_bytes(int64_t n_tokens, int32_t heads, int32_t d, int32_t du, int32_t T) {
@@ -1236,7 +1314,7 @@ int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, cons
   // TTC_LQR_FLAG_RESCUE_V1: no problem has a slot until the listed fp64 rescue gives it one
   RescueSlots rs{};
   if (flags & TTC_LQR_FLAG_RESCUE_V1) {
-    rs = rescue_slots(stash, P, d, du);
+    rs = rescue_slots(stash, P, d, du, T, (flags & TTC_LQR_FLAG_RESCUE_GAINS) != 0);
     hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, s, rs.slot_of, P, -1);
     if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
     if (rws == nullptr) rs = RescueSlots{};
@@ -1282,8 +1360,9 @@ int backward_entry(const float* A_diag, const float* B, const float* Q, const fl
     return TTC_LQR_EINVAL;
   const float* v1s = stash;
   const float* q0s = stash ? stash + n_tokens * heads * (int64_t)d * d : nullptr;
-  const RescueSlots rs = (flags & TTC_LQR_FLAG_RESCUE_V1) ? rescue_slots(stash, n_tokens * heads, d, du)
-                                                          : RescueSlots{};
+  const RescueSlots rs = (flags & TTC_LQR_FLAG_RESCUE_V1)
+                             ? rescue_slots(stash, n_tokens * heads, d, du, T, (flags & TTC_LQR_FLAG_RESCUE_GAINS) != 0)
+                             : RescueSlots{};
   return backward_core(A_diag, B, Q, R_inv, Q_f, log_gamma_A, log_gamma_B, log_gamma_Q, h0, u, d_u, n_tokens, heads,
                        d, du, T, flags, v1s, q0s, grad_A_diag, grad_B, grad_Q, grad_R_inv, grad_Q_f,
                        grad_log_gamma_A, grad_log_gamma_B, grad_log_gamma_Q, grad_h0,

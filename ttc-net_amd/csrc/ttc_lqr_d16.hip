@@ -32,10 +32,12 @@ int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
-                  float* gQp, float limit, int32_t* status, hipStream_t s) {
+                  float* gQp, float limit, int32_t* status, hipStream_t s, const int32_t* gidx,
+                  const double* gsl, const double* q0sl) {
   if (fp64)
     return launch_bwd<16, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, dU, kst, q0s, P, H, T, static_cast<double4*>(traj),
-                                 gA, gR, gQf, glA, glB, glQ, gh0, gBp, gQp, limit, status, s);
+                                 gA, gR, gQf, glA, glB, glQ, gh0, gBp, gQp, limit, status, s, gidx, gsl, q0sl);
+  if (gidx != nullptr) return TTC_LQR_EINVAL;  // kept gains are fp64
   return launch_bwd<16>(A, B, Q, R, Qf, lA, lB, lQ, h0, dU, kst, q0s, P, H, T, static_cast<float4*>(traj), gA, gR,
                        gQf, glA, glB, glQ, gh0, gBp, gQp, limit, status, s);
 }

@@ -38,7 +38,7 @@ static int rescue64(const float* A, const float* B, const float* Q, const float*
   const int64_t waves = resident_waves64<SM, WU, true>();
   hipLaunchKernelGGL((lqr_fwd64_mfma_kernel<SM, WU, true>), dim3((unsigned)waves), dim3(64), M64::LDS_BYTES, s, A,
                      B, Q, R, Qf, lA, lB, lQ, h0, P, H, T, u, st_a, st_b, status, rescue_ws, rs.slot_of, rs.slots,
-                     rs.nslot);
+                     rs.nslot, rs.gains, rs.ngslot);
   return TTC_LQR_OK;  // launch errors are the caller's to collect (hipGetLastError)
 }
 

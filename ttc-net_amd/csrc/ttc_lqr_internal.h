@@ -14,10 +14,14 @@ inline size_t rescue_ws_bytes(int64_t P) { return (size_t)(64 + (P > 0 ? P : 0))
 
 // TTC_LQR_FLAG_RESCUE_V1: where the d = 16 fp64 rescue keeps the fp64 V_1 and Quu_0 of list positions
 // below nslot (slots[k]: 256 doubles of V_1, then 256 of Quu_0; slot_of[problem] = k).
+// TTC_LQR_FLAG_RESCUE_GAINS adds every gain K_t of list positions below ngslot (<= nslot) in
+// gains[k] ([T][16][16] doubles).
 struct RescueSlots {
   int32_t* slot_of = nullptr;
   double* slots = nullptr;
   int64_t nslot = 0;
+  double* gains = nullptr;
+  int64_t ngslot = 0;
 };
 
 int launch_fwd_d16_mfma(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
@@ -61,7 +65,8 @@ int launch_bwd_d16(const float* A, const float* B, const float* Q, const float* 
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* dU,
                   const float* kst, const float* q0s, int64_t P, int H, int T, void* traj, bool fp64, float* gA,
                   float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
-                  float* gQp, float limit, int32_t* status, hipStream_t s);
+                  float* gQp, float limit, int32_t* status, hipStream_t s,
+                   const int32_t* gidx = nullptr, const double* gsl = nullptr, const double* q0sl = nullptr);
 // fp64: the row-layout Hamiltonian rollout in fp64 (long horizons, TTC_LQR_FLAG_FP64_*)
 int launch_ham_d16(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, const float* u0,

@@ -567,7 +567,9 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     int64_t P, int H, int T, int ntok_lds, typename Traj4<R>::type* __restrict__ traj, float* __restrict__ gA,
     float* __restrict__ gRinv, float* __restrict__ gQf, float* __restrict__ glgA,
     float* __restrict__ glgB, float* __restrict__ glgQ, float* __restrict__ gh0,
-    float* __restrict__ gBp, float* __restrict__ gQp, float grad_limit, int* __restrict__ status) {
+    float* __restrict__ gBp, float* __restrict__ gQp, float grad_limit, int* __restrict__ status,
+    const int32_t* __restrict__ gidx = nullptr, const double* __restrict__ gsl = nullptr,
+    const double* __restrict__ q0sl = nullptr) {
   using G = Geo<D>;
   extern __shared__ __align__(16) float smem_f[];
   R* const smem = reinterpret_cast<R*>(smem_f);
@@ -590,6 +592,17 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   }
   __syncthreads();
   const R* Bs = smem + (int)(n - n0) * G::MAT;
+  // this problem's gains [T][D][D] and Quu_0: the sweep's, or (fp64, gidx[p] >= 0) the forward
+  // rescue's kept ones in slot gidx[p] (gains in gsl, Quu_0 after V_1 in q0sl)
+  const R* kp = kst + (int64_t)p * T * D * D;
+  const R* q0p = reinterpret_cast<const R*>(q0stash) + (int64_t)p * D * D;
+  if constexpr (std::is_same<R, double>::value) {
+    const int64_t k = gidx != nullptr ? (int64_t)gidx[p] : -1;
+    if (k >= 0) {
+      kp = gsl + k * T * D * D;
+      q0p = q0sl + k * 2 * D * D + D * D;
+    }
+  }
   R* S = smem + ntok_lds * G::MAT + pb * G::PER_PROB;
   R* v0 = S + G::MAT;     // 8 vectors of D floats
   R* v1 = v0 + D;
@@ -622,7 +635,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   {
     R aug[D + 4];
     // Quu_0 as the forward sweep stored it (fp64 when it ran in fp64)
-    ld_global_row<D>(reinterpret_cast<const R*>(q0stash) + (p * D + li) * D, *reinterpret_cast<R(*)[D]>(aug));
+    ld_global_row<D>(q0p + li * D, *reinterpret_cast<R(*)[D]>(aug));
     aug[D] = dU[p * D + li];
     aug[D + 1] = aug[D + 2] = aug[D + 3] = R(0);
     R piv;
@@ -641,7 +654,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
   R h_i = h0[p * D + li];
   R hb_i = R(0);
   R knext[PF ? D : 1];
-  if constexpr (PF) ld_global_row<D>(kst + ((int64_t)p * T * D + li) * D, knext);
+  if constexpr (PF) ld_global_row<D>(kp + li * D, knext);
   for (int t = 0; t < T; ++t) {
     const R tp1 = (R)(t + 1);
     const R alpha_i = fma(a_i, exp(lgA_p * tp1), R(1));
@@ -650,7 +663,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     if constexpr (PF) {
 #pragma unroll
       for (int c = 0; c < D; ++c) krow[c] = knext[c];
-      if (t + 1 < T) ld_global_row<D>(kst + (((int64_t)p * T + t + 1) * D + li) * D, knext);
+      if (t + 1 < T) ld_global_row<D>(kp + ((int64_t)(t + 1) * D + li) * D, knext);
     }
     v0[li] = h_i;
     v1[li] = hb_i;
@@ -658,7 +671,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     R hv[D], hbv[D];
     ld_row<D>(v0, hv);
     ld_row<D>(v1, hbv);
-    if constexpr (!PF) ld_global_row<D>(kst + (((int64_t)p * T + t) * D + li) * D, krow);
+    if constexpr (!PF) ld_global_row<D>(kp + ((int64_t)t * D + li) * D, krow);
     R u_i = R(0), w_i = (t == 0) ? w0_i : R(0);
 #pragma unroll
     for (int c = 0; c < D; ++c) {
@@ -720,7 +733,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
     for (int c = 0; c < D; ++c) kcn[c] = R(0);
     if (T - 1 >= 1) {
 #pragma unroll
-      for (int c = 0; c < D; ++c) kcn[c] = kst[(((int64_t)p * T + (T - 1)) * D + c) * D + li];  // K_{T-1}[c, li]
+      for (int c = 0; c < D; ++c) kcn[c] = kp[((int64_t)(T - 1) * D + c) * D + li];  // K_{T-1}[c, li]
     }
   }
   for (int t = T - 1; t >= 0; --t) {
@@ -734,7 +747,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
         trn = traj[((int64_t)p * T + (t - 1)) * D + li];
         if (t - 1 >= 1) {
 #pragma unroll
-          for (int c = 0; c < D; ++c) kcn[c] = kst[(((int64_t)p * T + (t - 1)) * D + c) * D + li];
+          for (int c = 0; c < D; ++c) kcn[c] = kp[((int64_t)(t - 1) * D + c) * D + li];
         }
       }
     }
@@ -787,7 +800,7 @@ __global__ __launch_bounds__(Geo<D>::THREADS) void lqr_bwd_kernel(
         Qhb = fma(Qrow[c], qhb[c], Qhb);
         // Q_t = D_t Q D_t:  gradient D_t sym(h hb') D_t  (torch_lqr.py:55)
         gQrow[c] = fma(R(0.5) * q_i, fma(h_t, qhb[c], hb_t * qh[c]), gQrow[c]);
-        const R kji = PF ? kcol[c] : kst[(((int64_t)p * T + t) * D + c) * D + li];  // K_t[c, li]
+        const R kji = PF ? kcol[c] : kp[((int64_t)t * D + c) * D + li];  // K_t[c, li]
         kcu = fma(kji, cu[c], kcu);
         kcw = fma(kji, cw[c], kcw);
       }
@@ -1447,13 +1460,14 @@ inline int launch_bwd(const float* A, const float* B, const float* Q, const floa
                       const float* kst, const float* q0s, int64_t P, int H, int T,
                       typename Traj4<RT>::type* traj, float* gA,
                       float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
-                      float* gQp, float limit, int32_t* status, hipStream_t s) {
+                      float* gQp, float limit, int32_t* status, hipStream_t s, const int32_t* gidx = nullptr,
+                      const double* gsl = nullptr, const double* q0sl = nullptr) {
   if (P <= 0) return TTC_LQR_OK;
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
   hipLaunchKernelGGL((lqr_bwd_kernel<D, RT>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf, lA, lB,
                      lQ, h0, dU,
                      kst, q0s, P, H, T, ntok_lds_for<D>(H), traj, gA, gR, gQf, glA, glB, glQ, gh0, gBp, gQp,
-                     limit, status);
+                     limit, status, gidx, gsl, q0sl);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 

@@ -139,6 +139,9 @@ constexpr double kSym64AsymMax = 1.0e-11;
 // fp64 V_1 and Quu_0 in slots[k] (2 x 256 doubles) and k in slot_of[problem], for a later
 // fp64 rollout to start from.  Under STASH_V1 a null kstash / q0stash skips the fp32 copies (the
 // backward's sweep for its own slots, which leaves the forward's stash as it is).
+// gslots (with slots, not SYMP): list position k < ngslot (<= nslot) also keeps every gain K_t
+// of the problem in fp64 in gslots[k] ([T][16][16]), for the stable backward to read instead of
+// sweeping again.
 // SYMP: steps T-1 .. 1 as the symplectic sweep in fp64 instead (below), its certificate per
 // problem, then step 0 as above from V_1; a problem that misses the certificate stores nothing
 // (no u, stash or slot).
@@ -149,9 +152,11 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
     const float* __restrict__ lgB, const float* __restrict__ lgQ, const float* __restrict__ h0, int64_t P,
     int H, int T, float* __restrict__ u_out, float* __restrict__ kstash, float* __restrict__ q0stash,
     int* __restrict__ status, const int32_t* __restrict__ list, int32_t* __restrict__ slot_of = nullptr,
-    double* __restrict__ slots = nullptr, int64_t nslot = 0) {
+    double* __restrict__ slots = nullptr, int64_t nslot = 0, double* __restrict__ gslots = nullptr,
+    int64_t ngslot = 0) {
   constexpr int LDG = M64::LDG;
   constexpr bool KEEP64 = LISTED && SM == STASH_V1;  // the fp64 V_1 / Quu_0 slots may be written
+  constexpr bool KEEPG = KEEP64 && !SYMP;             // and the per-step gains of the first ngslot
   const bool keep64 = KEEP64 && slots != nullptr;
   extern __shared__ __align__(16) double sm64[];
   const int lane = threadIdx.x;
@@ -186,6 +191,8 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
     }
     const int64_t pg = g == 0 ? pq[0] : (g == 1 ? pq[1] : (g == 2 ? pq[2] : pq[3]));
     const bool vg = g == 0 ? vq[0] : (g == 1 ? vq[1] : (g == 2 ? vq[2] : vq[3]));
+    // this batch keeps per-step gains (some of its problems have list positions below ngslot)
+    const bool keepg = KEEPG && keep64 && gslots != nullptr && b0 < ngslot;
 
     // row layout: problem g, index c
     const double a_c = A_diag[pg * 16 + c];
@@ -501,7 +508,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
 #pragma unroll
           for (int s = 0; s < 4; ++s) Mt = mfma64(nU[s], nWt[s], Mt);  // M' = L^{-1} W'
           const double al_c = v[c];
-          if (SM == STASH_GAINS || t == 0) {
+          if (SM == STASH_GAINS || t == 0 || keepg) {
             // X = L^{-T} M' A: A operand L^{-T}[c][g + 4s] = -(-L^{-T})[c][g + 4s]
             double Lt[4];
             ld_row<4>(t0 + c * LDG + 4 * g, Lt);
@@ -513,6 +520,13 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
             if constexpr (SM == STASH_GAINS) {
               if (vq[q]) {
                 double* kd = reinterpret_cast<double*>(kstash) + ((int64_t)pq[q] * T + t) * 256;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -X[r];
+              }
+            }
+            if constexpr (KEEPG) {
+              if (keepg && vq[q] && b0 + q < ngslot) {
+                double* kd = gslots + ((b0 + q) * T + t) * 256;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -X[r];
               }
@@ -572,6 +586,13 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
           if constexpr (SM == STASH_GAINS) {
             if (vq[q]) {
               double* kd = reinterpret_cast<double*>(kstash) + ((int64_t)pq[q] * T + t) * 256;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -Xb[r];
+            }
+          }
+          if constexpr (KEEPG) {
+            if (keepg && vq[q] && b0 + q < ngslot) {
+              double* kd = gslots + ((b0 + q) * T + t) * 256;
 #pragma unroll
               for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -Xb[r];
             }

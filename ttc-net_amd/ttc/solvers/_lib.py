@@ -12,7 +12,7 @@ import os
 
 __all__ = ["lib", "lib_path", "LIB_NAME", "TTCLQRError", "check", "FLAG_FP64_RICCATI", "FLAG_ROW_KERNEL",
            "FLAG_STABLE_BWD", "FLAG_RICCATI_STEPS", "FLAG_COMPACT_STASH", "FLAG_FP64_RESCUE", "FLAG_FP64_FALLBACK",
-           "FLAG_KEEP_EXPANDED", "FLAG_RESCUE_V1"]
+           "FLAG_KEEP_EXPANDED", "FLAG_RESCUE_V1", "FLAG_RESCUE_GAINS"]
 
 FLAG_FP64_RICCATI = 1  # TTC_LQR_FLAG_FP64_RICCATI
 FLAG_ROW_KERNEL = 2    # TTC_LQR_FLAG_ROW_KERNEL
@@ -23,6 +23,7 @@ FLAG_FP64_RESCUE = 32  # TTC_LQR_FLAG_FP64_RESCUE
 FLAG_FP64_FALLBACK = 64  # TTC_LQR_FLAG_FP64_FALLBACK
 FLAG_KEEP_EXPANDED = 128  # TTC_LQR_FLAG_KEEP_EXPANDED
 FLAG_RESCUE_V1 = 256  # TTC_LQR_FLAG_RESCUE_V1
+FLAG_RESCUE_GAINS = 512  # TTC_LQR_FLAG_RESCUE_GAINS
 
 LIB_NAME = "libttc_lqr.so"
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -77,6 +78,8 @@ def _load():
     L.ttc_lqr_expanded_bytes.argtypes = [i64, i32, i32, i32]
     L.ttc_lqr_rescue_stash_bytes.restype = sz
     L.ttc_lqr_rescue_stash_bytes.argtypes = [i64, i32, i32, i32]
+    L.ttc_lqr_rescue_gains_bytes.restype = sz
+    L.ttc_lqr_rescue_gains_bytes.argtypes = [i64, i32, i32, i32, i32]
     L.ttc_lqr_factored_workspace_bytes.restype = sz
     L.ttc_lqr_factored_workspace_bytes.argtypes = [i64, i32, i32, i32, i32, i32, i32, i32, i32, i32, i32]
     L.ttc_lqr_forward_factored.restype = ctypes.c_int

@@ -58,7 +58,7 @@ import os
 import torch
 
 from ._lib import lib, check, FLAG_FP64_RICCATI, FLAG_ROW_KERNEL, FLAG_STABLE_BWD, FLAG_RICCATI_STEPS, \
-    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK, FLAG_KEEP_EXPANDED, FLAG_RESCUE_V1
+    FLAG_COMPACT_STASH, FLAG_FP64_RESCUE, FLAG_FP64_FALLBACK, FLAG_KEEP_EXPANDED, FLAG_RESCUE_V1, FLAG_RESCUE_GAINS
 
 __all__ = ["hip_lqr_solve", "HipLQRSolveFunc", "hip_lqr_solve_factored", "HipLQRFactoredFunc", "padded_dim",
            "check_deferred_status",
@@ -295,6 +295,11 @@ class HipLQRSolveFunc(torch.autograd.Function):
         if keep and _rescue_v1(flags, Dp):  # the rescue's fp64 V_1 / Quu_0 after the stash
             flags |= FLAG_RESCUE_V1
             st_bytes = _align256(stash_bytes) + lib.ttc_lqr_rescue_stash_bytes(bs, nh, Dp, Dp)
+            # and its fp64 gains, when they fit the stash budget too
+            with_gains = st_bytes + lib.ttc_lqr_rescue_gains_bytes(bs, nh, Dp, Dp, T)
+            if _keep_rescue_gains(dev, policy, with_gains):
+                flags |= FLAG_RESCUE_GAINS
+                st_bytes = with_gains
         st = torch.empty(st_bytes // 4, device=dev, dtype=torch.float32) if keep else None
         # the fp64 rescue's problem list (4 bytes a problem; long horizons only)
         fws_bytes = lib.ttc_lqr_forward_workspace_bytes(bs, nh, Dp, Dp, T, flags)
@@ -411,8 +416,18 @@ def _rescue_v1(flags: int, Dp: int) -> bool:
     """Whether a forward with a stash keeps the fp64 V_1 / Quu_0 of the problems its fp64 rescue
     recomputes (``TTC_LQR_FLAG_RESCUE_V1``, d = 16, under ``TTC_LQR_FLAG_FP64_RESCUE``): the
     backward's fp64 second rollout tier then starts them from those instead of their fp32
-    roundings, and more of them pass its certificate (each that does skips a stable-path sweep)."""
+    roundings, and more of them pass its certificate (each that does skips a stable-path sweep).
+    When the stash budget also holds their fp64 gains (``TTC_LQR_FLAG_RESCUE_GAINS``, 2 MB a kept
+    problem at T = 1024), the forward keeps those too and the backward's stable path reads them
+    instead of sweeping those problems again."""
     return bool(flags & FLAG_FP64_RESCUE) and Dp == 16
+
+
+def _keep_rescue_gains(dev, policy: str, nbytes: int) -> bool:
+    """Whether a forward that keeps the rescue's fp64 V_1 also keeps its fp64 gains
+    (``TTC_LQR_FLAG_RESCUE_GAINS``): when the stash with them (``nbytes``) fits the stash budget,
+    or the stash policy is "always"."""
+    return policy == "always" or _stash_fits(dev, nbytes)
 
 
 def _keep_expanded(dev, kind: str, stash_bytes: int, expanded_bytes: int) -> bool:
