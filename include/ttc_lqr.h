@@ -20,7 +20,7 @@
  *     unchanged).  Anything else returns TTC_LQR_EUNSUPPORTED.
  *   - Nothing here allocates device memory or throws.  All work is enqueued on
  *     `stream` (a hipStream_t, NULL = default stream); only ttc_lqr_backward
- *     synchronises it (once or twice per token chunk, to size its fallback).
+ *     synchronises it (one to five times per token chunk, to size its fallback).
  *   - `status` (device int32, caller-zeroed, may be NULL) receives bit flags:
  *     TTC_LQR_STATUS_NONFINITE if any output is NaN/Inf, TTC_LQR_STATUS_LARGE if
  *     a gradient has |g| >= grad_limit.  The caller reads it after the stream
@@ -227,9 +227,11 @@ int ttc_lqr_forward_ws(const float* A_diag, const float* B, const float* Q, cons
  * workspace, closed-loop costates).  With heads % 8 == 0 the rollout runs over head
  * groups of 8 in fp32; under TTC_LQR_FLAG_FP64_RICCATI / _FP64_RESCUE the problems of
  * the groups it rejects are rolled again one by one in fp64 before any reaches the
- * stable path.  *n_fallback (host, may be NULL) receives the number of problems that
- * took the stable path.  Reading the rejected counts synchronises `stream` once per
- * token chunk (twice with the fp64 second rollout).
+ * stable path, and at d = 16 those that still fail after starting from the stash's fp32
+ * V_1 once more from an fp64 V_1 of a certified fp64 symplectic sweep.  *n_fallback (host,
+ * may be NULL) receives the number of problems that took the stable path.  Reading the
+ * rejected counts synchronises `stream` once per token chunk (twice with the fp64 second
+ * rollout, four times with the third, five with TTC_LQR_FLAG_RESCUE_GAINS).
  * grad_B / grad_Q are summed over heads (B and Q are head-shared).
  * workspace_bytes must be at least ttc_lqr_workspace_bytes(1, ...); larger workspaces
  * give fewer, larger passes.  grad_limit: |g| >= grad_limit sets TTC_LQR_STATUS_LARGE

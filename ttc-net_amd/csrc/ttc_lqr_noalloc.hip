@@ -1,6 +1,6 @@
 // ttc_lqr_noalloc.hip -- ttc_lqr_backward_noalloc: ttc_lqr_backward over a fixed device scratch,
 // for callers that cannot allocate (tight serving loops, harnesses that forbid hipMalloc).  Like
-// ttc_lqr_backward it synchronises the stream once or twice per token chunk (it reads the counts of
+// ttc_lqr_backward it synchronises the stream once to five times per token chunk (it reads the counts of
 // problems the certificates rejected), so it cannot be recorded by HIP graph capture.
 //
 // The scratch is a file-scope device array of TTC_LQR_NOALLOC_SCRATCH_BYTES; every GPU the library
