@@ -628,7 +628,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
                              (int64_t)nfail, plist);
           if (hipGetLastError() != hipSuccess) return TTC_LQR_ELAUNCH;
           switch (d) {
-            case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist, rs.slot_of ? rs.slot_of + p0 : nullptr, rs.slots); break;
+            case 16: rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist, rs.slot_of ? rs.slot_of + p0 : nullptr, rs.slots, rs.nslot); break;
             case 32: rc = launch_ham_d32(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, np, H, T, tau, gA, gR, gQf, glA, glB, glQ, gh, gBp, gQp, grad_limit, list, cnt + 1, status, s, true, plist); break;
             default: return TTC_LQR_EUNSUPPORTED;
           }
@@ -659,7 +659,7 @@ static int backward_core(const float* A_diag, const float* B, const float* Q, co
             if (n3 > 0) {
               rc = launch_ham_d16(a, b, q, r, qf, la, lb, lq, hz, uz, dz, v1, q0, n3, H, T, tau, gA, gR, gQf, glA,
                                   glB, glQ, gh, gBp, gQp, grad_limit, plist, cnt + 3, status, s, true, list3 + 64, so3,
-                                  sl3);
+                                  sl3, L.n3);
               if (rc != TTC_LQR_OK) return rc;
             }
             rc = read_count(cnt + 3, nfail2, nstable);

@@ -48,10 +48,10 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
                   hipStream_t s, bool fp64, const int32_t* plist,
-                  const int32_t* slot_of, const double* slots) {
+                  const int32_t* slot_of, const double* slots, int64_t nslot) {
   if (fp64)
     return launch_ham<16, double>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
-                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist, slot_of, slots);
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist, slot_of, slots, nslot);
   return launch_ham<16>(A, B, Q, R, Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, tau, gA, gR, gQf, glA, glB,
                        glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, s, plist);
 }

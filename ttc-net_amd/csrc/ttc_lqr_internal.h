@@ -74,7 +74,7 @@ int launch_ham_d16(const float* A, const float* B, const float* Q, const float* 
                   float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                   float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
                   hipStream_t s, bool fp64, const int32_t* plist = nullptr, const int32_t* slot_of = nullptr,
-                  const double* slots = nullptr);
+                  const double* slots = nullptr, int64_t nslot = 0);
 int launch_fwd_d32(const float* A, const float* B, const float* Q, const float* R, const float* Qf,
                   const float* lA, const float* lB, const float* lQ, const float* h0, int64_t P, int H, int T,
                   float* u, float* st_a, float* st_b, int sm, int32_t* status, hipStream_t s, int flags,

@@ -881,7 +881,8 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
     float* __restrict__ gRinv, float* __restrict__ gQf, float* __restrict__ glgA, float* __restrict__ glgB,
     float* __restrict__ glgQ, float* __restrict__ gh0, float* __restrict__ gBp, float* __restrict__ gQp,
     float grad_limit, int* __restrict__ fail_list, int* __restrict__ fail_count, int* __restrict__ status,
-    const int* __restrict__ plist, const int32_t* __restrict__ slot_of, const double* __restrict__ slots) {
+    const int* __restrict__ plist, const int32_t* __restrict__ slot_of, const double* __restrict__ slots,
+    int64_t nslot) {
   using G = Geo<D>;
   extern __shared__ __align__(16) float smem_f[];
   R* const smem = reinterpret_cast<R*>(smem_f);
@@ -948,6 +949,7 @@ __attribute__((amdgpu_waves_per_eu(std::is_same<R, double>::value ? TTC_HAM64_WA
   int kslot = -1;
   if constexpr (LISTED && std::is_same<R, double>::value) {
     if (slot_of != nullptr) kslot = slot_of[p];
+    if (kslot >= nslot) kslot = -1;  // an index beyond the slots is no slot (never read past them)
   }
   // t = 0: adjoint feed-forward w_0 = -Quu_0^{-1} d_u (pivoted elimination)
   R w_i;
@@ -1440,17 +1442,18 @@ inline int launch_ham(const float* A, const float* B, const float* Q, const floa
                       float* gA, float* gR, float* gQf, float* glA, float* glB, float* glQ, float* gh0, float* gBp,
                       float* gQp, float limit, int32_t* fail_list, int32_t* fail_count, int32_t* status,
                       hipStream_t s, const int32_t* plist = nullptr, const int32_t* slot_of = nullptr,
-                      const double* slots = nullptr) {
+                      const double* slots = nullptr, int64_t nslot = 0) {
   if (P <= 0) return TTC_LQR_OK;
   const dim3 grid((unsigned)((P + Geo<D>::PPB - 1) / Geo<D>::PPB)), block(Geo<D>::THREADS);
   if (plist != nullptr)
     hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT, true>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R, Qf,
                        lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB, glQ,
-                       gh0, gBp, gQp, limit, fail_list, fail_count, status, plist, slot_of, slots);
+                       gh0, gBp, gQp, limit, fail_list, fail_count, status, plist, slot_of, slots, nslot);
   else
     hipLaunchKernelGGL((lqr_ham_bwd_kernel<D, RT, false>), grid, block, lds_bytes<D>(H, sizeof(RT)), s, A, B, Q, R,
                        Qf, lA, lB, lQ, h0, u0, dU, v1s, q0s, P, H, T, ntok_lds_for<D>(H), tau, gA, gR, gQf, glA, glB,
-                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, plist, nullptr, nullptr);
+                       glQ, gh0, gBp, gQp, limit, fail_list, fail_count, status, plist, nullptr, nullptr,
+                       (int64_t)0);
   return hipGetLastError() == hipSuccess ? TTC_LQR_OK : TTC_LQR_ELAUNCH;
 }
 
