@@ -207,8 +207,8 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
     rmin = fminf(rmin, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(rmin), 0x121, 0xF, 0xF, false)));
     const double piv_floor = 0.5 * (double)rmin;
 
-    // C layout, problem q: B of its token (B[g + 4s][c]), -sym(Q), N = -sym(Q_f), -R (diagonal)
-    double Bo[4][4], nR[4];
+    // C layout, problem q: B of its token (B[g + 4s][c]), -sym(Q), N = -sym(Q_f)
+    double Bo[4][4];
     v4d Qo[4], N[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -224,7 +224,6 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
         Qo[q][r] = -0.5 * ((double)qq[i * 16 + c] + (double)qq[c * 16 + i]);
         N[q][r] = -0.5 * ((double)fq[i * 16 + c] + (double)fq[c * 16 + i]);
       }
-      nR[q] = -1.0 / (double)Rinv[pq[q] * 16 + c];
     }
 
     // SYMP: steps T-1 .. 1 by the symplectic recursion (the reference's symplectic_iter.py:226-251,
@@ -265,44 +264,34 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
           }
           wave_sync();
           const bool renorm = (T - 1 - t) % 8 == 7;
-          // phase by phase over the wave's problems: each phase's products are independent of
-          // one another, so the matrix core runs one problem's while the next is scaled
-          v4d M[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {  // B' N: A operand B'[c][g + 4s] = B[g + 4s][c] (Bo)
-            if (q >= ppw) break;  // uniform
-            M[q] = v4d{0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-            for (int s = 0; s < 4; ++s) M[q] = mfma64(Bo[q][s], N[q][s], M[q]);
-          }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {  // M = R^{-1} B_k' Y2' (rows g + 4r); Y1' += B M
-            if (q >= ppw) break;  // uniform
-            double nbr[4];
-            ld_row<4>(VV(q) + 64 + 4 * g, nbr);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) M[q][r] *= nbr[r];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) Y1[q] = mfma64(Bt[q][s], M[q][s], Y1[q]);
-          }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {  // Y1' <- A^{-1} Y1'; -Y2' <- A (-Y2') - Qc Y1'
+          for (int q = 0; q < 4; ++q) {
             if (q >= ppw) break;  // uniform
             const double* v = VV(q);
-            double alr[4], iar[4], qr[4];
-            ld_row<4>(v + 4 * g, alr);
-            ld_row<4>(v + 16 + 4 * g, iar);
-            ld_row<4>(v + 48 + 4 * g, qr);
-            const double q_c = v[32 + c];
+            // M = R^{-1} B_k' Y2' = (B' N) rows scaled by -beta^2 R_inv: A operand
+            // B'[c][g + 4s] = B[g + 4s][c] (Bo), B operand N[g + 4s][c]
+            v4d M = v4d{0.0, 0.0, 0.0, 0.0};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              Y1[q][r] *= iar[r];
-              N[q][r] *= alr[r];
-            }
-            // A operand -Qc[c][g + 4s] = q_c (-sym Q)[g + 4s][c] q_{g + 4s}
+            for (int s = 0; s < 4; ++s) M = mfma64(Bo[q][s], N[q][s], M);
+            double sc[4];  // per row g + 4r: -beta^2 R_inv, then 1 / alpha, alpha, q
+            ld_row<4>(v + 64 + 4 * g, sc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) M[r] *= sc[r];
+            // Y1' <- A^{-1} (Y1' + B_k M)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) Y1[q] = mfma64(Bt[q][s], M[s], Y1[q]);
+            ld_row<4>(v + 16 + 4 * g, sc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Y1[q][r] *= sc[r];
+            ld_row<4>(v + 4 * g, sc);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) N[q][r] *= sc[r];
+            // -Y2' <- A (-Y2') - Qc Y1': A operand -Qc[c][g + 4s] = q_c (-sym Q)[g + 4s][c] q_{g + 4s}
+            ld_row<4>(v + 48 + 4 * g, sc);
+            const double q_c = v[32 + c];
             double op[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) op[s] = Qo[q][s] * (q_c * qr[s]);
+            for (int s = 0; s < 4; ++s) op[s] = Qo[q][s] * (q_c * sc[s]);
 #pragma unroll
             for (int s = 0; s < 4; ++s) N[q] = mfma64(op[s], Y1[q][s], N[q]);
           }
@@ -383,6 +372,10 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
       }
     }
     const bool accg = g == 0 ? acc[0] : (g == 1 ? acc[1] : (g == 2 ? acc[2] : acc[3]));
+    // -R (diagonal, column c) for the Riccati steps, formed after the symplectic ones (not live there)
+    double nR[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) nR[q] = -1.0 / (double)Rinv[pq[q] * 16 + c];
 
     // The discounts are exact exponentials at every step.  (By one-step multiplications with an
     // exact refresh every 8 steps -- ~1e-15 relative -- the undiscounted config-5b fixture's
