@@ -210,11 +210,31 @@ def make_oracle_fixtures():
         print("wrote", name)
 
 
+def make_beyond_fp64(name="mp_cfg5b_beyond_fp64.npz", n_tokens=12288, seed=21, p=5086, T=1024):
+    """u of one config-5b problem that fp64 does not resolve (problem 5086 of a 12,288-token
+    sample: the fp64 oracle and both fp64 rescue routes of the solver miss it by 10-33 %), in
+    40-digit arithmetic, with the problem's inputs."""
+    from oracle.inputs import layer_solver_inputs, make_x
+    ins = layer_solver_inputs("5b", make_x("5b", n_tokens=n_tokens, seed=seed))
+    sp = single_problem(ins, p, ins[0].shape[1])
+    out = mp_solve_grads(sp, T, np.zeros((1, 1, sp[1].shape[-1])), dps=40)
+    path = os.path.join(HERE, name)
+    np.savez_compressed(path, T=T, p=p, n_tokens=n_tokens, seed=seed, out_u=out["u"],
+                        **{f"in_{k}": v for k, v in zip(NAMES, sp)},
+                        meta=np.array(f"cfg5b seed{seed} n_tokens{n_tokens} problem{p} T{T} mpmath dps=40 (u only)"))
+    print("wrote", path)
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--skip-mp", action="store_true")
+    ap.add_argument("--beyond-fp64", action="store_true", help="write only mp_cfg5b_beyond_fp64.npz")
     a = ap.parse_args()
+    if a.beyond_fp64:
+        make_beyond_fp64()
+        raise SystemExit(0)
     make_oracle_fixtures()
     if not a.skip_mp:
         make_mp("mp_stress_cfg5_T64.npz", 5, 64, 5, 64)
         make_mp("mp_stress_cfg5_T1024.npz", 5, 16, 0, 1024)
+        make_beyond_fp64()
