@@ -179,12 +179,18 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
   int ppw = (int)((nprob + (int64_t)gridDim.x - 1) / (int64_t)gridDim.x);
   ppw = __builtin_amdgcn_readfirstlane(ppw < 1 ? 1 : (ppw > 4 ? 4 : ppw));
 
-  for (int64_t b0 = (int64_t)blockIdx.x * ppw; b0 < nprob; b0 += (int64_t)gridDim.x * ppw) {
+  // The batch body, with the wave's problem count fixed at four (FULL: the per-problem loops
+  // unroll into one basic block each, so the scheduler can overlap the problems' chains of
+  // dependent matrix products and LDS reads) or as counted (a short list: only the real problems'
+  // products are issued).
+  auto batch = [&](const int64_t b0, auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    const int np = FULL ? 4 : ppw;
     int64_t pq[4];
     bool vq[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      vq[q] = q < ppw && b0 + q < nprob;
+      vq[q] = q < np && b0 + q < nprob;
       const int64_t k = vq[q] ? b0 + q : b0;  // idle slots recompute a real problem, never store
       if constexpr (LISTED) pq[q] = (int64_t)list[64 + k];
       else pq[q] = k;
@@ -266,7 +272,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
           const bool renorm = (T - 1 - t) % 8 == 7;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            if (q >= ppw) break;  // uniform
+            if (q >= np) break;  // uniform
             const double* v = VV(q);
             // M = R^{-1} B_k' Y2' = (B' N) rows scaled by -beta^2 R_inv: A operand
             // B'[c][g + 4s] = B[g + 4s][c] (Bo), B operand N[g + 4s][c]
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
           if (renorm) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              if (q >= ppw) break;  // uniform
+              if (q >= np) break;  // uniform
               double mk = 0.0;
 #pragma unroll
               for (int r = 0; r < 4; ++r) mk = fmax(mk, fmax(fabs(Y1[q][r]), fabs(N[q][r])));
@@ -418,7 +424,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
       // order)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        if (q >= ppw) break;  // uniform
+        if (q >= np) break;  // uniform
         const double be_c = VV(q)[64 + c];
         double Bk[4];
 #pragma unroll
@@ -468,7 +474,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
         static_for<16>([&](auto kc) {
           constexpr int k = decltype(kc)::value;
           const double npiv = bcast16d<k>(qrow[k]);  // -d_k
-          bad |= g < ppw && !(-npiv >= piv_floor && -npiv < INFINITY);  // also catches NaN
+          bad |= g < np && !(-npiv >= piv_floor && -npiv < INFINITY);  // also catches NaN
           const double rs = rsqrt64(-npiv);
           const double ip = rs * rs;
           const double ni = irow[k] * ip;
@@ -488,7 +494,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
       if (!__any(bad)) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (q >= ppw) break;  // uniform
+          if (q >= np) break;  // uniform
           const double* t0 = T0(q);
           double* t1 = T1(q);
           const double* v = VV(q);
@@ -569,7 +575,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
         wave_sync();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (q >= ppw) break;  // uniform
+          if (q >= np) break;  // uniform
           const double* t0 = T0(q);
           double* t1 = T1(q);
           const double* v = VV(q);
@@ -615,14 +621,14 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
         wave_sync();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (q >= ppw) break;  // uniform
+          if (q >= np) break;  // uniform
 #pragma unroll
           for (int r = 0; r < 4; ++r) T1(q)[c * LDG + g + 4 * r] = N[q][r];
         }
         wave_sync();
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          if (q >= ppw) break;  // uniform
+          if (q >= np) break;  // uniform
 #pragma unroll
           for (int r = 0; r < 4; ++r) N[q][r] = 0.5 * (N[q][r] + T1(q)[(g + 4 * r) * LDG + c]);
         }
@@ -645,6 +651,10 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
       if (status != nullptr && vg && accg && !isfinite(u0)) atomicOr(status, TTC_LQR_STATUS_NONFINITE);
     }
     wave_sync();  // the next batch rewrites the tiles
+  };
+  for (int64_t b0 = (int64_t)blockIdx.x * ppw; b0 < nprob; b0 += (int64_t)gridDim.x * ppw) {
+    if (ppw == 4) batch(b0, std::true_type{});
+    else batch(b0, std::false_type{});
   }
 }
 
