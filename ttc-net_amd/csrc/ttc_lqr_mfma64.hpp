@@ -23,9 +23,10 @@
 // this kernel is the fp64 arithmetic of the same recursion for the long horizons where fp32
 // loses the gains.  Every Cholesky pivot of Quu = R + B'VB is at least min_j 1/R_inv_j in
 // exact arithmetic; a pivot below half of that (rounding-limited: on these horizons Quu reaches
-// 1e17 and more; or Quu indefinite) sends the wave's step to the row-layout sweep's pivoted LU
-// solve of [Quu | Qux] (X = Quu^{-1} Qux, N <- A(N A + W X) - Qc), and the next step tries
-// Cholesky again.  (Keeping such rounding-limited positive pivots cost the undiscounted
+// 1e17 and more; or Quu indefinite) sends that problem's step to the row-layout sweep's
+// pivoted LU solve of [Quu | Qux] (X = Quu^{-1} Qux, N <- A(N A + W X) - Qc), and the next step
+// tries Cholesky again.  The choice is per problem, so a problem's result does not depend on
+// the problems it shares a wave with.  (Keeping such rounding-limited positive pivots cost the undiscounted
 // config-5b fixture an order of magnitude in grad_B against the LU solve.)
 #pragma once
 #include "ttc_lqr_mfma16.hpp"
@@ -491,7 +492,14 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
         st_row<16>(t0 + c * LDG, prow);
       }
       wave_sync();
-      if (!__any(bad)) {
+      // Each problem takes the Cholesky path unless its own pivots fell below the floor: a
+      // problem's arithmetic never depends on the other problems of its wave (so neither on the
+      // order of a list nor on the wave's problem count).
+      const unsigned long long bb = __ballot(bad);
+      bool badq[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) badq[q] = ((bb >> (16 * q)) & 1ull) != 0ull;
+      {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           if (q >= np) break;  // uniform
@@ -517,20 +525,20 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
 #pragma unroll
             for (int r = 0; r < 4; ++r) X[r] *= al_c;
             if constexpr (SM == STASH_GAINS) {
-              if (vq[q]) {
+              if (vq[q] && !badq[q]) {
                 double* kd = reinterpret_cast<double*>(kstash) + ((int64_t)pq[q] * T + t) * 256;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -X[r];
               }
             }
             if constexpr (KEEPG) {
-              if (keepg && vq[q] && b0 + q < ngslot) {
+              if (keepg && vq[q] && !badq[q] && b0 + q < ngslot) {
                 double* kd = gslots + ((b0 + q) * T + t) * 256;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) kd[(g + 4 * r) * 16 + c] = -X[r];
               }
             }
-            if (t == 0) {
+            if (t == 0 && !badq[q]) {
 #pragma unroll
               for (int r = 0; r < 4; ++r) t1[(g + 4 * r) * LDG + c] = X[r];
             }
@@ -544,13 +552,19 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
             ld_row<4>(v + 48 + 4 * g, qr);   // q[g + 4r]
             const double q_c = v[32 + c];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) N[q][r] = fma(S[r], alr[r] * al_c, (qr[r] * q_c) * Qo[q][r]);
+            for (int r = 0; r < 4; ++r) {
+              const double nn = fma(S[r], alr[r] * al_c, (qr[r] * q_c) * Qo[q][r]);
+              N[q][r] = badq[q] ? N[q][r] : nn;  // a problem redone below keeps its N
+            }
           }
         }
-      } else {
+      }
+      if (bb != 0ull) {
         // A pivot below the floor (rounding-limited, or Quu indefinite): this step again, for
-        // every problem of the wave, by the row-layout sweep's pivoted LU solve of the rows
-        // [Quu | Qux] (Qux = W'A), X = Quu^{-1} Qux, then N <- A (N A + W X) - Qc.
+        // those problems, by the row-layout sweep's pivoted LU solve of the rows [Quu | Qux]
+        // (Qux = W'A), X = Quu^{-1} Qux, then N <- A (N A + W X) - Qc.  Every group solves its
+        // problem's rows (the tiles of the others were read above); only these problems keep
+        // the result.
         {
           double aug[32];
           double qrow[16];
@@ -576,6 +590,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           if (q >= np) break;  // uniform
+          if (!badq[q]) continue;  // uniform
           const double* t0 = T0(q);
           double* t1 = T1(q);
           const double* v = VV(q);
