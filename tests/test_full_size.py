@@ -6,9 +6,10 @@ T = 64; config 5b, x [4, 1024, 8, 32] -> 32,768 tokens x 8 heads = 262,144 probl
 At these sizes the fp64 oracle runs only on a sample, so the whole-size run is checked by
 * parity on a seeded sample of tokens against the fp64 oracle, at the 1e-4 bar of the other
   parity tests;
-* a token permutation: every problem is solved on its own (heads of one token share B and Q and
-  sit in one head group), so permuting the tokens permutes u and all nine gradients bit for bit
-  -- an indexing slip, a race or a read of another problem's data breaks it;
+* a token permutation: a problem's arithmetic depends at most on the other heads of its token
+  (they share B and Q and one head group), never on the wave, list position or chunk it lands
+  in, so permuting the tokens permutes u and all nine gradients bit for bit -- an indexing slip,
+  a race or a read of another token's data breaks it;
 * the scaling h0 -> 2 h0: u is linear in h0 and every gradient but grad_h0 is a product of one
   primal factor (scaled by 2) and one adjoint factor (independent of h0), while grad_h0 =
   A_0 lambda~_1 is purely adjoint.  Scaling by a power of two is exact in floating point except
