@@ -105,3 +105,100 @@ def test_full_size_h0_scaling(full):
         else:
             d = np.abs(res[k].astype(np.float64) - ref).max()
             assert d <= 1e-6 * np.abs(ref).max(), (k, d)
+
+
+# ---- configs 3 and 4 at full size through the factored entry points ---------------------------
+# Materialised, Q_f alone would be 137 GB at either config, so these run on the layer's low-rank
+# factors (hip_lqr_solve_factored), formed on the device by a seeded random-init TTCLayer's
+# front-end from the config's full x, as bench.py's full-size entries do.  The basis gradients
+# are sums over every token, so the sample checks the per-token outputs; the permutation and
+# scaling checks cover all eleven gradients.
+NAMES11 = ["A_diag", "coeff_B", "coeff_Q", "R_inv", "coeff_Qf", "lgA", "lgB", "lgQ", "h0", "B_basis", "Q_basis"]
+PER_TOKEN = NAMES11[:9]
+
+
+def _factored_full(cfg, seed):
+    from ttc import TTCLayer
+    c = CONFIGS[cfg]
+    dev = torch.device("cuda:0")
+    torch.manual_seed(seed)
+    layer = TTCLayer(c["in_dim"], c["out_dim"], c["h_dim"], c["num_heads"], c["b_rank"], c["q_rank"],
+                     solver_impl="hip").to(dev)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = (torch.randn(c["x_shape"], generator=g, device=dev) * c["scale"]).to(c["dtype"]).float()
+    with torch.no_grad():
+        ins = [t.detach().float().contiguous() for t in layer.factored_inputs(x)]
+    del layer, x
+    return ins
+
+
+def _run_factored(ins, dU, T):
+    """u and the eleven gradients, left on the device."""
+    from ttc.solvers.hip_lqr import hip_lqr_solve_factored, last_backward_stats
+    xs = [t.detach().requires_grad_(True) for t in ins]  # no copies: the inputs are tens of GB
+    u = hip_lqr_solve_factored(*xs, T, grad_limit=float("inf"))
+    (u * dU).sum().backward()
+    out = {"u": u.detach()}
+    for n, t in zip(NAMES11, xs):
+        out[n] = t.grad.detach()
+    out["_fallback"] = last_backward_stats["fallback"]
+    del xs, u
+    torch.cuda.empty_cache()
+    return out
+
+
+@pytest.fixture(scope="module", params=[3, 4], ids=lambda c: f"cfg{c}")
+def full_factored(request):
+    cfg = request.param
+    T = CONFIGS[cfg]["T"]
+    ins = _factored_full(cfg, seed=20 + cfg)
+    N, H, d = ins[0].shape
+    dU = torch.randn(N, H, d, generator=torch.Generator(device=ins[0].device).manual_seed(13), device=ins[0].device)
+    print(f"[cfg{cfg} full, factored] N={N} H={H} d={d} T={T}: solving", flush=True)
+    out = _run_factored(ins, dU, T)
+    print(f"   fallback {out['_fallback']}/{N * H}", flush=True)
+    yield cfg, T, ins, dU, out
+    del ins, dU, out
+    torch.cuda.empty_cache()
+
+
+def test_full_size_factored_sample_against_oracle(full_factored):
+    from test_factored import oracle_factored
+    cfg, T, ins, dU, out = full_factored
+    N = ins[0].shape[0]
+    idx = np.sort(np.random.default_rng(7).choice(N, size=2, replace=False))
+    sel = torch.as_tensor(idx, device=ins[0].device)
+    per_tok = [ins[k][sel].cpu() for k in range(9)] + [ins[9].cpu(), ins[10].cpu()]
+    ref = oracle_factored(per_tok, T, dU[sel].double().cpu().numpy())
+    errs = {}
+    for k in ["u"] + PER_TOKEN:
+        x = out[k][sel].double().cpu().numpy()
+        r = np.asarray(ref[k], dtype=np.float64)
+        errs[k] = float(np.abs(x - r).max() / max(np.abs(r).max(), 1e-30))
+    print("   " + " ".join(f"{k}:{v:.1e}" for k, v in errs.items()), flush=True)
+    bad = {k: v for k, v in errs.items() if not (v <= TOL)}
+    assert not bad, f"rel err above {TOL}: {bad}"
+
+
+def test_full_size_factored_token_permutation(full_factored):
+    cfg, T, ins, dU, out = full_factored
+    N = ins[0].shape[0]
+    perm = torch.randperm(N, generator=torch.Generator(device=ins[0].device).manual_seed(19), device=ins[0].device)
+    res = _run_factored([t[perm] for t in ins[:9]] + ins[9:], dU[perm], T)
+    assert res["_fallback"] == out["_fallback"]
+    for k in ["u"] + PER_TOKEN:
+        assert torch.equal(res[k], out[k][perm]), k
+    for k in NAMES11[9:]:  # sums over the tokens: the order of the terms changed
+        d = (res[k] - out[k]).abs().max().item()
+        assert d <= 1e-5 * out[k].abs().max().item(), (k, d)
+    del res
+    torch.cuda.empty_cache()
+
+
+def test_full_size_factored_h0_scaling(full_factored):
+    cfg, T, ins, dU, out = full_factored
+    res = _run_factored(ins[:8] + [2.0 * ins[8]] + ins[9:], dU, T)
+    assert res["_fallback"] == out["_fallback"]
+    for k in ["u"] + NAMES11:
+        ref = out[k] if k == "h0" else 2.0 * out[k]
+        assert torch.equal(res[k], ref), k
