@@ -1,7 +1,9 @@
-"""Configs 2 and 5b at their full size on the GPU, forward and backward through the autograd
+"""Configs 2, 5 and 5b at their full size on the GPU, forward and backward through the autograd
 Function: config 2, x [16, 2048, 8, 32] -> 262,144 tokens x 8 heads = 2,097,152 problems at
-T = 64; config 5b, x [4, 1024, 8, 32] -> 32,768 tokens x 8 heads = 262,144 problems at T = 1024
-(the fp32 sweep, its fp64 rescue, the three rollout tiers and the fp64 stable path).
+T = 64; configs 5 and 5b, x [256, 1, 8, 32] and [4, 1024, 8, 32] -> 2,048 and 32,768 tokens x 8
+heads = 16,384 and 262,144 problems at T = 1024 (the fp32 sweep, its fp64 rescue, the three
+rollout tiers and the fp64 stable path; config 5's short lists run one problem per wave, config
+5b's four).  Configs 3 and 4 follow below on the factored entry points.
 
 At these sizes the fp64 oracle runs only on a sample, so the whole-size run is checked by
 * parity on a seeded sample of tokens against the fp64 oracle, at the 1e-4 bar of the other
@@ -15,7 +17,7 @@ At these sizes the fp64 oracle runs only on a sample, so the whole-size run is c
   A_0 lambda~_1 is purely adjoint.  Scaling by a power of two is exact in floating point except
   where a value or an intermediate product falls below the smallest normal number, so u and
   those eight gradients double and grad_h0 stays: bit for bit at config 2, and to 1e-6 of each
-  tensor's largest entry at config 5b, whose tiniest entries (|x| < 1e-32) are subnormal in
+  tensor's largest entry at configs 5 and 5b, whose tiniest entries (|x| < 1e-32) are subnormal in
   fp32 or come from products that are.
 """
 import numpy as np
@@ -30,7 +32,7 @@ pytestmark = pytest.mark.gpu
 NAMES = ["A_diag", "B", "Q", "R_inv", "Q_f", "lgA", "lgB", "lgQ", "h0"]
 TOL = 1e-4
 # config: (x seed, problems, sampled tokens)
-CASES = {2: (3, 2_097_152, 64), "5b": (4, 262_144, 8)}
+CASES = {2: (3, 2_097_152, 64), 5: (6, 16_384, 8), "5b": (4, 262_144, 8)}
 
 
 def _run(ins, dU, T):
