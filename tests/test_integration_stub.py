@@ -1,6 +1,6 @@
-"""The reference-side ctypes binding that INTEGRATION.md gives a maintainer
+"""The reference-side ctypes binding that the repository's integration guide gives a maintainer
 (``ttc/solvers/hip_lqr_binding.py`` plus its ``LQR_SOLVER_IMPL_MAP["hip"]`` entry), executed
-from the code block of INTEGRATION.md itself, so that the documented binding is the tested one.
+from the guide's own code block, so that the documented binding is the tested one.
 
 CPU: the block binds every symbol it names and picks the flags of the precision policy.
 GPU: the registered solver against the fp64 oracle (u and all nine gradients within 1e-4) on a
@@ -20,15 +20,16 @@ from oracle.inputs import layer_solver_inputs, make_x
 from oracle.lqr64 import LQRProblem, solve_grads
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GUIDE = os.path.join(ROOT, "INTEGRATION.md")
 NAMES = ["A_diag", "B", "Q", "R_inv", "Q_f", "lgA", "lgB", "lgQ", "h0"]
 GUARDED = ["A_diag", "B", "Q", "R_inv", "Q_f", "h0"]
 
 
 def _stub_source():
-    with open(os.path.join(ROOT, "INTEGRATION.md")) as f:
+    with open(GUIDE) as f:
         text = f.read()
     m = re.search(r"```python\n(# ttc/solvers/hip_lqr_binding\.py\n.*?)```", text, re.S)
-    assert m, "INTEGRATION.md has no ttc/solvers/hip_lqr_binding.py block"
+    assert m, f"{GUIDE} has no ttc/solvers/hip_lqr_binding.py block"
     return m.group(1)
 
 
@@ -36,7 +37,7 @@ def _load_stub(monkeypatch):
     from ttc.solvers._lib import lib_path
     monkeypatch.setenv("TTC_LQR_LIB", lib_path())
     ns = {"LQR_SOLVER_IMPL_MAP": {}}
-    exec(compile(_stub_source(), "INTEGRATION.md (hip_lqr_binding.py)", "exec"), ns)
+    exec(compile(_stub_source(), "hip_lqr_binding.py", "exec"), ns)
     return ns
 
 
