@@ -565,6 +565,7 @@ __global__ __launch_bounds__(64) void lqr_fwd64_mfma_kernel(
         // (Qux = W'A), X = Quu^{-1} Qux, then N <- A (N A + W X) - Qc.  Every group solves its
         // problem's rows (the tiles of the others were read above); only these problems keep
         // the result.
+        wave_sync();  // the solve rewrites T0, which the Cholesky path above read
         {
           double aug[32];
           double qrow[16];
